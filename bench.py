@@ -1,0 +1,231 @@
+#!/usr/bin/env python
+"""Benchmark of the compressed-KV decode path on one MI355X.
+
+Headline (BASELINE.json metric): decode-attention HBM GB/s over the packed
+INT4 + QJL cache at 8K context — config C3: 32 sequences x 8192 cached
+tokens, 32 q heads / 8 kv heads, head_dim 128, one bf16 query per
+sequence, QJL on, query rotation (sign-flipped WHT) applied in-kernel.
+A step is one attention call over the whole batch; `value` is algorithmic
+bytes per call (140 B per cached (token, kv head) + q + out) / wall time per
+call with inputs resident in HBM.
+
+Also reported (extra keys): C2 serving (B=64, S=50, 32q/8kv, 256-adapter
+rank-8 LoRA gather on Q) p50/p99 latency and users/s; C4 encode GB/s
+(16 x 4096 x 8 kv heads, K and V, fused rotation); the reference's CPU path
+(the oracle restatement) timed on a bounded C3 sample on this host.
+
+    python bench.py [--gpus 1] [--steps 50] [--warmup 5]
+Prints one JSON line on stdout; progress goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "omnistack-rs_amd"), ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+BYTES_PER_TOKEN_HEAD = 64 + 8 + 4 + 64     # K nibbles + K signs + K norm (f32) + V nibbles
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def make_cache(B, Hkv, S, D, dev, seed, uid, cb, sign):
+    """bf16 N(0,1) K/V with 2% outlier channels x8, encoded on the GPU by the
+    fused rotate + encode kernel."""
+    import torch
+    from omnistack_rs.kernels.quantize import encode_kv
+    g = torch.Generator(device=dev).manual_seed(seed)
+    ch = torch.randperm(D, generator=torch.Generator().manual_seed(seed))[: max(1, round(0.02 * D))].to(dev)
+    out = []
+    for _ in range(2):
+        x = torch.randn(B, Hkv, S, D, generator=g, device=dev, dtype=torch.float32)
+        x[..., ch] *= 8.0
+        out.append(encode_kv(x.to(torch.bfloat16), cb, user_id=uid, sign_flip=sign))
+        del x
+    (kn, kq, kr), (vn, _, _) = out
+    return kn, kq, kr, vn
+
+
+def timed(fn, steps, warmup, stream):
+    """Wall time over `steps` back-to-back calls (synchronized both sides) and
+    per-call HIP event durations on the launch stream."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for s, e in evs:
+        s.record(stream)
+        fn()
+        e.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = [s.elapsed_time(e) * 1e-3 for s, e in evs]
+    return wall, per
+
+
+def cpu_baseline_c3(kn, kq, kr, vn, cb, q, sign, uid, budget_s):
+    """The reference's CPU path (rotate_queries + _fused_attn_python, restated
+    in oracle/) on whole sequences of the C3 batch until `budget_s` elapses."""
+    import torch
+    from oracle import restate
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    cbc, sc = cb.cpu(), sign.cpu()
+    B, Hkv, S, _ = kn.shape
+    done, t_total = 0, 0.0
+    for b in range(B):
+        sl = slice(b, b + 1)
+        args = [t[sl].cpu() for t in (kn, kq, kr, vn)]
+        qb = q[sl].cpu()
+        t0 = time.perf_counter()
+        qr = restate.rotate(qb, sc)
+        restate.fused_attn_python(qr, *args, cbc, uid, 1 / math.sqrt(128), True)
+        t_total += time.perf_counter() - t0
+        done += 1
+        if t_total >= budget_s:
+            break
+    return done, t_total
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-budget-s", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extras", action="store_true")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (this build shards nothing across GPUs); "
+              f"got --gpus {args.gpus}, WORLD_SIZE={world}. Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+    from omnistack_rs import _lib
+    from omnistack_rs.kernels.fused_attention import PackedKVAttention, _apply_lora_to_q
+    from omnistack_rs.kernels.quantize import encode_kv
+    from omnistack_rs.quantization import calibrate_codebook
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream(dev)
+    props = torch.cuda.get_device_properties(dev)
+    log(f"[bench] device {props.name} CUs={props.multi_processor_count}")
+
+    uid, D = 42, 128
+    sign = (torch.randint(0, 2, (D,), generator=torch.Generator().manual_seed(7)) * 2 - 1).to(torch.int8).to(dev)
+    cb1 = calibrate_codebook(torch.randn(1 << 16, generator=torch.Generator().manual_seed(11)), max_iters=100)
+
+    # ── C3: decode at 8K context ─────────────────────────────────────────
+    B, Hq, Hkv, S = 32, 32, 8, 8192
+    cb = cb1.reshape(1, 16).repeat(Hkv, 1).to(dev)
+    log("[bench] C3: encoding 32 x 8 x 8192 K/V")
+    kn, kq, kr, vn = make_cache(B, Hkv, S, D, dev, 42, uid, cb, sign)
+    q = torch.randn(B, Hq, 1, D, generator=torch.Generator(device=dev).manual_seed(43), device=dev).to(torch.bfloat16)
+    att = PackedKVAttention(kn, kq, kr, vn, cb, n_heads=Hq, user_id=uid, rotate_q=True, sign_flip=sign)
+    bytes_step = B * Hkv * S * BYTES_PER_TOKEN_HEAD + q.numel() * 2 + B * Hq * D * 4 + Hkv * 16 * 4 + Hkv * 64 * 16
+    log(f"[bench] C3: timing {args.steps} steps (warmup {args.warmup}); split-K workspace {att.ws_bytes} B")
+    wall, per = timed(lambda: att.run(q), args.steps, args.warmup, stream)
+    t_step = wall / args.steps
+    value = bytes_step / t_step / 1e9
+    ev_mean = statistics.fmean(per)
+    achieved = bytes_step / ev_mean / 1e9
+    log(f"[bench] C3: {t_step * 1e6:.1f} us/step wall, {ev_mean * 1e6:.1f} us/call events -> "
+        f"{value:.0f} GB/s ({value / HBM_PEAK_GBS:.1%} of peak)")
+
+    result = {
+        "metric": "compressed-KV decode attn HBM GB/s (% peak) @8K ctx; users/sec @B=64,L=50",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(t_step * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "C3 decode: 32 seq x 8192 cached tokens, 32 q / 8 kv heads, head_dim 128, "
+                               "INT4 Lloyd-Max + 1-bit QJL K, INT4 V, bf16 query, rotate_q in-kernel",
+                   "bytes_per_step": bytes_step, "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "omni::attn_kernel<128> (+ attn_combine_kernel<128> for split-K)",
+                     "avg_call_us_events": round(ev_mean * 1e6, 2)},
+    }
+
+    # ── extras: C2 serving and C4 encode ─────────────────────────────────
+    if not args.no_extras:
+        B2, S2, L2, R2, HID = 64, 50, 256, 8, 128
+        log("[bench] C2: serving B=64 S=50 with 256 x rank-8 LoRA")
+        kn2, kq2, kr2, vn2 = make_cache(B2, Hkv, S2, D, dev, 52, uid, cb, sign)
+        g2 = torch.Generator(device=dev).manual_seed(44)
+        la = (torch.randn(L2, R2, HID, generator=g2, device=dev) * 0.02).to(torch.bfloat16)
+        lb = (torch.randn(L2, Hq * D, R2, generator=g2, device=dev) * 0.02).to(torch.bfloat16)
+        ids = torch.randint(0, L2, (B2,), generator=torch.Generator().manual_seed(45), dtype=torch.int32).to(dev)
+        xh = torch.randn(B2, 1, HID, generator=g2, device=dev).to(torch.bfloat16)
+        q2 = torch.randn(B2, Hq, 1, D, generator=g2, device=dev).to(torch.bfloat16)
+        att2 = PackedKVAttention(kn2, kq2, kr2, vn2, cb, n_heads=Hq, user_id=uid, rotate_q=True, sign_flip=sign)
+        serve = lambda: att2.run(_apply_lora_to_q(q2, xh, la, lb, ids, 1.0, validate=False))
+        steps2 = max(args.steps, 100)
+        wall2, per2 = timed(serve, steps2, args.warmup, stream)
+        per2s = sorted(per2)
+        p50, p99 = per2s[len(per2s) // 2], per2s[min(len(per2s) - 1, int(0.99 * len(per2s)))]
+        result["serving_c2"] = {"p50_us": round(p50 * 1e6, 2), "p99_us": round(p99 * 1e6, 2),
+                                "users_per_s_gpu": round(B2 / statistics.fmean(per2), 1),
+                                "users_per_s_wall": round(B2 * steps2 / wall2, 1),
+                                "note": "per-call GPU latency from HIP events (LoRA kernel + attention)"}
+        log(f"[bench] C2: p50 {p50 * 1e6:.1f} us p99 {p99 * 1e6:.1f} us, "
+            f"{B2 / statistics.fmean(per2):.0f} users/s (GPU), {B2 * steps2 / wall2:.0f} users/s (wall)")
+
+        B4, T4 = 16, 4096
+        log("[bench] C4: encode 16 x 4096 x 8 K and V")
+        g4 = torch.Generator(device=dev).manual_seed(46)
+        k4 = torch.randn(B4, Hkv, T4, D, generator=g4, device=dev).to(torch.bfloat16)
+        v4 = torch.randn(B4, Hkv, T4, D, generator=g4, device=dev).to(torch.bfloat16)
+        enc = lambda: (encode_kv(k4, cb, user_id=uid, sign_flip=sign), encode_kv(v4, cb, user_id=uid, sign_flip=sign))
+        wall4, per4 = timed(enc, max(5, args.steps // 5), 2, stream)
+        rows = 2 * B4 * Hkv * T4
+        bytes4 = rows * (D * 2 + 64 + 8 + 4)
+        t4 = wall4 / max(5, args.steps // 5)
+        result["encode_c4"] = {"GB_s": round(bytes4 / t4 / 1e9, 1), "us_per_call": round(t4 * 1e6, 1),
+                               "bytes": bytes4, "pct_of_hbm_peak": round(100 * bytes4 / t4 / 1e9 / HBM_PEAK_GBS, 2)}
+        log(f"[bench] C4: {t4 * 1e6:.0f} us -> {bytes4 / t4 / 1e9:.0f} GB/s")
+
+    # ── CPU baseline (reference CPU path restated in oracle/) ────────────
+    if not args.no_cpu:
+        log(f"[bench] CPU baseline: oracle on C3 sequences, ~{args.cpu_budget_s:.0f} s budget")
+        n_seq, t_cpu = cpu_baseline_c3(kn, kq, kr, vn, cb, q, sign, uid, args.cpu_budget_s)
+        b_seq = Hkv * S * BYTES_PER_TOKEN_HEAD + Hq * D * 2 + Hq * D * 4
+        cores = len(os.sched_getaffinity(0))
+        result["cpu_baseline"] = {"value": round(b_seq * n_seq / t_cpu / 1e9, 4), "unit": "GB/s",
+                                  "cores": cores, "kind": "port",
+                                  "sample": f"{n_seq} of 32 C3 sequences (8 kv heads x 8192 tokens each): "
+                                            f"rotate_queries + dequantize_heads + reference_attn, fp32 torch, "
+                                            f"{t_cpu:.2f} s",
+                                  "cpu": platform.processor() or platform.machine()}
+        log(f"[bench] CPU: {n_seq} seq in {t_cpu:.2f} s")
+
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

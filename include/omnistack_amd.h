@@ -1,0 +1,151 @@
+/*
+ * omnistack_amd.h — C ABI of the MI355X (gfx950) KV-cache codec and
+ * compressed-KV attention library (libomnistack_amd.so).
+ *
+ * Plain pointers and sizes only: every tensor argument is a device pointer
+ * to a contiguous, row-major buffer that the caller allocated; `stream` is a
+ * hipStream_t passed as void*.  No entry point synchronizes the host; all
+ * device work is enqueued on `stream`.  Return value: OMNI_OK (0) or a
+ * negative OMNI_E* code; omni_last_error() returns a message for the
+ * calling thread.  The Python wrapper maps OMNI_EINVAL -> ValueError,
+ * OMNI_EINDEX -> IndexError, everything else -> RuntimeError.
+ *
+ * Layouts are the reference's (deepsheth3/Omnistack-RS, Python/torch):
+ *   rotated K/V         (B, H, T, D)        f32 | f16 | bf16
+ *   nibbles             (B, H, T, D/2)      u8   byte m = c[2m] | c[2m+1] << 4
+ *   qjl signs           (B, H, T, D/16)     u8   bit b of byte m = [P_{8m+b} >= 0]
+ *   norms               (B, H, T)           f32  ||x - cb[code]||_2
+ *   codebooks           (H, 16) or (16,)    f32
+ *   QJL G bits          (H, D/2, D/32)      u32  bit j%32 of word j/32 of row i
+ *                                                = [G_h[i][j] == +1]
+ * D is 128 (the reference's only head_dim) or 32 (generalized codec:
+ * QJL_DIM = D/2, alpha = sqrt(2/pi) * ||e|| / D).
+ */
+#ifndef OMNISTACK_AMD_H
+#define OMNISTACK_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum omni_dtype { OMNI_F32 = 0, OMNI_F16 = 1, OMNI_BF16 = 2 };
+
+enum omni_status {
+    OMNI_OK = 0,
+    OMNI_EINVAL = -1,     /* bad shape / argument   -> ValueError   */
+    OMNI_EINDEX = -2,     /* index out of range     -> IndexError   */
+    OMNI_ERUNTIME = -3,   /* HIP launch / runtime   -> RuntimeError */
+    OMNI_EWORKSPACE = -4  /* workspace too small    -> RuntimeError */
+};
+
+/* Message for the last non-OK return on the calling thread. */
+const char *omni_last_error(void);
+
+/* Library ABI version (bumped on any signature change). */
+int omni_abi_version(void);
+
+/*
+ * Host routine (no GPU).  QJL Rademacher matrix for one (user, head) seed,
+ * seed = (user_id % 1024) ^ head: row i, column j is +1 iff the low bit of
+ * the (D*i + j)-th output of std::mt19937(seed) is 1.  Writes
+ * (D/2) * (D/32) words to `out_words`.
+ * Replaces the G draw inside _batch_qjl_encode / _batch_qjl_reconstruct
+ * (omnistack_rs/kernels/quantize.py:410-414, :443-447) and
+ * RademacherQJL._make_G (omnistack_rs/quantization/qjl.py:59-76).
+ */
+int omni_qjl_g_bits(uint32_t seed, int head_dim, uint32_t *out_words);
+
+/*
+ * Normalized Walsh-Hadamard rotation of `rows` vectors of length head_dim:
+ * out = dtype(fp32 WHT(sign_flip * x) * fp32(1/sqrt(D))), butterflies in the
+ * reference order h = 1, 2, ..., D/2.  sign_flip (length D, +-1) may be NULL.
+ * out may alias x.
+ * Replaces _wht_torch / _wht_rotate / rotate_queries / rotate_kv_cache
+ * (omnistack_rs/kernels/hadamard.py:51-85, :155-191, :196-234).
+ */
+int omni_wht_rotate(const void *x, int dtype, int64_t rows, int head_dim,
+                    const int8_t *sign_flip, void *out, void *stream);
+
+/*
+ * Fused KV encoder.  For each row of x (B, H, T, D):
+ *   if rotate:  x <- dtype(WHT(sign_flip * x))        (as omni_wht_rotate)
+ *   code_d  = argmin_k fp32|x_d - cb_h[k]|  (first index on ties, NaN wins)
+ *   e       = x - cb_h[code]   (fp32),   norm = ||e||_2 (fp64 sum, rounded)
+ *   bit_i   = [sum_j G_h[i][j] e_j >= 0] (exact sign), packed LSB-first
+ * codebooks: (H,16) when per_head_codebook, else (16,).
+ * g_bits: (H, D/2, D/32) words for seeds (user_id % 1024) ^ h.
+ * Replaces quantize_heads (omnistack_rs/kernels/quantize.py:542-590) and,
+ * with rotate=1, the bake's _wht_torch + quantize_heads
+ * (scripts/run_criteo_benchmark.py:355, :367).
+ */
+int omni_encode(const void *x, int x_dtype, int64_t B, int H, int64_t T, int head_dim,
+                int rotate, const int8_t *sign_flip,
+                const float *codebooks, int per_head_codebook,
+                const uint32_t *g_bits,
+                uint8_t *nibbles, uint8_t *qjl, float *norms, void *stream);
+
+/*
+ * Dequantize packed rows to f32 (B, H, T, D):
+ *   out = cb_h[code] + (b+- . G_h) * fp32(norm * fp32(sqrt(2/pi)/D))   (with_qjl)
+ *   out = cb_h[code]                                                   (otherwise)
+ * b+- . G_h is an integer sum (computed exactly by popcount), so the result
+ * is bit-identical to the reference's fp32 path.  qjl / norms / g_bits may
+ * be NULL when with_qjl == 0.
+ * Replaces dequantize_heads (omnistack_rs/kernels/quantize.py:593-640).
+ */
+int omni_dequantize(const uint8_t *nibbles, const uint8_t *qjl, const float *norms,
+                    const float *codebooks, int per_head_codebook,
+                    const uint32_t *g_bits, int64_t B, int H, int64_t T, int head_dim,
+                    int with_qjl, float *out, void *stream);
+
+/*
+ * Per-user LoRA on queries, branchless gather-apply:
+ *   q_out[b] = dtype(q[b] + reshape(((x[b] A[id]^T) B[id]^T) * alpha))  if id = idx[b] >= 0
+ *   q_out[b] = q[b]                                                      if id < 0
+ * (a select, never a multiply-by-zero).  Shapes: q (B, Hq, T, D), x (B, T,
+ * hidden), A (n_loras, rank, hidden), Bw (n_loras, Hq*D, rank), idx (B,)
+ * int32, rank <= 64; x, A, Bw share `w_dtype`; q_out has q_dtype and may
+ * alias q.  An index >= n_loras writes NaN rows (never reads out of bounds);
+ * callers that need the reference's IndexError validate indices on the host.
+ * Replaces _apply_lora_to_q (omnistack_rs/kernels/fused_attention.py:401-430)
+ * and the kernel's LoRA block (:166-191).
+ */
+int omni_lora_apply(const void *q, int q_dtype, const void *x, const void *A, const void *Bw,
+                    int w_dtype, const int32_t *idx, int64_t B, int Hq, int64_t T,
+                    int head_dim, int hidden, int rank, int n_loras, float alpha,
+                    void *q_out, void *stream);
+
+/*
+ * Attention over the packed cache (any T; the decode path is T = 1):
+ *   k_hat = cb[code_k] + alpha_s * (b+- G_h),  v_hat = cb[code_v],
+ *   out[b, hq, t] = softmax_s(scale * q_eff . k_hat_s + mask) . v_hat
+ * with GQA kv head = hq / (Hq / Hkv).  The QJL term is applied as a score
+ * correction alpha_s * sum_i b_i (G_h q)_i.  causal_offset < 0: no mask;
+ * otherwise query t attends keys s <= causal_offset + t.  rotate_q applies
+ * WHT(sign_flip * q) to the query inside the kernel (the K/V cache lives in
+ * rotated space); 0 reproduces omni_attn, which takes q as given.
+ * Output f32 (B, Hq, T, D).  `workspace` must hold
+ * omni_attn_workspace_size(...) bytes (may be 0 -> NULL allowed).
+ * Replaces omni_attn / OmniAttention.forward / _fused_attn_triton /
+ * _fused_attn_python (omnistack_rs/kernels/fused_attention.py:320-396,
+ * :435-466, :471-565).
+ */
+size_t omni_attn_workspace_size(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int head_dim);
+
+int omni_attn(const void *q, int q_dtype,
+              const uint8_t *k_nib, const uint8_t *k_qjl, const float *k_norms,
+              const uint8_t *v_nib, const float *codebooks, int per_head_codebook,
+              const uint32_t *g_bits,
+              int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int head_dim,
+              float scale, int with_qjl, int64_t causal_offset,
+              int rotate_q, const int8_t *sign_flip,
+              float *out, void *workspace, size_t workspace_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OMNISTACK_AMD_H */

@@ -1,0 +1,515 @@
+// Attention over the packed INT4 + QJL cache on gfx950 (decode: T = 1;
+// any T works, rows = query tokens x GQA heads).
+//
+// Reference semantics: _fused_attn_python + reference_attn
+// (omnistack_rs/kernels/fused_attention.py:435-466,
+//  omnistack_rs/attention/reference.py:72-177): K_hat with QJL, V INT4
+// (same per-head codebook), fp32 online softmax, GQA kv = hq / (Hq/Hkv).
+// The QJL term enters as a score correction
+//   q . k_hat = q . cb[code] + alpha_s * sum_i b+-_i (G_h q)_i,
+//   alpha_s = ||e_s|| sqrt(2/pi) / D,
+// with the encoder's per-head G (seed (user % 1024) ^ h).
+//
+// Work decomposition.  One block streams one (batch, kv head, token split)
+// for up to 16 query rows (all GQA heads of the group for one or more query
+// tokens), so every cached byte is read once per group, not once per q head.
+// Each wave takes 16-token tiles round-robin and runs three MFMA chains
+// (v_mfma_f32_16x16x16_f16, tokens on M, query rows on N):
+//   S^T  = K_hat16 (16 x D)  . (scale log2e Q)^T        D/16 k-steps
+//   C^T  = B+-     (16 x D/2) . (scale log2e G Q)^T      D/32 k-steps
+//   O^T += V^T_hi (D x 16)   . P^T ; O^T += V^T_lo . P^T  D/16 row blocks
+// K_hat16 is the fp16 codebook value (one LDS lookup per cache byte gives
+// two halves).  V is split hi + lo (two fp16) so the value path keeps ~22
+// bits.  Online softmax in fp32 (exp2 domain) with P rounded to fp16 for
+// the PV product; the softmax denominator sums the same rounded P.
+#include <math.h>
+
+#include "omni_common.h"
+
+namespace omni {
+
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kTile = 16;      // tokens per MFMA tile
+constexpr int kRows = 16;      // query rows per block (MFMA N)
+constexpr int kMaxWaves = 8;
+
+struct AttnArgs {
+    const void *q;
+    const uint8_t *k_nib;
+    const uint8_t *k_qjl;
+    const float *k_norms;
+    const uint8_t *v_nib;
+    const float *codebooks;
+    const uint32_t *g_bits;
+    const int8_t *sign_flip;
+    float *out;
+    float *ws;                 // split partials: [unit][split][row][D + 2]
+    int64_t T, S, split_len;
+    int64_t causal_offset;     // < 0: no mask
+    int q_dtype, per_head, Hq, Hkv, G, n_rchunks, splits, ncopy;
+    int with_qjl, rotate_q;
+    float qscale;              // scale * log2(e)
+    float alpha_c;             // fp32 sqrt(2/pi)/D (qscale is already folded into G q)
+    float wht_scale;
+};
+
+__device__ __forceinline__ int64_t imin64(int64_t x, int64_t y) { return x < y ? x : y; }
+
+__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
+    return (uint32_t)f32_to_f16_rne(a) | ((uint32_t)f32_to_f16_rne(b) << 16);
+}
+
+__device__ __forceinline__ half4_t as_half4(uint32_t lo, uint32_t hi) {
+    uint2 t = make_uint2(lo, hi);
+    return __builtin_bit_cast(half4_t, t);
+}
+
+__device__ __forceinline__ float wave_max_xor16_32(float v) {
+    v = fmaxf(v, __shfl_xor(v, 16));
+    v = fmaxf(v, __shfl_xor(v, 32));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum_xor16_32(float v) {
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    return v;
+}
+
+// Dynamic LDS layout (bytes):
+//   klut  256*ncopy u32      K:  byte -> (hi(cb[lo nib]), hi(cb[hi nib]))
+//   vlut  256*ncopy uint2    V:  byte -> (hi pair, lo pair)
+//   qlut  16 uint2           QJL nibble -> four +-1.0 halves
+//   qs    kRows*D f32        query rows (fp32, rotated if requested)
+//   gq    kRows*D/2 f32      G_h q rows
+// The combine phase reuses [0, ...) after the main loop.
+template <int D>
+struct Lds {
+    static constexpr int QD = D / 2;
+    __host__ __device__ static size_t lut_bytes(int ncopy) { return (size_t)256 * ncopy * 12 + 16 * 8; }
+    __host__ __device__ static size_t comb_bytes(int nw) { (void)nw; return (size_t)(2 * kMaxWaves * kRows + kRows * D) * 4; }
+    __host__ __device__ static size_t fixed_bytes() { return (size_t)kRows * (D + QD) * 4; }
+    static size_t total(int ncopy, int nw) {
+        size_t a = lut_bytes(ncopy), c = comb_bytes(nw);
+        return (a > c ? a : c) + fixed_bytes();
+    }
+};
+
+template <int D>
+__global__ __launch_bounds__(64 * kMaxWaves) void attn_kernel(AttnArgs a) {
+    constexpr int QD = D / 2;
+    constexpr int KSTEPS = D / 16;      // QK k-steps (16 d each)
+    constexpr int QSTEPS = QD / 16;     // QJL k-steps (16 signs each) (>= 1)
+    constexpr int VB = D / 32;          // V bytes per lane per token
+    constexpr int NBLK = 2 * VB;        // PV row blocks (16 d each)
+
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    const int ncopy = a.ncopy;
+    uint32_t *klut = reinterpret_cast<uint32_t *>(smem);
+    uint2 *vlut = reinterpret_cast<uint2 *>(smem + (size_t)256 * ncopy * 4);
+    uint2 *qlut = reinterpret_cast<uint2 *>(smem + (size_t)256 * ncopy * 12);
+    const int nw = blockDim.x >> 6;
+    const size_t var_bytes = Lds<D>::lut_bytes(ncopy) > Lds<D>::comb_bytes(nw) ? Lds<D>::lut_bytes(ncopy)
+                                                                                 : Lds<D>::comb_bytes(nw);
+    float *qs = reinterpret_cast<float *>(smem + var_bytes);
+    float *gq = qs + kRows * D;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int split = blockIdx.x;
+    const int hk = blockIdx.y;
+    const int64_t bz = blockIdx.z;
+    const int64_t b = bz / a.n_rchunks;
+    const int rc = (int)(bz % a.n_rchunks);
+    const int64_t nrows_total = a.T * a.G;
+
+    // ── prologue: LUTs ────────────────────────────────────────────────
+    const float *cbp = a.codebooks + (a.per_head ? hk * 16 : 0);
+    for (int s = tid; s < 256 * ncopy; s += blockDim.x) {
+        const int e = s / ncopy;
+        const float c0 = cbp[e & 15], c1 = cbp[e >> 4];
+        const float h0 = f16_to_f32(f32_to_f16_rne(c0)), h1 = f16_to_f32(f32_to_f16_rne(c1));
+        const uint32_t hi = pack_h2(c0, c1);
+        klut[s] = hi;
+        vlut[s] = make_uint2(hi, pack_h2(c0 - h0, c1 - h1));
+    }
+    if (tid < 16) {
+        uint32_t w[2];
+        for (int k = 0; k < 2; ++k) {
+            const uint32_t b0 = (tid >> (2 * k)) & 1u, b1 = (tid >> (2 * k + 1)) & 1u;
+            w[k] = (b0 ? 0x3C00u : 0xBC00u) | ((b1 ? 0x3C00u : 0xBC00u) << 16);
+        }
+        qlut[tid] = make_uint2(w[0], w[1]);
+    }
+
+    // ── prologue: query rows (row r <-> flat (t, gh) = rc*16 + r) ─────
+    for (int s = tid; s < kRows * D; s += blockDim.x) {
+        const int r = s / D, d = s % D;
+        const int64_t rho = (int64_t)rc * kRows + r;
+        float v = 0.0f;
+        if (rho < nrows_total) {
+            const int64_t t = rho / a.G;
+            const int hq = hk * a.G + (int)(rho % a.G);
+            v = load_as_f32(a.q, a.q_dtype, ((b * a.Hq + hq) * a.T + t) * D + d);
+        }
+        qs[s] = v;
+    }
+    __syncthreads();
+    if (a.rotate_q && tid < kRows) {
+        // rotate_queries in-kernel: dtype(WHT(sign_flip * q)), hadamard.py:51-85.
+        float *row = qs + tid * D;
+        if (a.sign_flip)
+            for (int d = 0; d < D; ++d) row[d] = a.sign_flip[d] < 0 ? -row[d] : row[d];
+        for (int h = 1; h < D; h <<= 1)
+            for (int base = 0; base < D; base += 2 * h)
+                for (int i = 0; i < h; ++i) {
+                    const float u = row[base + i], l = row[base + h + i];
+                    row[base + i] = u + l;
+                    row[base + h + i] = u - l;
+                }
+        for (int d = 0; d < D; ++d) row[d] = round_to_dtype(row[d] * a.wht_scale, a.q_dtype);
+    }
+    __syncthreads();
+    if (a.with_qjl) {
+        const uint32_t *gh = a.g_bits + (int64_t)hk * QD * (D / 32);
+        for (int s = tid; s < kRows * QD; s += blockDim.x) {
+            const int r = s / QD, i = s % QD;
+            const float *row = qs + r * D;
+            float acc = 0.0f;
+            for (int j = 0; j < D; ++j) {
+                const float g = ((gh[i * (D / 32) + (j >> 5)] >> (j & 31)) & 1u) ? 1.0f : -1.0f;
+                acc = __builtin_fmaf(g, row[j], acc);
+            }
+            gq[s] = acc;
+        }
+    }
+    __syncthreads();
+
+    // ── per-lane MFMA B operands ──────────────────────────────────────
+    const int r = lane & 15;          // query row (MFMA column)
+    const int g = lane >> 4;          // k-group
+    half4_t qb[KSTEPS];
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) {
+        const float *row = qs + r * D + g * (D / 4) + 4 * s;
+        qb[s] = as_half4(pack_h2(row[0] * a.qscale, row[1] * a.qscale),
+                         pack_h2(row[2] * a.qscale, row[3] * a.qscale));
+    }
+    half4_t gb[QSTEPS];
+#pragma unroll
+    for (int s = 0; s < QSTEPS; ++s) {
+        if (a.with_qjl) {
+            const float *row = gq + r * QD + g * (QD / 4) + 4 * s;
+            gb[s] = as_half4(pack_h2(row[0] * a.qscale, row[1] * a.qscale),
+                             pack_h2(row[2] * a.qscale, row[3] * a.qscale));
+        } else {
+            gb[s] = as_half4(0u, 0u);
+        }
+    }
+
+    // Causal limit for this lane's row.
+    const int64_t rho = (int64_t)rc * kRows + r;
+    const bool row_valid = rho < nrows_total;
+    const int64_t key_limit = (a.causal_offset >= 0 && row_valid) ? a.causal_offset + rho / a.G : INT64_MAX;
+
+    // ── main loop ─────────────────────────────────────────────────────
+    const int64_t s_begin = (int64_t)split * a.split_len;
+    const int64_t s_end = imin64(a.S, s_begin + a.split_len);
+    const int64_t kv_base = (b * a.Hkv + hk) * a.S;   // token row base of this (b, hk)
+    const int cmask = ncopy - 1;
+    const int cl = lane & cmask;
+
+    float4_t o_acc[NBLK];
+#pragma unroll
+    for (int k = 0; k < NBLK; ++k) o_acc[k] = float4_t{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    for (int64_t t0 = s_begin + (int64_t)wave * kTile; t0 < s_end; t0 += (int64_t)nw * kTile) {
+        // A-operand token for K / QJL: t0 + (lane % 16); output tokens: t0 + 4g + i.
+        const int64_t ta = imin64(t0 + r, s_end - 1);
+        const int64_t tok_row = kv_base + ta;
+
+        // K nibbles: D/8 bytes per lane.
+        uint32_t kw[D / 32];
+        if constexpr (D == 128) {
+            uint4 t = reinterpret_cast<const uint4 *>(a.k_nib + tok_row * (D / 2))[g];
+            kw[0] = t.x; kw[1] = t.y; kw[2] = t.z; kw[3] = t.w;
+        } else {
+            kw[0] = reinterpret_cast<const uint32_t *>(a.k_nib + tok_row * (D / 2))[g];
+        }
+
+        float4_t sacc = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s) {
+            const uint32_t w = kw[s >> 1];
+            const uint32_t b0 = (w >> (16 * (s & 1))) & 0xffu;
+            const uint32_t b1 = (w >> (16 * (s & 1) + 8)) & 0xffu;
+            const half4_t av = as_half4(klut[b0 * ncopy + cl], klut[b1 * ncopy + cl]);
+            sacc = __builtin_amdgcn_mfma_f32_16x16x16f16(av, qb[s], sacc, 0, 0, 0);
+        }
+
+        float4_t cacc = float4_t{0.f, 0.f, 0.f, 0.f};
+        float4_t alpha4 = float4_t{0.f, 0.f, 0.f, 0.f};
+        if (a.with_qjl) {
+            uint32_t sb;
+            if constexpr (D == 128) {
+                sb = reinterpret_cast<const uint16_t *>(a.k_qjl + tok_row * (D / 16))[g];
+            } else {
+                sb = (reinterpret_cast<const uint16_t *>(a.k_qjl + tok_row * (D / 16))[0] >> (4 * g)) & 0xfu;
+            }
+#pragma unroll
+            for (int s = 0; s < QSTEPS; ++s) {
+                const uint2 e = qlut[(sb >> (4 * s)) & 0xfu];
+                cacc = __builtin_amdgcn_mfma_f32_16x16x16f16(as_half4(e.x, e.y), gb[s], cacc, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int64_t tn = imin64(t0 + 4 * g + i, s_end - 1);
+                alpha4[i] = a.k_norms[kv_base + tn] * a.alpha_c;
+            }
+        }
+
+        // Scores (log2 units) with masking.
+        float sc[4];
+        float mt = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int64_t tn = t0 + 4 * g + i;
+            float v = __builtin_fmaf(alpha4[i], cacc[i], sacc[i]);
+            if (tn >= s_end || tn > key_limit) v = -INFINITY;
+            sc[i] = v;
+            mt = fmaxf(mt, v);
+        }
+        mt = wave_max_xor16_32(mt);
+        const float m_new = fmaxf(m_run, mt);
+        const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
+        const float resc = exp2f(m_run - m_use);
+        uint32_t ph[2];
+        float psum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint16_t p0 = f32_to_f16_rne(exp2f(sc[2 * i] - m_use));
+            const uint16_t p1 = f32_to_f16_rne(exp2f(sc[2 * i + 1] - m_use));
+            psum += f16_to_f32(p0) + f16_to_f32(p1);
+            ph[i] = (uint32_t)p0 | ((uint32_t)p1 << 16);
+        }
+        l_run = __builtin_fmaf(l_run, resc, psum);
+        m_run = m_new;
+        const half4_t pb = as_half4(ph[0], ph[1]);
+#pragma unroll
+        for (int k = 0; k < NBLK; ++k) o_acc[k] *= resc;
+
+        // V: lane row rr = lane % 16 takes byte group rr of tokens t0 + 4g + i.
+        uint2 vl[4][VB];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int64_t tn = imin64(t0 + 4 * g + i, s_end - 1);
+            const uint8_t *vrow = a.v_nib + (kv_base + tn) * (D / 2);
+            uint32_t w;
+            if constexpr (D == 128) w = reinterpret_cast<const uint32_t *>(vrow)[r];
+            else w = vrow[r];
+#pragma unroll
+            for (int bb = 0; bb < VB; ++bb) vl[i][bb] = vlut[((w >> (8 * bb)) & 0xffu) * ncopy + cl];
+        }
+#pragma unroll
+        for (int bb = 0; bb < VB; ++bb) {
+#pragma unroll
+            for (int n = 0; n < 2; ++n) {
+                const uint32_t sel = n ? 0x07060302u : 0x05040100u;
+                const half4_t ah = as_half4(__builtin_amdgcn_perm(vl[1][bb].x, vl[0][bb].x, sel),
+                                            __builtin_amdgcn_perm(vl[3][bb].x, vl[2][bb].x, sel));
+                const half4_t al = as_half4(__builtin_amdgcn_perm(vl[1][bb].y, vl[0][bb].y, sel),
+                                            __builtin_amdgcn_perm(vl[3][bb].y, vl[2][bb].y, sel));
+                o_acc[2 * bb + n] = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, pb, o_acc[2 * bb + n], 0, 0, 0);
+                o_acc[2 * bb + n] = __builtin_amdgcn_mfma_f32_16x16x16f16(al, pb, o_acc[2 * bb + n], 0, 0, 0);
+            }
+        }
+    }
+
+    // ── combine waves in LDS (deterministic order) ────────────────────
+    l_run = wave_sum_xor16_32(l_run);
+    __syncthreads();   // LUTs are dead from here on
+    float *wm = reinterpret_cast<float *>(smem);           // [nw][kRows] running max
+    float *wl = wm + kMaxWaves * kRows;                     // [nw][kRows] denominators
+    float *ob = wl + kMaxWaves * kRows;                     // [kRows][D] merged O
+    if (g == 0) {
+        wm[wave * kRows + r] = m_run;
+        wl[wave * kRows + r] = l_run;
+    }
+    __syncthreads();
+    float mx = -INFINITY;
+    for (int w = 0; w < nw; ++w) mx = fmaxf(mx, wm[w * kRows + r]);
+    const float mu = (mx == -INFINITY) ? 0.0f : mx;
+    const float fw = exp2f(m_run - mu);
+    // o_acc[blk][i] holds O^T[d][r] with d = (2*VB) * (4g + i) + blk.
+    for (int w = 0; w < nw; ++w) {
+        if (wave == w) {
+#pragma unroll
+            for (int k = 0; k < NBLK; ++k)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float *dst = ob + r * D + (2 * VB) * (4 * g + i) + k;
+                    const float v = o_acc[k][i] * fw;
+                    *dst = (w == 0) ? v : (*dst + v);
+                }
+        }
+        __syncthreads();
+    }
+
+    const int64_t unit = (b * a.Hkv + hk) * a.n_rchunks + rc;
+    for (int s = tid; s < kRows * D; s += blockDim.x) {
+        const int rr = s / D, d = s % D;
+        const int64_t rr_rho = (int64_t)rc * kRows + rr;
+        if (rr_rho >= nrows_total) continue;
+        float rmx = -INFINITY;
+        for (int w = 0; w < nw; ++w) rmx = fmaxf(rmx, wm[w * kRows + rr]);
+        const float rmu = (rmx == -INFINITY) ? 0.0f : rmx;
+        float lsum = 0.0f;
+        for (int w = 0; w < nw; ++w) lsum = __builtin_fmaf(exp2f(wm[w * kRows + rr] - rmu), wl[w * kRows + rr], lsum);
+        const float osum = ob[rr * D + d];
+        if (a.splits == 1) {
+            const int64_t t = rr_rho / a.G;
+            const int hq = hk * a.G + (int)(rr_rho % a.G);
+            a.out[((b * a.Hq + hq) * a.T + t) * D + d] = osum / lsum;
+        } else {
+            float *wp = a.ws + ((unit * a.splits + split) * kRows + rr) * (D + 2);
+            wp[d] = osum;
+            if (d == 0) { wp[D] = rmx; wp[D + 1] = lsum; }
+        }
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
+    const int hk = blockIdx.y;
+    const int64_t bz = blockIdx.z;
+    const int64_t b = bz / a.n_rchunks;
+    const int rc = (int)(bz % a.n_rchunks);
+    const int64_t unit = (b * a.Hkv + hk) * a.n_rchunks + rc;
+    const int64_t nrows_total = a.T * a.G;
+    for (int s = threadIdx.x; s < kRows * D; s += blockDim.x) {
+        const int rr = s / D, d = s % D;
+        const int64_t rho = (int64_t)rc * kRows + rr;
+        if (rho >= nrows_total) continue;
+        float mx = -INFINITY;
+        for (int sp = 0; sp < a.splits; ++sp)
+            mx = fmaxf(mx, a.ws[((unit * a.splits + sp) * kRows + rr) * (D + 2) + D]);
+        const float mu = (mx == -INFINITY) ? 0.0f : mx;
+        float lsum = 0.0f, osum = 0.0f;
+        for (int sp = 0; sp < a.splits; ++sp) {
+            const float *wp = a.ws + ((unit * a.splits + sp) * kRows + rr) * (D + 2);
+            const float f = exp2f(wp[D] - mu);
+            lsum = __builtin_fmaf(f, wp[D + 1], lsum);
+            osum = __builtin_fmaf(f, wp[d], osum);
+        }
+        const int64_t t = rho / a.G;
+        const int hq = hk * a.G + (int)(rho % a.G);
+        a.out[((b * a.Hq + hq) * a.T + t) * D + d] = osum / lsum;
+    }
+}
+
+// ── launch planning ─────────────────────────────────────────────────────
+
+struct Plan {
+    int n_rchunks, splits, nw, ncopy;
+    int64_t split_len;
+    size_t lds, ws_bytes;
+};
+
+static int device_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cached[dev]) {
+        hipDeviceProp_t p;
+        cached[dev] = (hipGetDeviceProperties(&p, dev) == hipSuccess && p.multiProcessorCount > 0)
+                          ? p.multiProcessorCount : 256;
+    }
+    return cached[dev];
+}
+
+static Plan make_plan(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int D) {
+    Plan p;
+    const int G = Hq / Hkv;
+    p.n_rchunks = (int)((T * G + kRows - 1) / kRows);
+    const int64_t units = B * (int64_t)Hkv * p.n_rchunks;
+    const int64_t tiles = (S + kTile - 1) / kTile;
+    const int cus = device_cus();
+    int64_t splits = (2 * (int64_t)cus + units - 1) / (units > 0 ? units : 1);
+    const int64_t max_splits = tiles / (2 * kMaxWaves) > 1 ? tiles / (2 * kMaxWaves) : 1;
+    if (splits > max_splits) splits = max_splits;
+    if (splits < 1) splits = 1;
+    const int64_t tiles_per_split = (tiles + splits - 1) / splits;
+    p.splits = (int)splits;
+    p.split_len = tiles_per_split * kTile;
+    int nw = (int)((tiles_per_split + 1) / 2);
+    p.nw = nw < 1 ? 1 : (nw > kMaxWaves ? kMaxWaves : nw);
+    p.ncopy = tiles_per_split >= 64 ? 16 : (tiles_per_split >= 8 ? 4 : 1);
+    p.lds = D == 128 ? Lds<128>::total(p.ncopy, p.nw) : Lds<32>::total(p.ncopy, p.nw);
+    p.ws_bytes = p.splits > 1 ? (size_t)units * p.splits * kRows * (D + 2) * sizeof(float) : 0;
+    return p;
+}
+
+}  // namespace omni
+
+using namespace omni;
+
+extern "C" size_t omni_attn_workspace_size(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int head_dim) {
+    if (B <= 0 || Hq <= 0 || Hkv <= 0 || T <= 0 || S <= 0 || Hq % Hkv || !head_dim_ok(head_dim)) return 0;
+    return make_plan(B, Hq, Hkv, T, S, head_dim).ws_bytes;
+}
+
+extern "C" int omni_attn(const void *q, int q_dtype, const uint8_t *k_nib, const uint8_t *k_qjl,
+                         const float *k_norms, const uint8_t *v_nib, const float *codebooks,
+                         int per_head_codebook, const uint32_t *g_bits, int64_t B, int Hq, int Hkv,
+                         int64_t T, int64_t S, int head_dim, float scale, int with_qjl,
+                         int64_t causal_offset, int rotate_q, const int8_t *sign_flip, float *out,
+                         void *workspace, size_t workspace_bytes, void *stream) {
+    OMNI_CHECK_ARG(dtype_ok(q_dtype), "omni_attn: bad q dtype %d", q_dtype);
+    OMNI_CHECK_ARG(head_dim_ok(head_dim), "omni_attn: head_dim must be 128 or 32, got %d", head_dim);
+    OMNI_CHECK_ARG(B >= 0 && Hq > 0 && Hkv > 0 && T >= 0 && S >= 0, "omni_attn: bad shape");
+    OMNI_CHECK_ARG(Hq % Hkv == 0, "omni_attn: n_heads (%d) must be divisible by n_kv_heads (%d)", Hq, Hkv);
+    if (B == 0 || T == 0) return OMNI_OK;
+    OMNI_CHECK_ARG(S > 0, "omni_attn: empty KV cache (S = 0) has no softmax");
+    OMNI_CHECK_ARG(q && k_nib && v_nib && codebooks && out, "omni_attn: NULL pointer");
+    OMNI_CHECK_ARG(!with_qjl || (k_qjl && k_norms && g_bits), "omni_attn: NULL QJL pointer");
+    OMNI_CHECK_ARG(isfinite(scale), "omni_attn: scale must be finite");
+    Plan p = make_plan(B, Hq, Hkv, T, S, head_dim);
+    OMNI_CHECK_ARG(Hkv <= 65535 && B * p.n_rchunks <= 2147483647LL && p.splits <= 2147483647,
+                   "omni_attn: grid too large");
+    if (p.ws_bytes > 0 && (workspace == nullptr || workspace_bytes < p.ws_bytes)) {
+        set_error("omni_attn: workspace of %zu bytes required, %zu given", p.ws_bytes, workspace_bytes);
+        return OMNI_EWORKSPACE;
+    }
+    AttnArgs a;
+    a.q = q; a.k_nib = k_nib; a.k_qjl = k_qjl; a.k_norms = k_norms; a.v_nib = v_nib;
+    a.codebooks = codebooks; a.g_bits = g_bits; a.sign_flip = sign_flip; a.out = out;
+    a.ws = reinterpret_cast<float *>(workspace);
+    a.T = T; a.S = S; a.split_len = p.split_len; a.causal_offset = causal_offset;
+    a.q_dtype = q_dtype; a.per_head = per_head_codebook; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv;
+    a.n_rchunks = p.n_rchunks; a.splits = p.splits; a.ncopy = p.ncopy;
+    a.with_qjl = with_qjl; a.rotate_q = rotate_q;
+    const double log2e = 1.4426950408889634;
+    a.qscale = (float)((double)scale * log2e);
+    a.alpha_c = (float)(sqrt(2.0 / M_PI) / (double)head_dim);
+    a.wht_scale = inv_sqrt_dim_f32(head_dim);
+    dim3 grid((unsigned)p.splits, (unsigned)Hkv, (unsigned)(B * p.n_rchunks));
+    dim3 block(64 * p.nw);
+    if (head_dim == 128)
+        hipLaunchKernelGGL(attn_kernel<128>, grid, block, p.lds, as_stream(stream), a);
+    else
+        hipLaunchKernelGGL(attn_kernel<32>, grid, block, p.lds, as_stream(stream), a);
+    OMNI_CHECK_LAUNCH("omni_attn");
+    if (p.splits > 1) {
+        dim3 g2(1, (unsigned)Hkv, (unsigned)(B * p.n_rchunks));
+        if (head_dim == 128)
+            hipLaunchKernelGGL(attn_combine_kernel<128>, g2, dim3(256), 0, as_stream(stream), a);
+        else
+            hipLaunchKernelGGL(attn_combine_kernel<32>, g2, dim3(256), 0, as_stream(stream), a);
+        OMNI_CHECK_LAUNCH("omni_attn combine");
+    }
+    return OMNI_OK;
+}

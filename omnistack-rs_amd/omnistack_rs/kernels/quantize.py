@@ -1,0 +1,207 @@
+"""INT4 Lloyd-Max + 1-bit Rademacher QJL codec on gfx950.
+
+API of the reference module omnistack_rs/kernels/quantize.py: constants
+(:46-49), ``_make_qjl_seed`` (:293-295), the nibble layout helpers
+(:237-288, :372-395), ``quantize_heads`` (:542-590), ``dequantize_heads``
+(:593-640), ``quantize_rows`` / ``dequantize_rows`` (:456-537).
+
+``quantize_heads`` runs ``omni_encode`` (nibbles and QJL sign bytes are
+bit-identical to the reference's CPU encoder; norms are the correctly
+rounded fp32 norm, within 2 ulp of torch's fp32 reduction), and
+``dequantize_heads`` runs ``omni_dequantize`` (bit-identical).  The
+row-seeded ``quantize_rows`` / ``dequantize_rows`` follow the reference's
+torch branch (seed (user_id % 1024) ^ (base + row)), not its Triton/Philox
+branch.
+
+Extension: ``encode_kv`` fuses the rotation (optionally sign-flipped) into
+the encoder, replacing the bake's ``_wht_torch`` + ``quantize_heads``.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from .. import _lib
+from .hadamard import HEAD_DIM
+
+QJL_DIM: int = 64
+_NBYTES_NIBBLE = HEAD_DIM // 2
+_NBYTES_QJL = QJL_DIM // 8
+_WORDS_PER_ROW = HEAD_DIM // 8
+
+
+def _make_qjl_seed(user_id: int, row_seed: int) -> int:
+    """(user_id % 1024) ^ row_seed with Python semantics (quantize.py:293-295)."""
+    return (user_id % 1024) ^ row_seed
+
+
+# ── nibble layout helpers (integer tensor ops, any device) ─────────────
+
+def _pack_nibbles_torch(codes: torch.Tensor) -> torch.Tensor:
+    """(D,) codes -> (D/2,) bytes, byte m = code[2m] | code[2m+1] << 4."""
+    c = codes.to(torch.int32).reshape(-1, 2)
+    return ((c[:, 0] & 0xF) | ((c[:, 1] & 0xF) << 4)).to(torch.uint8)
+
+
+def _unpack_nibbles_torch(packed: torch.Tensor) -> torch.Tensor:
+    """(D/2,) bytes -> (D,) codes (low nibble first)."""
+    p = packed.to(torch.int32)
+    return torch.stack([p & 0xF, (p >> 4) & 0xF], dim=-1).reshape(-1).to(torch.uint8)
+
+
+def _xor_unpack_word_torch(packed: torch.Tensor) -> torch.Tensor:
+    """(D/2,) bytes -> (D,) codes through little-endian 32-bit words."""
+    return _batch_xor_unpack(packed.reshape(1, -1)).reshape(-1)
+
+
+def _batch_pack_nibbles(codes: torch.Tensor) -> torch.Tensor:
+    """(N, D) codes -> (N, D/2) bytes."""
+    c = codes.to(torch.int32)
+    return ((c[:, 0::2] & 0xF) | ((c[:, 1::2] & 0xF) << 4)).to(torch.uint8)
+
+
+def _batch_xor_unpack(nib_flat: torch.Tensor) -> torch.Tensor:
+    """(N, D/2) bytes -> (N, D) codes: word w = bytes 4w..4w+3, nibble k of
+    word w is code 8w + k."""
+    N, nb = nib_flat.shape
+    words = nib_flat.contiguous().view(torch.int32) if nib_flat.is_contiguous() and nb % 4 == 0 else None
+    if words is None:
+        p = nib_flat.to(torch.int32)
+        words = p[:, 0::4] | (p[:, 1::4] << 8) | (p[:, 2::4] << 16) | (p[:, 3::4] << 24)
+    shifts = torch.arange(0, 32, 4, dtype=torch.int32, device=nib_flat.device)
+    return ((words.unsqueeze(2) >> shifts) & 0xF).reshape(N, 2 * nb).to(torch.uint8)
+
+
+# ── head-level codec ────────────────────────────────────────────────────
+
+def _prep_codebooks(codebooks: torch.Tensor, n_heads: int, device) -> tuple[torch.Tensor, int]:
+    per_head = codebooks.dim() == 2
+    if per_head:
+        if tuple(codebooks.shape) != (n_heads, 16):
+            raise ValueError(f"codebooks must be ({n_heads}, 16) or (16,), got {tuple(codebooks.shape)}")
+    elif tuple(codebooks.shape) != (16,):
+        raise ValueError(f"codebooks must be ({n_heads}, 16) or (16,), got {tuple(codebooks.shape)}")
+    return codebooks.to(device=device, dtype=torch.float32).contiguous(), int(per_head)
+
+
+def _encode(x: torch.Tensor, codebooks: torch.Tensor, user_id: int, rotate: bool,
+            sign_flip: Optional[torch.Tensor]):
+    if x.dim() != 4:
+        raise ValueError(f"x must be (B, n_heads, T, head_dim), got {tuple(x.shape)}")
+    B, H, T, D = x.shape
+    if D not in (128, 32):
+        raise ValueError(f"head_dim must be {HEAD_DIM} (or 32), got {D}")
+    dev = _lib.require_device(x, codebooks if codebooks.is_cuda else None, sign_flip)
+    xc = x if x.dtype in _lib.DTYPE_CODE else x.float()
+    xc = xc.contiguous()
+    cb, per_head = _prep_codebooks(codebooks, H, dev)
+    gb = _lib.g_bits(_lib.head_seeds(user_id, H), D, dev)
+    nib = torch.empty(B, H, T, D // 2, dtype=torch.uint8, device=dev)
+    qjl = torch.empty(B, H, T, D // 16, dtype=torch.uint8, device=dev)
+    nrm = torch.empty(B, H, T, dtype=torch.float32, device=dev)
+    sf = None
+    if sign_flip is not None:
+        sf = torch.where(sign_flip.reshape(-1) < 0, -1, 1).to(torch.int8).contiguous()
+    _lib.check(_lib.lib().omni_encode(
+        _lib.ptr(xc), _lib.dtype_code(xc.dtype), B, H, T, D, int(rotate), _lib.ptr(sf),
+        _lib.ptr(cb), per_head, _lib.ptr(gb), _lib.ptr(nib), _lib.ptr(qjl), _lib.ptr(nrm),
+        _lib.stream_of(dev)))
+    return nib, qjl, nrm
+
+
+def quantize_heads(x: torch.Tensor, codebooks: torch.Tensor, user_id: int = 0):
+    """Per-head INT4 + QJL encode of rotated K/V (quantize.py:542-590).
+
+    x (B, n_heads, T, 128) rotated activations; codebooks (n_heads, 16) or
+    (16,).  Returns (nibbles u8 (B,H,T,64), qjl u8 (B,H,T,8), norms f32 (B,H,T)).
+    """
+    return _encode(x, codebooks, user_id, rotate=False, sign_flip=None)
+
+
+def encode_kv(x: torch.Tensor, codebooks: torch.Tensor, user_id: int = 0,
+              sign_flip: Optional[torch.Tensor] = None):
+    """Fused bake: quantize_heads(rotate(x, sign_flip), codebooks, user_id) in
+    one kernel (the rotated tensor never reaches HBM)."""
+    return _encode(x, codebooks, user_id, rotate=True, sign_flip=sign_flip)
+
+
+def dequantize_heads(nibbles: torch.Tensor, qjl_packed: torch.Tensor, norms: torch.Tensor,
+                     codebooks: torch.Tensor, user_id: int = 0, with_qjl: bool = True) -> torch.Tensor:
+    """(B, n_heads, T, 128) float32 reconstruction (quantize.py:593-640)."""
+    if nibbles.dim() != 4:
+        raise ValueError(f"nibbles must be (B, n_heads, T, D/2), got {tuple(nibbles.shape)}")
+    B, H, T, nb = nibbles.shape
+    D = 2 * nb
+    dev = _lib.require_device(nibbles, qjl_packed if with_qjl else None, norms if with_qjl else None)
+    cb, per_head = _prep_codebooks(codebooks, H, dev)
+    nib = nibbles.contiguous()
+    q = qjl_packed.contiguous() if with_qjl else None
+    n = norms.to(torch.float32).contiguous() if with_qjl else None
+    gb = _lib.g_bits(_lib.head_seeds(user_id, H), D, dev) if with_qjl else None
+    out = torch.empty(B, H, T, D, dtype=torch.float32, device=dev)
+    _lib.check(_lib.lib().omni_dequantize(
+        _lib.ptr(nib), _lib.ptr(q), _lib.ptr(n), _lib.ptr(cb), per_head, _lib.ptr(gb),
+        B, H, T, D, int(with_qjl), _lib.ptr(out), _lib.stream_of(dev)))
+    return out
+
+
+# ── row-level codec (per-row seeds) ─────────────────────────────────────
+
+_ROW_CHUNK = 65535
+
+
+def quantize_rows(x: torch.Tensor, codebook: torch.Tensor, base_head_idx: int = 0, user_id: int = 0):
+    """Row-seeded encode (quantize.py:456-499, torch branch): row i of the
+    flattened input uses seed (user_id % 1024) ^ (base_head_idx + i)."""
+    D = x.shape[-1]
+    if D not in (128, 32):
+        raise ValueError(f"head_dim must be {HEAD_DIM} (or 32), got {D}")
+    dev = _lib.require_device(x)
+    flat = x.reshape(-1, D)
+    N = flat.shape[0]
+    nib = torch.empty(N, D // 2, dtype=torch.uint8, device=dev)
+    qjl = torch.empty(N, D // 16, dtype=torch.uint8, device=dev)
+    nrm = torch.empty(N, dtype=torch.float32, device=dev)
+    cb = codebook.reshape(16)
+    for s in range(0, N, _ROW_CHUNK):
+        e = min(N, s + _ROW_CHUNK)
+        seeds = tuple(_make_qjl_seed(user_id, base_head_idx + i) for i in range(s, e))
+        # One "head" per row: its own G, shared codebook.
+        xs = flat[s:e].reshape(1, e - s, 1, D)
+        xc = xs if xs.dtype in _lib.DTYPE_CODE else xs.float()
+        xc = xc.contiguous()
+        cbd, _ = _prep_codebooks(cb, e - s, dev)
+        gb = _lib.g_bits(seeds, D, dev)
+        _lib.check(_lib.lib().omni_encode(
+            _lib.ptr(xc), _lib.dtype_code(xc.dtype), 1, e - s, 1, D, 0, None, _lib.ptr(cbd), 0,
+            _lib.ptr(gb), _lib.ptr(nib[s:e]), _lib.ptr(qjl[s:e]), _lib.ptr(nrm[s:e]),
+            _lib.stream_of(dev)))
+    batch = x.shape[:-1]
+    return nib.reshape(*batch, D // 2), qjl.reshape(*batch, D // 16), nrm.reshape(*batch)
+
+
+def dequantize_rows(nibbles: torch.Tensor, qjl_packed: torch.Tensor, norms: torch.Tensor,
+                    codebook: torch.Tensor, base_head_idx: int = 0, user_id: int = 0,
+                    with_qjl: bool = True) -> torch.Tensor:
+    """Row-seeded reconstruction (quantize.py:502-537)."""
+    nb = nibbles.shape[-1]
+    D = 2 * nb
+    dev = _lib.require_device(nibbles)
+    nib = nibbles.reshape(-1, nb).contiguous()
+    N = nib.shape[0]
+    q = qjl_packed.reshape(N, D // 16).contiguous()
+    n = norms.reshape(N).to(torch.float32).contiguous()
+    out = torch.empty(N, D, dtype=torch.float32, device=dev)
+    cb = codebook.reshape(16)
+    for s in range(0, N, _ROW_CHUNK):
+        e = min(N, s + _ROW_CHUNK)
+        cbd, _ = _prep_codebooks(cb, e - s, dev)
+        gb = None
+        if with_qjl:
+            seeds = tuple(_make_qjl_seed(user_id, base_head_idx + i) for i in range(s, e))
+            gb = _lib.g_bits(seeds, D, dev)
+        _lib.check(_lib.lib().omni_dequantize(
+            _lib.ptr(nib[s:e]), _lib.ptr(q[s:e]), _lib.ptr(n[s:e]), _lib.ptr(cbd), 0, _lib.ptr(gb),
+            1, e - s, 1, D, int(with_qjl), _lib.ptr(out[s:e]), _lib.stream_of(dev)))
+    return out.reshape(*nibbles.shape[:-1], D)

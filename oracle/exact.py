@@ -1,0 +1,82 @@
+"""fp64 / explicit-loop ground truth that pins oracle.restate (test only).
+
+These restate what the mathematics fixes, independently of torch's fp32
+reduction orders: exact projections for QJL sign bits, correctly rounded
+residual norms, first-index argmin with torch's NaN rule, and brute-force
+softmax attention.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+from . import mt19937
+
+
+def argmin_first(x: np.ndarray, cb: np.ndarray) -> np.ndarray:
+    """Nearest centroid by an explicit loop over k: fp32 |x - c_k|, strictly
+    smaller wins (first index on ties); a NaN distance counts as the minimum
+    (torch.argmin's documented NaN propagation).  x (...,) fp32, cb (16,)."""
+    x = np.asarray(x, dtype=np.float32)
+    cb = np.asarray(cb, dtype=np.float32)
+    best = np.abs(x - cb[0]).astype(np.float32)
+    code = np.zeros(x.shape, dtype=np.uint8)
+    for k in range(1, cb.shape[0]):
+        d = np.abs(x - cb[k]).astype(np.float32)
+        take = (d < best) | (np.isnan(d) & ~np.isnan(best))
+        best = np.where(take, d, best)
+        code = np.where(take, np.uint8(k), code)
+    return code
+
+
+def g_from_mt(seed: int, head_dim: int = 128) -> np.ndarray:
+    """(head_dim/2, head_dim) +-1 from textbook MT19937 low bits."""
+    qd = head_dim // 2
+    b = mt19937.bits(seed, qd * head_dim).reshape(qd, head_dim).astype(np.float64)
+    return 2.0 * b - 1.0
+
+
+def projections_fp64(error: np.ndarray, G: np.ndarray) -> np.ndarray:
+    """e @ G.T in fp64 (the e_j are fp32 values; fp64 makes the sign exact
+    except when |P| is ~1e-15 of the summands)."""
+    return np.asarray(error, dtype=np.float64) @ np.asarray(G, dtype=np.float64).T
+
+
+def pack_bits_lsb(bits: np.ndarray) -> np.ndarray:
+    """(N, 8k) 0/1 -> (N, k) bytes, bit b of byte m = bits[8m + b]."""
+    N, nb = bits.shape
+    b = bits.reshape(N, nb // 8, 8).astype(np.uint8)
+    return (b << np.arange(8, dtype=np.uint8)).sum(axis=2).astype(np.uint8)
+
+
+def residual_norm(error: np.ndarray) -> np.ndarray:
+    """Correctly rounded (to fp32) ||e||_2 computed in fp64."""
+    e = np.asarray(error, dtype=np.float64)
+    return np.sqrt((e * e).sum(axis=-1)).astype(np.float32)
+
+
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, mask=None) -> torch.Tensor:
+    """Brute-force fp64 GQA softmax attention; q (B,Hq,T,D), k/v (B,Hkv,S,D)."""
+    q = q.double()
+    k = k.double()
+    v = v.double()
+    g = q.shape[1] // k.shape[1]
+    k = k.repeat_interleave(g, dim=1)
+    v = v.repeat_interleave(g, dim=1)
+    s = torch.matmul(q, k.transpose(-2, -1)) * scale
+    if mask is not None:
+        s = s + mask.double()
+    p = torch.softmax(s, dim=-1)
+    return torch.matmul(p, v)
+
+
+def ulp_distance_f32(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """|a - b| in units of fp32 ulps (for finite, same-sign values)."""
+    ai = np.asarray(a, dtype=np.float32).view(np.int32).astype(np.int64)
+    bi = np.asarray(b, dtype=np.float32).view(np.int32).astype(np.int64)
+    return np.abs(ai - bi)
+
+
+SQRT_2_OVER_PI = math.sqrt(2.0 / math.pi)

@@ -1,0 +1,175 @@
+"""GPU parity of compressed-KV attention (omni_attn) against the CPU oracle.
+
+Bar (north star): max-abs <= 2e-3 and mean-abs <= 2e-4 against the
+reference's own CPU path (_fused_attn_python restated in oracle.restate),
+on identical packed inputs.  Shapes cover the reference's tests
+(tests/unit/test_fused_attention.py, test_multi_lora.py) plus the build's
+configs; the same inputs are also checked against fp64 brute force.
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import exact, restate
+from tests import _data
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS, MEAN_ABS = 2e-3, 2e-4
+
+
+def _cache(B, Hkv, S, seed, user_id, D=128, outliers=True, scale_v=1.0):
+    x = _data.kv((2, B, Hkv, S, D), seed=seed, dtype=torch.float32, outliers=outliers)
+    k = restate.wht(x[0])
+    v = restate.wht(x[1]) * scale_v
+    cb = torch.stack([restate.lloyd_max(k[:, h].reshape(-1)[:50000], max_iters=60) for h in range(Hkv)])
+    kn, kq, kr = restate.quantize_heads(k, cb, user_id=user_id)
+    vn, _, _ = restate.quantize_heads(v, cb, user_id=user_id)
+    return kn, kq, kr, vn, cb
+
+
+def _run(device, q, kn, kq, kr, vn, cb, uid, with_qjl=True, scale=None, **kw):
+    from omnistack_rs.kernels.fused_attention import omni_attn
+    args = [t.to(device) for t in (q, kn, kq, kr, vn, cb)]
+    return omni_attn(*args, user_id=uid, scale=scale, with_qjl=with_qjl, **kw)
+
+
+def _assert_close(got, want, tag):
+    d = (got.cpu().double() - want.double()).abs()
+    mx, mn = d.max().item(), d.mean().item()
+    print(f"[attn] {tag}: max {mx:.3e} mean {mn:.3e}", flush=True)
+    assert mx <= MAX_ABS and mn <= MEAN_ABS, f"{tag}: max {mx:.3e} mean {mn:.3e}"
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,T,S", [
+    (1, 4, 2, 8, 32), (2, 8, 4, 16, 64), (1, 8, 8, 1, 128), (2, 4, 2, 32, 48),   # reference test shapes
+    (4, 8, 4, 1, 256), (2, 32, 8, 1, 50), (3, 32, 8, 1, 1000), (1, 4, 1, 1, 17), (2, 2, 2, 5, 1),
+])
+@pytest.mark.parametrize("with_qjl", [True, False])
+def test_attn_matches_oracle(device, B, Hq, Hkv, T, S, with_qjl):
+    uid = 7
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=1000 + S, user_id=uid)
+    q = _data.query((B, Hq, T, 128), seed=S + T)
+    got = _run(device, q, kn, kq, kr, vn, cb, uid, with_qjl)
+    assert got.dtype == torch.float32 and got.shape == (B, Hq, T, 128)
+    want = restate.fused_attn_python(q, kn, kq, kr, vn, cb, uid, 1 / math.sqrt(128), with_qjl)
+    _assert_close(got, want, f"B{B} Hq{Hq} Hkv{Hkv} T{T} S{S} qjl{int(with_qjl)}")
+
+
+def test_attn_long_context_split(device):
+    # split-K path (several blocks per (b, kv head) + combine)
+    B, Hq, Hkv, T, S, uid = 2, 8, 2, 1, 8192, 42
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=77, user_id=uid)
+    q = _data.query((B, Hq, T, 128), seed=78)
+    got = _run(device, q, kn, kq, kr, vn, cb, uid)
+    want = restate.fused_attn_python(q, kn, kq, kr, vn, cb, uid, 1 / math.sqrt(128), True)
+    _assert_close(got, want, "S8192 split")
+
+
+def test_attn_vs_fp64(device):
+    B, Hq, Hkv, T, S, uid = 2, 8, 2, 2, 300, 3
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=5, user_id=uid)
+    q = _data.query((B, Hq, T, 128), seed=6)
+    got = _run(device, q, kn, kq, kr, vn, cb, uid)
+    k = restate.dequantize_heads(kn, kq, kr, cb, user_id=uid)
+    v = restate.dequantize_heads(vn, kq, kr, cb, user_id=uid, with_qjl=False)
+    _assert_close(got, exact.attention(q, k, v, 1 / math.sqrt(128)), "fp64")
+
+
+def test_attn_v_constant_gives_constant(device):
+    B, Hq, Hkv, T, S = 1, 4, 2, 3, 64
+    kn, kq, kr, _, cb = _cache(B, Hkv, S, seed=8, user_id=0)
+    vn = torch.full((B, Hkv, S, 64), 0x55, dtype=torch.uint8)      # every V code = 5
+    q = _data.query((B, Hq, T, 128), seed=9)
+    got = _run(device, q, kn, kq, kr, vn, cb, 0).cpu()
+    want = cb[:, 5].repeat_interleave(Hq // Hkv).reshape(1, Hq, 1, 1).expand(B, Hq, T, 128)
+    assert (got - want).abs().max().item() < 1e-6
+
+
+def test_attn_extreme_q_no_overflow(device):
+    kn, kq, kr, vn, cb = _cache(1, 2, 64, seed=10, user_id=0)
+    q = torch.randn(1, 4, 4, 128, generator=_data.gen(11)) * 200.0
+    got = _run(device, q, kn, kq, kr, vn, cb, 0)
+    assert torch.isfinite(got).all()
+    want = restate.fused_attn_python(q, kn, kq, kr, vn, cb, 0, 1 / math.sqrt(128), True)
+    _assert_close(got, want, "q x200")
+
+
+def test_attn_user_id_and_qjl_change_output(device):
+    kn, kq, kr, vn, cb = _cache(1, 2, 32, seed=12, user_id=0)
+    q = _data.query((1, 4, 4, 128), seed=13)
+    a = _run(device, q, kn, kq, kr, vn, cb, 0)
+    b = _run(device, q, kn, kq, kr, vn, cb, 1)
+    c = _run(device, q, kn, kq, kr, vn, cb, 0, with_qjl=False)
+    assert (a - b).abs().max().item() > 1e-5 and (a - c).abs().max().item() > 1e-6
+
+
+def test_attn_inputs_not_modified(device):
+    kn, kq, kr, vn, cb = _cache(1, 2, 32, seed=14, user_id=0)
+    q = _data.query((1, 4, 4, 128), seed=15)
+    ts = [t.to(device) for t in (q, kn, kq, kr, vn, cb)]
+    before = [t.clone() for t in ts]
+    from omnistack_rs.kernels.fused_attention import omni_attn
+    omni_attn(*ts, user_id=0)
+    assert all(torch.equal(a, b) for a, b in zip(ts, before))
+
+
+def test_attn_custom_scale_and_fp32_q(device):
+    kn, kq, kr, vn, cb = _cache(2, 2, 90, seed=16, user_id=2)
+    q = torch.randn(2, 4, 3, 128, generator=_data.gen(17))
+    got = _run(device, q, kn, kq, kr, vn, cb, 2, scale=0.05)
+    want = restate.fused_attn_python(q, kn, kq, kr, vn, cb, 2, 0.05, True)
+    _assert_close(got, want, "scale 0.05")
+
+
+def test_attn_causal_offset(device):
+    B, Hq, Hkv, T, S, off, uid = 2, 8, 2, 40, 200, 160, 4
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=18, user_id=uid)
+    q = _data.query((B, Hq, T, 128), seed=19)
+    got = _run(device, q, kn, kq, kr, vn, cb, uid, causal_offset=off)
+    mask = torch.zeros(1, 1, T, S)
+    for t in range(T):
+        mask[..., t, off + t + 1:] = float("-inf")
+    want = restate.fused_attn_python(q, kn, kq, kr, vn, cb, uid, 1 / math.sqrt(128), True, mask=mask)
+    _assert_close(got, want, "causal")
+
+
+def test_attn_rotate_q_in_kernel(device):
+    B, Hq, Hkv, T, S, uid = 2, 8, 2, 1, 100, 5
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=20, user_id=uid)
+    q = _data.query((B, Hq, T, 128), seed=21)
+    s = _data.sign_flip()
+    got = _run(device, q, kn, kq, kr, vn, cb, uid, rotate_q=True, sign_flip=s.to(device))
+    want = restate.fused_attn_python(restate.rotate(q, s), kn, kq, kr, vn, cb, uid, 1 / math.sqrt(128), True)
+    _assert_close(got, want, "rotate_q")
+
+
+def test_attn_head_dim_32(device):
+    B, Hq, Hkv, T, S, uid = 2, 8, 2, 3, 120, 6
+    x = torch.randn(2, B, Hkv, S, 32, generator=_data.gen(22))
+    k, v = restate.wht(x[0]), restate.wht(x[1])
+    cb = torch.stack([restate.lloyd_max(k[:, h].reshape(-1), max_iters=60) for h in range(Hkv)])
+    kn, kq, kr = restate.quantize_heads(k, cb, user_id=uid)
+    vn, _, _ = restate.quantize_heads(v, cb, user_id=uid)
+    q = torch.randn(B, Hq, T, 32, generator=_data.gen(23))
+    got = _run(device, q, kn, kq, kr, vn, cb, uid)
+    want = restate.fused_attn_python(q, kn, kq, kr, vn, cb, uid, 1 / math.sqrt(32), True)
+    _assert_close(got, want, "d32")
+
+
+def test_attn_shared_codebook(device):
+    kn, kq, kr, vn, cb = _cache(1, 2, 70, seed=24, user_id=0)
+    cb1 = cb[0]
+    q = _data.query((1, 4, 2, 128), seed=25)
+    got = _run(device, q, kn, kq, kr, vn, cb1, 0)
+    want = restate.fused_attn_python(q, kn, kq, kr, vn, cb1, 0, 1 / math.sqrt(128), True)
+    _assert_close(got, want, "shared cb")
+
+
+def test_attn_rejects_bad_shapes(device):
+    kn, kq, kr, vn, cb = _cache(1, 2, 16, seed=26, user_id=0)
+    with pytest.raises(ValueError):
+        _run(device, torch.randn(1, 3, 1, 128), kn, kq, kr, vn, cb, 0)
+    with pytest.raises(ValueError):
+        _run(device, torch.randn(1, 4, 1, 128), kn, kq, kr, vn[:, :, :8], cb, 0)

@@ -1,0 +1,206 @@
+"""GPU parity of the codec kernels against the CPU oracle (bit-exact bar).
+
+WHT rotation, the fused encoder (nibbles, QJL sign bytes, norms) and the
+dequantizer run through libomnistack_amd.so on cuda:0 and are compared with
+oracle.restate on the same seeded inputs.  Sign bits must equal the exact
+(fp64) projection sign everywhere and the oracle's fp32-BLAS sign except
+where |P|/||e|| < 1e-6 (boundary rule); norms must be within 1 ulp of the
+correctly rounded fp64 norm and 2 ulp of the oracle's fp32 torch norm.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import exact, restate
+from tests import _data
+
+pytestmark = pytest.mark.gpu
+
+
+def _check_encode(x_rot_cpu, cb_cpu, user_id, nib, qjl, nrm, tag=""):
+    """x_rot_cpu: the rotated fp input on CPU exactly as the encoder sees it."""
+    B, H, T, D = x_rot_cpu.shape
+    r_nib, r_qjl, r_nrm = restate.quantize_heads(x_rot_cpu, cb_cpu, user_id=user_id)
+    nib, qjl, nrm = nib.cpu(), qjl.cpu(), nrm.cpu()
+    assert torch.equal(nib, r_nib), f"{tag}: nibbles differ at {(nib != r_nib).nonzero()[:5].tolist()}"
+    # residuals + exact projections per head
+    per_head = cb_cpu.dim() == 2
+    n_mis_oracle = 0
+    for h in range(H):
+        cb = (cb_cpu[h] if per_head else cb_cpu).float()
+        xh = x_rot_cpu[:, h].reshape(-1, D).float()
+        _, deq = restate.quantize_int4(xh, cb)
+        e = (xh - deq).numpy()
+        P = exact.projections_fp64(e, exact.g_from_mt(restate.make_qjl_seed(user_id, h), D))
+        ebits = exact.pack_bits_lsb((P >= 0).astype(np.uint8))
+        g = qjl[:, h].reshape(-1, D // 16).numpy()
+        finite = np.isfinite(e).all(axis=1)
+        assert np.array_equal(g[finite], ebits[finite]), f"{tag}: sign bits differ from exact sign (head {h})"
+        o = r_qjl[:, h].reshape(-1, D // 16).numpy()
+        diff = np.unpackbits(g ^ o, axis=1, bitorder="little").astype(bool)
+        if diff.any():
+            en = np.linalg.norm(e.astype(np.float64), axis=1, keepdims=True)
+            rel = np.abs(P) / np.where(en > 0, en, 1)
+            assert (rel[diff] < 1e-6).all(), f"{tag}: sign mismatch outside the boundary rule"
+            n_mis_oracle += int(diff.sum())
+        gn = nrm[:, h].reshape(-1).numpy()
+        en32 = exact.residual_norm(e)
+        fin = np.isfinite(en32)
+        assert exact.ulp_distance_f32(gn[fin], en32[fin]).max(initial=0) <= 1, f"{tag}: norm vs exact"
+        assert exact.ulp_distance_f32(gn[fin], r_nrm[:, h].reshape(-1).numpy()[fin]).max(initial=0) <= 2
+    return n_mis_oracle
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("use_sign", [False, True])
+def test_wht_bit_exact(device, dtype, use_sign):
+    from omnistack_rs.kernels.hadamard import rotate, rotate_queries
+    x = _data.kv((3, 4, 37, 128), dtype=dtype)
+    s = _data.sign_flip() if use_sign else None
+    got = rotate(x.to(device), None if s is None else s.to(device)).cpu()
+    want = restate.rotate(x, s)
+    assert got.dtype == dtype
+    assert torch.equal(got.view(torch.int16) if dtype != torch.float32 else got.view(torch.int32),
+                       want.view(torch.int16) if dtype != torch.float32 else want.view(torch.int32))
+    if not use_sign:
+        assert torch.equal(rotate_queries(x.to(device)).cpu(), want)
+
+
+def test_wht_rejects_bad_dim(device):
+    from omnistack_rs.kernels.hadamard import rotate_queries
+    with pytest.raises(ValueError, match="head_dim"):
+        rotate_queries(torch.randn(2, 64, device=device))
+
+
+@pytest.mark.parametrize("B,H,T", [(2, 4, 8), (1, 8, 300), (3, 2, 1), (2, 8, 513)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_quantize_heads_bit_exact(device, B, H, T, dtype):
+    from omnistack_rs.kernels.quantize import quantize_heads
+    print(f"[encode] B={B} H={H} T={T} {dtype}", flush=True)
+    x = restate.wht(_data.kv((B, H, T, 128), seed=B * 100 + T, dtype=dtype))
+    cb = _data.gaussian_codebook(H) * torch.linspace(0.8, 1.6, H).reshape(H, 1)
+    uid = 42
+    nib, qjl, nrm = quantize_heads(x.to(device), cb.to(device), user_id=uid)
+    assert nib.shape == (B, H, T, 64) and qjl.shape == (B, H, T, 8) and nrm.shape == (B, H, T)
+    assert nib.dtype == torch.uint8 and qjl.dtype == torch.uint8 and nrm.dtype == torch.float32
+    _check_encode(x, cb, uid, nib, qjl, nrm, tag=f"{B}x{H}x{T}")
+
+
+def test_quantize_heads_shared_codebook_and_uids(device):
+    from omnistack_rs.kernels.quantize import quantize_heads
+    x = restate.wht(_data.kv((2, 3, 40, 128), seed=5, dtype=torch.float32))
+    cb = _data.gaussian_codebook(1)[0]
+    for uid in (0, 7, 1023, 1024, 5000):
+        nib, qjl, nrm = quantize_heads(x.to(device), cb.to(device), user_id=uid)
+        _check_encode(x, cb, uid, nib, qjl, nrm, tag=f"uid{uid}")
+    # user 1024 aliases user 0 (reference test_quant.py:626-632)
+    a = quantize_heads(x.to(device), cb.to(device), user_id=0)[1]
+    b = quantize_heads(x.to(device), cb.to(device), user_id=1024)[1]
+    assert torch.equal(a, b)
+
+
+def test_encode_edge_cases(device):
+    from omnistack_rs.kernels.quantize import quantize_heads
+    cb = _data.gaussian_codebook(1)[0].clone()
+    cb[7] = cb[8]                                        # duplicate centroid (ties)
+    x = torch.randn(1, 1, 64, 128, generator=_data.gen(9))
+    x[0, 0, 0] = 0.0                                     # all-zero residual candidates
+    x[0, 0, 1, :16] = cb                                 # exact centroid hits
+    x[0, 0, 2, :15] = (cb[:-1] + cb[1:]) / 2             # midpoints
+    x[0, 0, 3] = cb[3]                                   # residual exactly zero -> 0xFF
+    x[0, 0, 4, :5] = torch.tensor([1e30, -1e30, 1e-30, -1e-30, 0.0])
+    x[0, 0, 5] = 100.0                                   # far outside the codebook
+    nib, qjl, nrm = quantize_heads(x.to(device), cb.to(device), user_id=3)
+    _check_encode(x, cb, 3, nib, qjl, nrm, tag="edge")
+    assert (qjl[0, 0, 3].cpu() == 0xFF).all()
+    assert nrm[0, 0, 3].item() == 0.0
+
+
+def test_encode_nonfinite_rows(device):
+    from omnistack_rs.kernels.quantize import quantize_heads
+    cb = _data.gaussian_codebook(1)[0]
+    x = torch.randn(1, 1, 4, 128, generator=_data.gen(10))
+    x[0, 0, 0, 5] = float("nan")
+    x[0, 0, 1, 9] = float("inf")
+    x[0, 0, 2, 9], x[0, 0, 2, 10] = float("inf"), float("-inf")
+    nib, qjl, nrm = quantize_heads(x.to(device), cb.to(device), user_id=1)
+    r_nib, r_qjl, r_nrm = restate.quantize_heads(x, cb, user_id=1)
+    assert torch.equal(nib.cpu(), r_nib)
+    assert torch.equal(qjl.cpu(), r_qjl)                 # non-finite sums have order-free signs
+    assert torch.isnan(nrm[0, 0, 0]).item() and torch.isinf(nrm[0, 0, 1]).item()
+
+
+def test_encode_kv_fused_rotation(device):
+    from omnistack_rs.kernels.quantize import encode_kv
+    x = _data.kv((2, 8, 200, 128))                       # bf16 with outliers
+    s = _data.sign_flip()
+    cb = _data.gaussian_codebook(8)
+    nib, qjl, nrm = encode_kv(x.to(device), cb.to(device), user_id=42, sign_flip=s.to(device))
+    _check_encode(restate.rotate(x, s), cb, 42, nib, qjl, nrm, tag="fused")
+
+
+def test_encode_head_dim_32(device):
+    from omnistack_rs.kernels.quantize import quantize_heads
+    x = restate.wht(torch.randn(2, 3, 50, 32, generator=_data.gen(11)))
+    cb = _data.gaussian_codebook(3)
+    nib, qjl, nrm = quantize_heads(x.to(device), cb.to(device), user_id=4)
+    assert nib.shape == (2, 3, 50, 16) and qjl.shape == (2, 3, 50, 2)
+    _check_encode(x, cb, 4, nib, qjl, nrm, tag="d32")
+
+
+def test_encode_empty_and_input_untouched(device):
+    from omnistack_rs.kernels.quantize import quantize_heads
+    cb = _data.gaussian_codebook(2).to(device)
+    nib, qjl, nrm = quantize_heads(torch.zeros(2, 2, 0, 128, device=device), cb)
+    assert nib.shape == (2, 2, 0, 64)
+    x = torch.randn(1, 2, 9, 128, device=device)
+    x0 = x.clone()
+    quantize_heads(x, cb)
+    assert torch.equal(x, x0)
+    with pytest.raises(ValueError):
+        quantize_heads(x, torch.zeros(3, 16, device=device))
+
+
+@pytest.mark.parametrize("with_qjl", [True, False])
+@pytest.mark.parametrize("D", [128, 32])
+def test_dequantize_bit_exact(device, with_qjl, D):
+    from omnistack_rs.kernels.quantize import dequantize_heads
+    g = _data.gen(12)
+    B, H, T = 2, 4, 77
+    nib = torch.randint(0, 256, (B, H, T, D // 2), generator=g, dtype=torch.uint8)
+    qjl = torch.randint(0, 256, (B, H, T, D // 16), generator=g, dtype=torch.uint8)
+    nrm = torch.rand(B, H, T, generator=g) * 3
+    cb = _data.gaussian_codebook(H) * torch.linspace(0.5, 2.0, H).reshape(H, 1)
+    got = dequantize_heads(nib.to(device), qjl.to(device), nrm.to(device), cb.to(device), user_id=17,
+                           with_qjl=with_qjl).cpu()
+    want = restate.dequantize_heads(nib, qjl, nrm, cb, user_id=17, with_qjl=with_qjl)
+    assert torch.equal(got.view(torch.int32), want.view(torch.int32))
+
+
+def test_encode_decode_roundtrip_mse(device):
+    from omnistack_rs.kernels.quantize import quantize_heads, dequantize_heads
+    x = restate.wht(torch.randn(2, 4, 64, 128, generator=_data.gen(13))).to(device)
+    cb = _data.gaussian_codebook(4).to(device)
+    nib, qjl, nrm = quantize_heads(x, cb, user_id=5)
+    x4 = dequantize_heads(nib, qjl, nrm, cb, user_id=5, with_qjl=False)
+    xq = dequantize_heads(nib, qjl, nrm, cb, user_id=5, with_qjl=True)
+    xw = dequantize_heads(nib, qjl, nrm, cb, user_id=6, with_qjl=True)
+    m4, mq, mw = (((x - y) ** 2).mean().item() for y in (x4, xq, xw))
+    assert (m4 - mq) / m4 >= 0.05                        # reference test_quant.py:308-322
+    assert mw > mq                                       # wrong user id is worse (:647-664)
+
+
+def test_rows_api_matches_oracle(device):
+    from omnistack_rs.kernels.quantize import quantize_rows, dequantize_rows
+    x = restate.wht(torch.randn(2, 3, 5, 128, generator=_data.gen(14)))
+    cb = _data.gaussian_codebook(1)[0]
+    nib, qjl, nrm = quantize_rows(x.to(device), cb.to(device), base_head_idx=3, user_id=11)
+    r_nib, r_qjl, r_nrm = restate.quantize_rows(x, cb, base_head_idx=3, user_id=11)
+    assert torch.equal(nib.cpu(), r_nib)
+    assert (qjl.cpu() != r_qjl).sum().item() == 0
+    assert exact.ulp_distance_f32(nrm.cpu().numpy(), r_nrm.numpy()).max() <= 2
+    out = dequantize_rows(nib, qjl, nrm, cb.to(device), base_head_idx=3, user_id=11).cpu()
+    want = restate.dequantize_rows(nib.cpu(), qjl.cpu(), nrm.cpu(), cb, base_head_idx=3, user_id=11)
+    assert (out - want).abs().max().item() < 1e-6

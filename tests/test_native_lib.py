@@ -1,0 +1,164 @@
+"""The C ABI library: loads, exports every symbol the header declares, and its
+host-only routines behave (no GPU needed).  CPU only."""
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import exact
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "omnistack_amd.h")
+
+
+def _declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(omni_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def L():
+    from omnistack_rs import _lib
+    return _lib.lib()
+
+
+def test_library_exports_every_declared_symbol(L):
+    from omnistack_rs import _lib
+    syms = _declared_symbols()
+    assert len(syms) >= 9
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r"\bT (omni_\w+)", out))
+    missing = [s for s in syms if s not in exported]
+    assert not missing, missing
+    assert set(_lib.SIGNATURES) == set(syms)
+
+
+def test_abi_version(L):
+    assert L.omni_abi_version() == 1
+
+
+@pytest.mark.parametrize("seed", [0, 42, 42 ^ 5, 1023, 2047])
+@pytest.mark.parametrize("D", [128, 32])
+def test_host_g_bits_equal_torch_randint(seed, D):
+    from omnistack_rs import _lib
+    words = _lib.qjl_g_bits_host(seed, D).numpy().view(np.uint32)
+    bits = np.unpackbits(words.view(np.uint8), bitorder="little").reshape(D // 2, D)
+    gen = torch.Generator().manual_seed(seed)
+    ref = torch.randint(0, 2, (D // 2, D), generator=gen).numpy()
+    assert np.array_equal(bits, ref)
+    assert np.array_equal(bits * 2.0 - 1, exact.g_from_mt(seed, D))
+
+
+def test_validation_errors_before_any_device_work(L):
+    from omnistack_rs import _lib
+    rc = L.omni_encode(None, 0, 1, 1, 1, 64, 0, None, None, 0, None, None, None, None, None)
+    assert rc == _lib.OMNI_EINVAL and "head_dim" in _lib.last_error()
+    rc = L.omni_attn(None, 0, None, None, None, None, None, 0, None, 1, 6, 4, 1, 1, 128, 1.0, 0, -1, 0,
+                     None, None, None, 0, None)
+    assert rc == _lib.OMNI_EINVAL and "divisible" in _lib.last_error()
+    rc = L.omni_lora_apply(None, 0, None, None, None, 0, None, 1, 1, 1, 128, 8, 65, 1, 1.0, None, None)
+    assert rc == _lib.OMNI_EINVAL and "rank" in _lib.last_error()
+    rc = L.omni_wht_rotate(None, 0, 1, 100, None, None, None)
+    assert rc == _lib.OMNI_EINVAL
+    with pytest.raises(ValueError):
+        _lib.check(rc)
+    assert L.omni_qjl_g_bits(1, 64, None) == _lib.OMNI_EINVAL
+
+
+def test_empty_shapes_are_noops(L):
+    assert L.omni_encode(None, 2, 0, 8, 0, 128, 0, None, None, 0, None, None, None, None, None) == 0
+    assert L.omni_dequantize(None, None, None, None, 0, None, 0, 8, 10, 128, 1, None, None) == 0
+    assert L.omni_attn(None, 2, None, None, None, None, None, 0, None, 0, 4, 2, 1, 10, 128, 1.0, 1, -1, 0,
+                       None, None, None, 0, None) == 0
+
+
+def test_workspace_size_host_only(L):
+    # planning is host arithmetic; C3 shape needs split partials
+    n = L.omni_attn_workspace_size(32, 32, 8, 1, 8192, 128)
+    assert n % 4 == 0
+    assert L.omni_attn_workspace_size(1, 3, 2, 1, 10, 128) == 0   # invalid GQA -> 0
+
+
+def test_host_api_rejects_cpu_tensors():
+    from omnistack_rs.kernels.quantize import quantize_heads
+    from omnistack_rs.kernels.fused_attention import omni_attn
+    x = torch.randn(1, 2, 4, 128)
+    with pytest.raises(RuntimeError, match="HIP devices only"):
+        quantize_heads(x, torch.linspace(-1, 1, 16))
+    nib = torch.zeros(1, 2, 4, 64, dtype=torch.uint8)
+    with pytest.raises(RuntimeError, match="HIP devices only"):
+        omni_attn(torch.randn(1, 4, 1, 128), nib, torch.zeros(1, 2, 4, 8, dtype=torch.uint8),
+                  torch.zeros(1, 2, 4), nib, torch.zeros(2, 16))
+
+
+def test_reference_signatures_kept():
+    import inspect
+    from omnistack_rs.kernels import fused_attention as fa, quantize as qz, hadamard as hd
+    from omnistack_rs import quantization, attention
+    p = lambda f: list(inspect.signature(f).parameters)
+    assert p(fa.omni_attn)[:15] == ["q", "k_nibbles", "k_qjl", "k_norms", "v_nibbles", "codebooks", "user_id",
+                                    "scale", "with_qjl", "g_matrix", "x", "lora_a", "lora_b", "lora_indices",
+                                    "lora_alpha"]
+    assert p(qz.quantize_heads) == ["x", "codebooks", "user_id"]
+    assert p(qz.dequantize_heads) == ["nibbles", "qjl_packed", "norms", "codebooks", "user_id", "with_qjl"]
+    assert p(qz.quantize_rows) == ["x", "codebook", "base_head_idx", "user_id"]
+    assert p(hd.rotate_kv_cache) == ["k", "v"]
+    assert p(attention.reference_attn) == ["q", "k", "v", "mask", "scale", "tile_size"]
+    assert p(quantization.qjl_encode) == ["x_orig", "x_dequant", "head_idx", "qjl_dim", "user_id"]
+    assert qz.QJL_DIM == 64 and qz._NBYTES_NIBBLE == 64 and qz._NBYTES_QJL == 8 and hd.HEAD_DIM == 128
+    assert qz._make_qjl_seed(1025, 7) == 1 ^ 7
+
+
+def test_make_g_matrix_packing():
+    from omnistack_rs.kernels.fused_attention import make_g_matrix
+    lo, hi = make_g_matrix(2, 42)
+    assert lo.shape == (2, 64) and lo.dtype == torch.int64
+    gen = torch.Generator().manual_seed(42)
+    bits = torch.randint(0, 2, (2, 64, 128), generator=gen)
+    j = 5
+    assert ((lo[1, 3] >> j) & 1).item() == bits[1, 3, j].item()
+    assert ((hi[0, 7] >> j) & 1).item() == bits[0, 7, 64 + j].item()
+
+
+def test_omni_config_validation():
+    from omnistack_rs.config import OmniConfig
+    assert OmniConfig().n_groups == 4
+    with pytest.raises(ValueError):
+        OmniConfig(head_dim=96)
+    with pytest.raises(ValueError):
+        OmniConfig(n_heads=6, n_kv_heads=4)
+    with pytest.raises(ValueError):
+        OmniConfig(quant_bits=3)
+
+
+def test_nibble_helpers_known_answers():
+    from omnistack_rs.kernels import quantize as qz
+    codes = torch.zeros(128, dtype=torch.uint8)
+    codes[0], codes[1] = 5, 3
+    assert qz._pack_nibbles_torch(codes)[0].item() == 53
+    packed = torch.zeros(64, dtype=torch.uint8)
+    packed[:4] = torch.tensor([0x53, 0x24, 0x71, 0xA6])
+    assert qz._xor_unpack_word_torch(packed)[:8].tolist() == [3, 5, 4, 2, 1, 7, 6, 10]
+    g = torch.Generator().manual_seed(1)
+    c = torch.randint(0, 16, (5, 128), generator=g, dtype=torch.uint8)
+    assert torch.equal(qz._batch_xor_unpack(qz._batch_pack_nibbles(c)), c)
+    assert torch.equal(qz._unpack_nibbles_torch(qz._pack_nibbles_torch(c[0])), c[0])
+
+
+def test_calibrator_api():
+    from omnistack_rs.quantization import LloydMaxCalibrator, calibrate_per_group
+    with pytest.raises(RuntimeError, match="fit"):
+        _ = LloydMaxCalibrator().codebook
+    with pytest.raises(ValueError, match="16"):
+        LloydMaxCalibrator(n_centroids=8)
+    g = torch.Generator().manual_seed(99)
+    cb = LloydMaxCalibrator().fit(torch.randn(10000, generator=g)).codebook
+    assert cb.shape == (16,) and (cb[1:] > cb[:-1]).all()
+    # Lloyd-Max for N(0,1): outer centroids near +-2.73 (Max 1960)
+    assert abs(cb[-1].item() - 2.733) < 0.15 and abs(cb[0].item() + 2.733) < 0.15
+    assert calibrate_per_group([torch.randn(500, generator=g), torch.randn(500, generator=g) * 3]).shape == (2, 16)
