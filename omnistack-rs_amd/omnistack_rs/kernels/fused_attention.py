@@ -111,6 +111,8 @@ def _attn(q, k_nibbles, k_qjl, k_norms, v_nibbles, codebooks, user_id, scale, wi
     gb = _lib.g_bits(_lib.head_seeds(user_id, Hkv), D, dev) if with_qjl else None
     sf = None
     if rotate_q and sign_flip is not None:
+        if sign_flip.numel() != D:
+            raise ValueError(f"sign_flip must have {D} entries, got {sign_flip.numel()}")
         sf = torch.where(sign_flip.reshape(-1) < 0, -1, 1).to(torch.int8).to(dev).contiguous()
     out = torch.empty(B, Hq, T, D, dtype=torch.float32, device=dev)
     L = _lib.lib()
@@ -200,6 +202,8 @@ class PackedKVAttention:
         self.gb = _lib.g_bits(_lib.head_seeds(user_id, Hkv), D, dev) if with_qjl else None
         self.sf = None
         if rotate_q and sign_flip is not None:
+            if sign_flip.numel() != D:
+                raise ValueError(f"sign_flip must have {D} entries, got {sign_flip.numel()}")
             self.sf = torch.where(sign_flip.reshape(-1) < 0, -1, 1).to(torch.int8).to(dev).contiguous()
         self.shape = (B, n_heads, q_tokens, D)
         self.q_dtype = q_dtype

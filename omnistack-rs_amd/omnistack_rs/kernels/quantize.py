@@ -102,7 +102,9 @@ def _encode(x: torch.Tensor, codebooks: torch.Tensor, user_id: int, rotate: bool
     nrm = torch.empty(B, H, T, dtype=torch.float32, device=dev)
     sf = None
     if sign_flip is not None:
-        sf = torch.where(sign_flip.reshape(-1) < 0, -1, 1).to(torch.int8).contiguous()
+        if sign_flip.numel() != D:
+            raise ValueError(f"sign_flip must have {D} entries, got {sign_flip.numel()}")
+        sf = torch.where(sign_flip.reshape(-1) < 0, -1, 1).to(torch.int8).to(dev).contiguous()
     _lib.check(_lib.lib().omni_encode(
         _lib.ptr(xc), _lib.dtype_code(xc.dtype), B, H, T, D, int(rotate), _lib.ptr(sf),
         _lib.ptr(cb), per_head, _lib.ptr(gb), _lib.ptr(nib), _lib.ptr(qjl), _lib.ptr(nrm),
