@@ -15,12 +15,13 @@
 // tokens), so every cached byte is read once per group, not once per q head.
 // Each wave takes 16-token tiles round-robin and runs three MFMA chains
 // (v_mfma_f32_16x16x16_f16, tokens on M, query rows on N):
-//   S^T  = K_hat16 (16 x D)  . (scale log2e Q)^T        D/16 k-steps
+//   S^T  = K16 (16 x D) . (scale log2e Q16)^T, three fp16 passes
+//          (K_hi.Q_hi + K_hi.Q_lo + K_lo.Q_hi)         3 * D/16 k-steps
 //   C^T  = B+-     (16 x D/2) . (scale log2e G Q)^T      D/32 k-steps
 //   O^T += V^T_hi (D x 16)   . P^T ; O^T += V^T_lo . P^T  D/16 row blocks
-// K_hat16 is the fp16 codebook value (one LDS lookup per cache byte gives
-// two halves).  V is split hi + lo (two fp16) so the value path keeps ~22
-// bits.  Online softmax in fp32 (exp2 domain) with P rounded to fp16 for
+// Codebook values enter as fp16 hi + fp16 remainder (one 8-byte LDS lookup
+// per cache byte gives both halves of two codes); q is split the same way,
+// so scores and values keep ~22 bits.  Online softmax in fp32 (exp2 domain) with P rounded to fp16 for
 // the PV product; the softmax denominator sums the same rounded P.
 #include <math.h>
 
@@ -79,8 +80,8 @@ __device__ __forceinline__ float wave_sum_xor16_32(float v) {
 }
 
 // Dynamic LDS layout (bytes):
-//   klut  256*ncopy u32      K:  byte -> (hi(cb[lo nib]), hi(cb[hi nib]))
-//   vlut  256*ncopy uint2    V:  byte -> (hi pair, lo pair)
+//   lut   256*ncopy uint2    byte -> (hi pair, lo pair): fp16 hi(cb[lo nib]),
+//                            hi(cb[hi nib]) and the fp16 remainders cb - hi
 //   qlut  16 uint2           QJL nibble -> four +-1.0 halves
 //   qs    kRows*D f32        query rows (fp32, rotated if requested)
 //   gq    kRows*D/2 f32      G_h q rows
@@ -88,7 +89,7 @@ __device__ __forceinline__ float wave_sum_xor16_32(float v) {
 template <int D>
 struct Lds {
     static constexpr int QD = D / 2;
-    __host__ __device__ static size_t lut_bytes(int ncopy) { return (size_t)256 * ncopy * 12 + 16 * 8; }
+    __host__ __device__ static size_t lut_bytes(int ncopy) { return (size_t)256 * ncopy * 8 + 16 * 8; }
     __host__ __device__ static size_t comb_bytes(int nw) { (void)nw; return (size_t)(2 * kMaxWaves * kRows + kRows * D) * 4; }
     __host__ __device__ static size_t fixed_bytes() { return (size_t)kRows * (D + QD) * 4; }
     static size_t total(int ncopy, int nw) {
@@ -107,9 +108,8 @@ __global__ __launch_bounds__(64 * kMaxWaves) void attn_kernel(AttnArgs a) {
 
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const int ncopy = a.ncopy;
-    uint32_t *klut = reinterpret_cast<uint32_t *>(smem);
-    uint2 *vlut = reinterpret_cast<uint2 *>(smem + (size_t)256 * ncopy * 4);
-    uint2 *qlut = reinterpret_cast<uint2 *>(smem + (size_t)256 * ncopy * 12);
+    uint2 *vlut = reinterpret_cast<uint2 *>(smem);
+    uint2 *qlut = reinterpret_cast<uint2 *>(smem + (size_t)256 * ncopy * 8);
     const int nw = blockDim.x >> 6;
     const size_t var_bytes = Lds<D>::lut_bytes(ncopy) > Lds<D>::comb_bytes(nw) ? Lds<D>::lut_bytes(ncopy)
                                                                                  : Lds<D>::comb_bytes(nw);
@@ -132,9 +132,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void attn_kernel(AttnArgs a) {
         const int e = s / ncopy;
         const float c0 = cbp[e & 15], c1 = cbp[e >> 4];
         const float h0 = f16_to_f32(f32_to_f16_rne(c0)), h1 = f16_to_f32(f32_to_f16_rne(c1));
-        const uint32_t hi = pack_h2(c0, c1);
-        klut[s] = hi;
-        vlut[s] = make_uint2(hi, pack_h2(c0 - h0, c1 - h1));
+        vlut[s] = make_uint2(pack_h2(c0, c1), pack_h2(c0 - h0, c1 - h1));
     }
     if (tid < 16) {
         uint32_t w[2];
@@ -191,12 +189,20 @@ __global__ __launch_bounds__(64 * kMaxWaves) void attn_kernel(AttnArgs a) {
     // ── per-lane MFMA B operands ──────────────────────────────────────
     const int r = lane & 15;          // query row (MFMA column)
     const int g = lane >> 4;          // k-group
-    half4_t qb[KSTEPS];
+    // Q in two fp16 halves (hi + remainder): with the codebook's hi/lo split
+    // the score keeps ~22 bits (hi.hi + lo_q.hi + hi.lo_k).
+    half4_t qb[KSTEPS], qbl[KSTEPS];
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) {
         const float *row = qs + r * D + g * (D / 4) + 4 * s;
-        qb[s] = as_half4(pack_h2(row[0] * a.qscale, row[1] * a.qscale),
-                         pack_h2(row[2] * a.qscale, row[3] * a.qscale));
+        float v[4], lo[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            v[j] = row[j] * a.qscale;
+            lo[j] = v[j] - f16_to_f32(f32_to_f16_rne(v[j]));
+        }
+        qb[s] = as_half4(pack_h2(v[0], v[1]), pack_h2(v[2], v[3]));
+        qbl[s] = as_half4(pack_h2(lo[0], lo[1]), pack_h2(lo[2], lo[3]));
     }
     half4_t gb[QSTEPS];
 #pragma unroll
@@ -247,8 +253,11 @@ __global__ __launch_bounds__(64 * kMaxWaves) void attn_kernel(AttnArgs a) {
             const uint32_t w = kw[s >> 1];
             const uint32_t b0 = (w >> (16 * (s & 1))) & 0xffu;
             const uint32_t b1 = (w >> (16 * (s & 1) + 8)) & 0xffu;
-            const half4_t av = as_half4(klut[b0 * ncopy + cl], klut[b1 * ncopy + cl]);
-            sacc = __builtin_amdgcn_mfma_f32_16x16x16f16(av, qb[s], sacc, 0, 0, 0);
+            const uint2 e0 = vlut[b0 * ncopy + cl], e1 = vlut[b1 * ncopy + cl];
+            const half4_t ah = as_half4(e0.x, e1.x), al = as_half4(e0.y, e1.y);
+            sacc = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, qb[s], sacc, 0, 0, 0);
+            sacc = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, qbl[s], sacc, 0, 0, 0);
+            sacc = __builtin_amdgcn_mfma_f32_16x16x16f16(al, qb[s], sacc, 0, 0, 0);
         }
 
         float4_t cacc = float4_t{0.f, 0.f, 0.f, 0.f};

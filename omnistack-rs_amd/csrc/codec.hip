@@ -162,15 +162,17 @@ __global__ __launch_bounds__(kRowsPerBlock) void encode_kernel(
         v[d] = v[d] - cval;  // residual e_d (fp32), quantize.py:580
     }
 
-    // ||e||_2: fp64 accumulation, rounded once to fp32.
+    // ||e||_2: fp32 squares (as the reference's fp32 norm forms them) summed
+    // in fp64 and rounded once; a sum beyond the fp32 range is +inf, where the
+    // reference's fp32 accumulation overflows.
     double ss = 0.0;
     float abs_sum = 0.0f;
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-        ss += (double)v[d] * (double)v[d];
+        ss += (double)__fmul_rn(v[d], v[d]);
         abs_sum += fabsf(v[d]);
     }
-    const float nrm = (float)sqrt(ss);
+    const float nrm = ss > 3.4028234663852886e38 ? INFINITY : (float)sqrt(ss);
 
     // QJL signs.  fp32 sequential sums carry |err| <= (D-1) u sum|e_j|; a
     // result farther than D * 2^-24 * abs_sum from zero has a certain sign,
@@ -281,8 +283,8 @@ __global__ __launch_bounds__(kRowsPerBlock) void dequant_kernel(
         float v0 = cb[byte & 15u], v1 = cb[byte >> 4];
         if (with_qjl) {
             const int d0 = 2 * m, d1 = 2 * m + 1;
-            const float s0 = (float)(QD - 2 * __popcll(sb ^ gcol[d0]));
-            const float s1 = (float)(QD - 2 * __popcll(sb ^ gcol[d1]));
+            const float s0 = (float)(QD - 2 * (int)__popcll(sb ^ gcol[d0]));
+            const float s1 = (float)(QD - 2 * (int)__popcll(sb ^ gcol[d1]));
             v0 = __fadd_rn(v0, __fmul_rn(s0, sc));
             v1 = __fadd_rn(v1, __fmul_rn(s1, sc));
         }

@@ -52,9 +52,13 @@ def pack_bits_lsb(bits: np.ndarray) -> np.ndarray:
 
 
 def residual_norm(error: np.ndarray) -> np.ndarray:
-    """Correctly rounded (to fp32) ||e||_2 computed in fp64."""
+    """||e||_2 computed in fp64 and rounded to fp32.  A sum of squares beyond
+    the fp32 range gives +inf: the reference's fp32 norm (torch vector_norm,
+    fp32 accumulation without scaling) overflows there."""
     e = np.asarray(error, dtype=np.float64)
-    return np.sqrt((e * e).sum(axis=-1)).astype(np.float32)
+    ss = (e * e).sum(axis=-1)
+    out = np.sqrt(ss).astype(np.float32)
+    return np.where(ss > np.finfo(np.float32).max, np.float32(np.inf), out)
 
 
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, mask=None) -> torch.Tensor:

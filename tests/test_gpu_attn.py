@@ -2,7 +2,11 @@
 
 Bar (north star): max-abs <= 2e-3 and mean-abs <= 2e-4 against the
 reference's own CPU path (_fused_attn_python restated in oracle.restate),
-on identical packed inputs.  Shapes cover the reference's tests
+on identical packed inputs.  The reference's CPU path returns q's dtype
+(reference_attn casts its fp32 result back, attention/reference.py:177)
+while its device path returns fp32; the oracle is therefore fed q as fp32
+holding the identical (bf16) values, which is the reference's own fp32
+computation without the final cast.  Shapes cover the reference's tests
 (tests/unit/test_fused_attention.py, test_multi_lora.py) plus the build's
 configs; the same inputs are also checked against fp64 brute force.
 """
@@ -53,7 +57,7 @@ def test_attn_matches_oracle(device, B, Hq, Hkv, T, S, with_qjl):
     q = _data.query((B, Hq, T, 128), seed=S + T)
     got = _run(device, q, kn, kq, kr, vn, cb, uid, with_qjl)
     assert got.dtype == torch.float32 and got.shape == (B, Hq, T, 128)
-    want = restate.fused_attn_python(q, kn, kq, kr, vn, cb, uid, 1 / math.sqrt(128), with_qjl)
+    want = restate.fused_attn_python(q.float(), kn, kq, kr, vn, cb, uid, 1 / math.sqrt(128), with_qjl)
     _assert_close(got, want, f"B{B} Hq{Hq} Hkv{Hkv} T{T} S{S} qjl{int(with_qjl)}")
 
 
@@ -63,7 +67,7 @@ def test_attn_long_context_split(device):
     kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=77, user_id=uid)
     q = _data.query((B, Hq, T, 128), seed=78)
     got = _run(device, q, kn, kq, kr, vn, cb, uid)
-    want = restate.fused_attn_python(q, kn, kq, kr, vn, cb, uid, 1 / math.sqrt(128), True)
+    want = restate.fused_attn_python(q.float(), kn, kq, kr, vn, cb, uid, 1 / math.sqrt(128), True)
     _assert_close(got, want, "S8192 split")
 
 
@@ -74,7 +78,7 @@ def test_attn_vs_fp64(device):
     got = _run(device, q, kn, kq, kr, vn, cb, uid)
     k = restate.dequantize_heads(kn, kq, kr, cb, user_id=uid)
     v = restate.dequantize_heads(vn, kq, kr, cb, user_id=uid, with_qjl=False)
-    _assert_close(got, exact.attention(q, k, v, 1 / math.sqrt(128)), "fp64")
+    _assert_close(got, exact.attention(q.float(), k, v, 1 / math.sqrt(128)), "fp64")
 
 
 def test_attn_v_constant_gives_constant(device):
@@ -92,7 +96,7 @@ def test_attn_extreme_q_no_overflow(device):
     q = torch.randn(1, 4, 4, 128, generator=_data.gen(11)) * 200.0
     got = _run(device, q, kn, kq, kr, vn, cb, 0)
     assert torch.isfinite(got).all()
-    want = restate.fused_attn_python(q, kn, kq, kr, vn, cb, 0, 1 / math.sqrt(128), True)
+    want = restate.fused_attn_python(q.float(), kn, kq, kr, vn, cb, 0, 1 / math.sqrt(128), True)
     _assert_close(got, want, "q x200")
 
 
@@ -119,7 +123,7 @@ def test_attn_custom_scale_and_fp32_q(device):
     kn, kq, kr, vn, cb = _cache(2, 2, 90, seed=16, user_id=2)
     q = torch.randn(2, 4, 3, 128, generator=_data.gen(17))
     got = _run(device, q, kn, kq, kr, vn, cb, 2, scale=0.05)
-    want = restate.fused_attn_python(q, kn, kq, kr, vn, cb, 2, 0.05, True)
+    want = restate.fused_attn_python(q.float(), kn, kq, kr, vn, cb, 2, 0.05, True)
     _assert_close(got, want, "scale 0.05")
 
 
@@ -131,7 +135,7 @@ def test_attn_causal_offset(device):
     mask = torch.zeros(1, 1, T, S)
     for t in range(T):
         mask[..., t, off + t + 1:] = float("-inf")
-    want = restate.fused_attn_python(q, kn, kq, kr, vn, cb, uid, 1 / math.sqrt(128), True, mask=mask)
+    want = restate.fused_attn_python(q.float(), kn, kq, kr, vn, cb, uid, 1 / math.sqrt(128), True, mask=mask)
     _assert_close(got, want, "causal")
 
 
@@ -141,7 +145,7 @@ def test_attn_rotate_q_in_kernel(device):
     q = _data.query((B, Hq, T, 128), seed=21)
     s = _data.sign_flip()
     got = _run(device, q, kn, kq, kr, vn, cb, uid, rotate_q=True, sign_flip=s.to(device))
-    want = restate.fused_attn_python(restate.rotate(q, s), kn, kq, kr, vn, cb, uid, 1 / math.sqrt(128), True)
+    want = restate.fused_attn_python(restate.rotate(q, s).float(), kn, kq, kr, vn, cb, uid, 1 / math.sqrt(128), True)
     _assert_close(got, want, "rotate_q")
 
 
@@ -154,7 +158,7 @@ def test_attn_head_dim_32(device):
     vn, _, _ = restate.quantize_heads(v, cb, user_id=uid)
     q = torch.randn(B, Hq, T, 32, generator=_data.gen(23))
     got = _run(device, q, kn, kq, kr, vn, cb, uid)
-    want = restate.fused_attn_python(q, kn, kq, kr, vn, cb, uid, 1 / math.sqrt(32), True)
+    want = restate.fused_attn_python(q.float(), kn, kq, kr, vn, cb, uid, 1 / math.sqrt(32), True)
     _assert_close(got, want, "d32")
 
 
@@ -163,7 +167,7 @@ def test_attn_shared_codebook(device):
     cb1 = cb[0]
     q = _data.query((1, 4, 2, 128), seed=25)
     got = _run(device, q, kn, kq, kr, vn, cb1, 0)
-    want = restate.fused_attn_python(q, kn, kq, kr, vn, cb1, 0, 1 / math.sqrt(128), True)
+    want = restate.fused_attn_python(q.float(), kn, kq, kr, vn, cb1, 0, 1 / math.sqrt(128), True)
     _assert_close(got, want, "shared cb")
 
 

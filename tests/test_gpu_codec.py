@@ -48,6 +48,7 @@ def _check_encode(x_rot_cpu, cb_cpu, user_id, nib, qjl, nrm, tag=""):
         gn = nrm[:, h].reshape(-1).numpy()
         en32 = exact.residual_norm(e)
         fin = np.isfinite(en32)
+        assert np.array_equal(np.isposinf(gn), np.isposinf(en32)), f"{tag}: norm overflow rule"
         assert exact.ulp_distance_f32(gn[fin], en32[fin]).max(initial=0) <= 1, f"{tag}: norm vs exact"
         assert exact.ulp_distance_f32(gn[fin], r_nrm[:, h].reshape(-1).numpy()[fin]).max(initial=0) <= 2
     return n_mis_oracle

@@ -156,6 +156,19 @@ def test_norms_within_2ulp_of_exact():
     assert exact.ulp_distance_f32(ref, ex).max() <= 2
 
 
+def test_norm_overflow_rule_matches_torch():
+    # torch's fp32 vector_norm accumulates unscaled fp32 squares: beyond the
+    # fp32 range it returns inf, and exact.residual_norm encodes that rule.
+    e = torch.zeros(3, 128)
+    e[0, :2] = 1.5e19          # sum of squares 4.5e38 > fp32 max
+    e[1, :2] = 1.0e19          # 2e38 < fp32 max
+    e[2, 0] = 1e30
+    want = exact.residual_norm(e.numpy())
+    got = e.norm(dim=-1).numpy()
+    assert np.isinf(got[0]) and np.isinf(want[0]) and np.isinf(got[2]) and np.isinf(want[2])
+    assert exact.ulp_distance_f32(got[1:2], want[1:2]).max() <= 1
+
+
 def test_qjl_reduces_mse_by_5pct():
     # reference tests/unit/test_quant.py:308-322 (>= 5% MSE improvement)
     g = torch.Generator().manual_seed(1)
