@@ -167,7 +167,7 @@ def main() -> int:
                    "bytes_per_step": bytes_step, "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "omni::attn_kernel<128> (+ attn_combine_kernel<128> for split-K)",
+                     "kernel": "omni::attn_decode128_kernel (+ attn_combine_kernel<128> when split-K)",
                      "avg_call_us_events": round(ev_mean * 1e6, 2)},
     }
 

@@ -51,6 +51,7 @@ struct AttnArgs {
     int64_t causal_offset;     // < 0: no mask
     int q_dtype, per_head, Hq, Hkv, G, n_rchunks, splits, ncopy;
     int with_qjl, rotate_q;
+    int rows;                  // query rows per block (16: generic kernel, 8: D=128 decode kernel)
     float qscale;              // scale * log2(e)
     float alpha_c;             // fp32 sqrt(2/pi)/D (qscale is already folded into G q)
     float wht_scale;
@@ -397,19 +398,20 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
     const int64_t bz = blockIdx.z;
     const int64_t b = bz / a.n_rchunks;
     const int rc = (int)(bz % a.n_rchunks);
+    const int rows = a.rows;
     const int64_t unit = (b * a.Hkv + hk) * a.n_rchunks + rc;
     const int64_t nrows_total = a.T * a.G;
-    for (int s = threadIdx.x; s < kRows * D; s += blockDim.x) {
+    for (int s = threadIdx.x; s < rows * D; s += blockDim.x) {
         const int rr = s / D, d = s % D;
-        const int64_t rho = (int64_t)rc * kRows + rr;
+        const int64_t rho = (int64_t)rc * rows + rr;
         if (rho >= nrows_total) continue;
         float mx = -INFINITY;
         for (int sp = 0; sp < a.splits; ++sp)
-            mx = fmaxf(mx, a.ws[((unit * a.splits + sp) * kRows + rr) * (D + 2) + D]);
+            mx = fmaxf(mx, a.ws[((unit * a.splits + sp) * rows + rr) * (D + 2) + D]);
         const float mu = (mx == -INFINITY) ? 0.0f : mx;
         float lsum = 0.0f, osum = 0.0f;
         for (int sp = 0; sp < a.splits; ++sp) {
-            const float *wp = a.ws + ((unit * a.splits + sp) * kRows + rr) * (D + 2);
+            const float *wp = a.ws + ((unit * a.splits + sp) * rows + rr) * (D + 2);
             const float f = exp2f(wp[D] - mu);
             lsum = __builtin_fmaf(f, wp[D + 1], lsum);
             osum = __builtin_fmaf(f, wp[d], osum);
@@ -420,10 +422,443 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
     }
 }
 
+// ── D = 128 decode kernel ───────────────────────────────────────────────
+//
+// 32-token tiles per wave iteration; v_mfma_f32_16x16x32_f16 throughout.
+// Query rows (<= 8) sit in MFMA columns 0-7.
+//   K pass   A = K16 (16 tok x 256 slots): each cache byte's LUT entry
+//            (hi(c_even), hi(c_odd), lo(c_even), lo(c_odd)) fills four
+//            consecutive k-slots as loaded, so B repeats q over the hi and
+//            lo slots: columns 0-7 = Q_hi (both slots), columns 8-15 = Q_lo
+//            (hi slots only).  S_main(row n) = acc[n] + acc[n+8]
+//            = K_hi.Q_hi + K_lo.Q_hi + K_hi.Q_lo.
+//   QJL pass A = B+- (16 tok x 64), B = scale log2e G_h q in columns 0-7.
+//   score = S_main + alpha_t * qjl
+// One DPP row shift moves columns 8-15 onto 0-7.  PV contracts the 32
+// tokens of the tile: O^T (128 x 16) += V^T_hi . P^T + V^T_lo . P^T, plus a
+// ones row that accumulates the softmax denominator from the same fp16 P.
+//
+// LDS (static): [0, 64K)       byte LUT, 32 bank-private copies at a
+//                              256-byte stride, so one v_perm forms the
+//                              LDS address (byte << 8) | (lane % 32) * 8
+//               [64K, 68K)     sign byte -> eight +-1.0 halves
+//               [68K, 74K)     query rows and G q (prologue)
+constexpr int kDecRows = 8;
+constexpr int kDecWaves = 8;
+constexpr int kDecTile = 32;
+constexpr int kDecPrefetch = 3;      // tiles in flight per wave (ring depth)
+constexpr int kLutOff = 0;
+constexpr int kLutBytes = 256 * 256;
+constexpr int kSlutOff = kLutBytes;
+constexpr int kSlutBytes = 256 * 16;
+constexpr int kDecQsOff = kSlutOff + kSlutBytes;
+constexpr int kDecLdsBytes = kDecQsOff + kDecRows * (128 + 64) * 4;
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ half8_t as_half8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    uint4 t = make_uint4(a, b, c, d);
+    return __builtin_bit_cast(half8_t, t);
+}
+
+__device__ __forceinline__ half8_t pair_half8(uint2 x, uint2 y) {
+    return as_half8(x.x, x.y, y.x, y.y);
+}
+
+__device__ __forceinline__ float dpp_row_shl8(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x108, 0xf, 0xf, false));
+}
+
+// LDS byte offset of the LUT entry for byte k of w: (byte << 8) | copy offset.
+__device__ __forceinline__ uint32_t lut_addr(uint32_t w, uint32_t laneoff, int k) {
+    return __builtin_amdgcn_perm(w, laneoff, 0x0C0C0000u | ((uint32_t)(4 + k) << 8));
+}
+
+struct DecTileRaw {
+    uint4 k[2];        // K nibbles: token t0 + 16u + (lane % 16), bytes 16g .. 16g + 15
+    uint2 sg[2];       // sign rows of the same tokens
+    float nr[2][4];    // norms of output tokens t0 + 16u + 4g + i
+    uint32_t v[8];     // V dword (lane % 16) of tokens t0 + 16(i/4) + 4g + i%4
+};
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+constexpr int kBufWord3 = 0x00020000;   // raw buffer, gfx9 descriptor dword 3
+
+// Buffer descriptors over one (b, kv head) token stream, limited to the
+// split's end: reads past it return 0 (those tokens are masked anyway).
+struct DecBufs {
+    __amdgpu_buffer_rsrc_t kn, vn, kq, kr;
+};
+
+// Lane-constant byte offsets; the tile offset goes in the scalar offset and
+// the sub-tile / token steps in the instruction's immediate offset.
+struct DecOffsets {
+    uint32_t k, sg, nr, v;
+};
+
+template <bool QJL>
+__device__ __forceinline__ void dec_load(DecTileRaw &R, const DecBufs &P, const DecOffsets &O, int t0) {
+    const uint32_t t = (uint32_t)t0;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const u32x4_t kv4 = __builtin_amdgcn_raw_buffer_load_b128(P.kn, O.k + 1024u * u, t * 64u, 0);
+        R.k[u] = make_uint4(kv4.x, kv4.y, kv4.z, kv4.w);
+        if (QJL) {
+            const u32x2_t sv = __builtin_amdgcn_raw_buffer_load_b64(P.kq, O.sg + 128u * u, t * 8u, 0);
+            R.sg[u] = make_uint2(sv.x, sv.y);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                R.nr[u][i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(P.kr, O.nr + 4u * (16 * u + i), t * 4u, 0));
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        R.v[i] = __builtin_amdgcn_raw_buffer_load_b32(P.vn, O.v + 64u * (16 * (i / 4) + (i % 4)), t * 64u, 0);
+}
+
+__device__ __forceinline__ uint32_t cvt_pk_h2(float x, float y) {
+    typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+    typedef float f2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2_t){x, y}, h2_t));
+}
+
+// max over lanes {l, l^16, l^32, l^48} without LDS (v_permlane16/32_swap).
+__device__ __forceinline__ float max_over_groups(float m) {
+    auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    m = fmaxf(__uint_as_float(t[0]), __uint_as_float(t[1]));
+    auto u = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    return fmaxf(__uint_as_float(u[0]), __uint_as_float(u[1]));
+}
+
+template <bool QJL, int PF>
+__global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs a) {
+    constexpr int D = 128, QD = 64;
+    __shared__ __attribute__((aligned(16))) unsigned char smem[kDecLdsBytes];
+    float *qs = reinterpret_cast<float *>(smem + kDecQsOff);
+    float *gq = qs + kDecRows * D;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nw = blockDim.x >> 6;
+    const int split = blockIdx.x, hk = blockIdx.y;
+    const int64_t bz = blockIdx.z;
+    const int64_t b = bz / a.n_rchunks;
+    const int rc = (int)(bz % a.n_rchunks);
+    const int64_t nrows_total = a.T * a.G;
+    const int ncopy = a.ncopy;
+
+    // ── prologue: LUTs ────────────────────────────────────────────────
+    const float *cbp = a.codebooks + (a.per_head ? hk * 16 : 0);
+    float cbv[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) cbv[k] = cbp[k];          // uniform: scalar loads
+    for (int s = tid; s < 256 * ncopy; s += blockDim.x) {
+        const int e = s / ncopy, c = s % ncopy;
+        float c0 = cbv[0], c1 = cbv[0];
+#pragma unroll
+        for (int k = 1; k < 16; ++k) {
+            c0 = (e & 15) == k ? cbv[k] : c0;
+            c1 = (e >> 4) == k ? cbv[k] : c1;
+        }
+        const float h0 = f16_to_f32(f32_to_f16_rne(c0)), h1 = f16_to_f32(f32_to_f16_rne(c1));
+        *reinterpret_cast<uint2 *>(smem + kLutOff + e * 256 + c * 8) =
+            make_uint2(pack_h2(c0, c1), pack_h2(c0 - h0, c1 - h1));
+    }
+    for (int e = tid; e < 256; e += blockDim.x) {
+        uint32_t w[4];
+        for (int k = 0; k < 4; ++k)
+            w[k] = (((e >> (2 * k)) & 1) ? 0x3C00u : 0xBC00u) | ((((e >> (2 * k + 1)) & 1) ? 0x3C00u : 0xBC00u) << 16);
+        *reinterpret_cast<uint4 *>(smem + kSlutOff + e * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+    // ── prologue: query rows (row r <-> flat (t, gh) = rc*8 + r) ──────
+    for (int s = tid; s < kDecRows * D; s += blockDim.x) {
+        const int r = s / D, d = s % D;
+        const int64_t rho = (int64_t)rc * kDecRows + r;
+        float v = 0.0f;
+        if (rho < nrows_total) {
+            const int64_t t = rho / a.G;
+            const int hq = hk * a.G + (int)(rho % a.G);
+            v = load_as_f32(a.q, a.q_dtype, ((b * a.Hq + hq) * a.T + t) * D + d);
+            if (a.rotate_q && a.sign_flip && a.sign_flip[d] < 0) v = -v;
+        }
+        qs[s] = v;
+    }
+    __syncthreads();
+    if (a.rotate_q) {
+        // rotate_queries in-kernel, all threads: butterfly stages h = 1..64 in
+        // the reference order (hadamard.py:51-85), then scale and round.
+        for (int h = 1; h < D; h <<= 1) {
+            for (int pidx = tid; pidx < kDecRows * (D / 2); pidx += blockDim.x) {
+                const int r = pidx / (D / 2), k = pidx % (D / 2);
+                const int u = (k / h) * 2 * h + (k % h);
+                float *row = qs + r * D;
+                const float x0 = row[u], x1 = row[u + h];
+                row[u] = x0 + x1;
+                row[u + h] = x0 - x1;
+            }
+            __syncthreads();
+        }
+        for (int s = tid; s < kDecRows * D; s += blockDim.x) qs[s] = round_to_dtype(qs[s] * a.wht_scale, a.q_dtype);
+        __syncthreads();
+    }
+    if (QJL && wave == 0) {
+        // GQ (rows x 64) = Q (rows x 128) . G_h^T on MFMA: Q as fp16 hi + lo,
+        // G rows expanded 8 bits at a time through the sign LUT.
+        const int rr = lane & 15, gg = lane >> 4;
+        const uint32_t *gh = a.g_bits + (int64_t)hk * QD * 4;
+        half8_t ah[4], al[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            uint32_t hw[4], lw[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float v0 = rr < kDecRows ? qs[rr * D + 32 * s + 8 * gg + 2 * j] : 0.0f;
+                const float v1 = rr < kDecRows ? qs[rr * D + 32 * s + 8 * gg + 2 * j + 1] : 0.0f;
+                hw[j] = pack_h2(v0, v1);
+                lw[j] = pack_h2(v0 - f16_to_f32(f32_to_f16_rne(v0)), v1 - f16_to_f32(f32_to_f16_rne(v1)));
+            }
+            ah[s] = as_half8(hw[0], hw[1], hw[2], hw[3]);
+            al[s] = as_half8(lw[0], lw[1], lw[2], lw[3]);
+        }
+#pragma unroll
+        for (int cb = 0; cb < QD / 16; ++cb) {
+            float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
+            const int o = 16 * cb + rr;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const uint32_t byte = (gh[o * 4 + s] >> (8 * gg)) & 0xffu;
+                const uint4 gv = *reinterpret_cast<const uint4 *>(smem + kSlutOff + byte * 16u);
+                const half8_t bg = as_half8(gv.x, gv.y, gv.z, gv.w);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[s], bg, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[s], bg, acc, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (4 * gg + i < kDecRows) gq[(4 * gg + i) * QD + o] = acc[i];
+        }
+    }
+    __syncthreads();
+
+    // ── per-lane B operands ───────────────────────────────────────────
+    const int n = lane & 15, g = lane >> 4;
+    const bool lo_col = n >= kDecRows;           // columns 8-15
+    const int rn = lo_col ? n - kDecRows : n;
+    half8_t bk[8], bgq[2];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        // slots: [hi d0 d1 | lo d0 d1 | hi d2 d3 | lo d2 d3], d0 = 32g + 4s
+        const float *row = qs + rn * D + 32 * g + 4 * s;
+        float h[4], l[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            h[j] = row[j] * a.qscale;
+            l[j] = h[j] - f16_to_f32(f32_to_f16_rne(h[j]));
+        }
+        if (lo_col)
+            bk[s] = as_half8(pack_h2(l[0], l[1]), 0u, pack_h2(l[2], l[3]), 0u);
+        else
+            bk[s] = as_half8(pack_h2(h[0], h[1]), pack_h2(h[0], h[1]), pack_h2(h[2], h[3]), pack_h2(h[2], h[3]));
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float *row = gq + rn * QD + 32 * s + 8 * g + 2 * j;
+            w[j] = (!lo_col && QJL) ? pack_h2(row[0] * a.qscale, row[1] * a.qscale) : 0u;
+        }
+        bgq[s] = as_half8(w[0], w[1], w[2], w[3]);
+    }
+    const int64_t rho_n = (int64_t)rc * kDecRows + rn;
+    const int64_t key_limit64 = (a.causal_offset >= 0 && rho_n < nrows_total) ? a.causal_offset + rho_n / a.G
+                                                                               : INT64_MAX;
+
+    // ── main loop ─────────────────────────────────────────────────────
+    const int s_begin = split * (int)a.split_len;
+    const int s_end = (int)imin64(a.S, (int64_t)s_begin + a.split_len);
+    const int key_limit = (int)imin64(key_limit64, (int64_t)0x7fffffff);
+    // tiles ending at or below min(s_end, first masked key of any row) need no masks
+    const int64_t min_limit64 = (a.causal_offset >= 0) ? a.causal_offset + ((int64_t)rc * kDecRows) / a.G : INT64_MAX;
+    const int full_end = (int)imin64((int64_t)s_end, min_limit64 + 1);
+    const int64_t kv_base = (b * a.Hkv + hk) * a.S;
+    DecBufs P;
+    P.kn = __builtin_amdgcn_make_buffer_rsrc((void *)(a.k_nib + kv_base * 64), (short)0, s_end * 64, kBufWord3);
+    P.vn = __builtin_amdgcn_make_buffer_rsrc((void *)(a.v_nib + kv_base * 64), (short)0, s_end * 64, kBufWord3);
+    P.kq = __builtin_amdgcn_make_buffer_rsrc((void *)(QJL ? a.k_qjl + kv_base * 8 : a.k_nib), (short)0,
+                                             QJL ? s_end * 8 : 0, kBufWord3);
+    P.kr = __builtin_amdgcn_make_buffer_rsrc((void *)(QJL ? a.k_norms + kv_base : (const float *)a.k_nib), (short)0,
+                                             QJL ? s_end * 4 : 0, kBufWord3);
+    DecOffsets OFS;
+    OFS.k = (uint32_t)n * 64u + 16u * g;
+    OFS.sg = (uint32_t)n * 8u;
+    OFS.nr = 16u * g;
+    OFS.v = 256u * g + 4u * n;
+    const uint32_t laneoff = (uint32_t)(lane & (ncopy - 1)) * 8u;
+    // ones on the hi slots of each (hi, lo) pair: sums every token's P once
+    const half8_t ones = as_half8(0x3C003C00u, 0u, 0x3C003C00u, 0u);
+    const unsigned char *lut = smem + kLutOff;
+
+    float4_t oacc[8], lacc_sum;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) oacc[k] = float4_t{0.f, 0.f, 0.f, 0.f};
+    lacc_sum = float4_t{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY;
+
+    const int stride = nw * kDecTile;
+    DecTileRaw ring[PF];
+#pragma unroll
+    for (int p = 0; p < PF - 1; ++p) {
+        const int tp = s_begin + wave * kDecTile + p * stride;
+        if (tp < s_end) dec_load<QJL>(ring[p], P, OFS, tp);
+    }
+    for (int base = s_begin + wave * kDecTile; base < s_end; base += PF * stride) {
+#pragma unroll
+        for (int p = 0; p < PF; ++p) {
+            const int tt = base + p * stride;
+            if (tt >= s_end) break;
+            const int tpre = tt + (PF - 1) * stride;
+            if (tpre < s_end) dec_load<QJL>(ring[(p + PF - 1) % PF], P, OFS, tpre);
+            DecTileRaw &R = ring[p];
+            const bool full = tt + kDecTile <= full_end;
+
+            // scores: lane (n, g) holds tokens tt + 16u + 4g + i
+            float sc[8];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f}, qacc = float4_t{0.f, 0.f, 0.f, 0.f};
+                const uint32_t kw[4] = {R.k[u].x, R.k[u].y, R.k[u].z, R.k[u].w};
+#pragma unroll
+                for (int s = 0; s < 8; ++s) {
+                    const uint2 e0 = *reinterpret_cast<const uint2 *>(lut + lut_addr(kw[s >> 1], laneoff, 2 * (s & 1)));
+                    const uint2 e1 = *reinterpret_cast<const uint2 *>(lut + lut_addr(kw[s >> 1], laneoff, 2 * (s & 1) + 1));
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pair_half8(e0, e1), bk[s], acc, 0, 0, 0);
+                }
+                if (QJL) {
+#pragma unroll
+                    for (int s = 0; s < 2; ++s) {
+                        const uint32_t byte = ((s ? R.sg[u].y : R.sg[u].x) >> (8 * g)) & 0xffu;
+                        const uint4 sv = *reinterpret_cast<const uint4 *>(smem + kSlutOff + byte * 16u);
+                        qacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(sv.x, sv.y, sv.z, sv.w), bgq[s], qacc, 0, 0, 0);
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float v = acc[i] + dpp_row_shl8(acc[i]);
+                    if (QJL) v = __builtin_fmaf(R.nr[u][i] * a.alpha_c, qacc[i], v);
+                    sc[4 * u + i] = lo_col ? -INFINITY : v;
+                }
+            }
+            if (!full) {
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int tn = tt + 16 * u + 4 * g + i;
+                        if (tn >= s_end || tn > key_limit) sc[4 * u + i] = -INFINITY;
+                    }
+            }
+
+            // online softmax (exp2 domain), lazy rescale
+            float mt = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+            mt = max_over_groups(mt);
+            const bool need = mt > m_run + 8.0f;
+            if (__builtin_amdgcn_ballot_w64(need)) {
+                const float f = need ? __builtin_amdgcn_exp2f(m_run - mt) : 1.0f;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) oacc[k] *= f;
+                lacc_sum *= f;
+                m_run = need ? mt : m_run;
+            }
+            const float m_use = (m_run == -INFINITY) ? 0.0f : m_run;
+            half8_t pb[2];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const uint32_t p01 = cvt_pk_h2(__builtin_amdgcn_exp2f(sc[4 * u] - m_use), __builtin_amdgcn_exp2f(sc[4 * u + 1] - m_use));
+                const uint32_t p23 = cvt_pk_h2(__builtin_amdgcn_exp2f(sc[4 * u + 2] - m_use), __builtin_amdgcn_exp2f(sc[4 * u + 3] - m_use));
+                pb[u] = as_half8(p01, p01, p23, p23);
+                lacc_sum = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb[u], lacc_sum, 0, 0, 0);
+            }
+
+            // PV: pair bytes interleave the nibbles of two tokens at one d, so
+            // each LUT entry is an MFMA-ready (hi pair, lo pair) for that d.
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                uint32_t ev[2], od[2];
+#pragma unroll
+                for (int pr = 0; pr < 2; ++pr) {
+                    const uint32_t va = R.v[4 * u + 2 * pr], vb = R.v[4 * u + 2 * pr + 1];
+                    ev[pr] = (va & 0x0F0F0F0Fu) | ((vb & 0x0F0F0F0Fu) << 4);
+                    od[pr] = ((va >> 4) & 0x0F0F0F0Fu) | (vb & 0xF0F0F0F0u);
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint2 e0 = *reinterpret_cast<const uint2 *>(lut + lut_addr(ev[0], laneoff, j));
+                    const uint2 e1 = *reinterpret_cast<const uint2 *>(lut + lut_addr(ev[1], laneoff, j));
+                    oacc[2 * j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pair_half8(e0, e1), pb[u], oacc[2 * j], 0, 0, 0);
+                    const uint2 f0 = *reinterpret_cast<const uint2 *>(lut + lut_addr(od[0], laneoff, j));
+                    const uint2 f1 = *reinterpret_cast<const uint2 *>(lut + lut_addr(od[1], laneoff, j));
+                    oacc[2 * j + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pair_half8(f0, f1), pb[u], oacc[2 * j + 1], 0, 0, 0);
+                }
+            }
+        }
+    }
+
+    // ── combine waves (deterministic order) ──────────────────────────
+    __syncthreads();   // LUTs are dead from here on
+    float *wm = reinterpret_cast<float *>(smem);
+    float *wl = wm + kDecWaves * kDecRows;
+    float *ob = wl + kDecWaves * kDecRows;          // [kDecRows][D]
+    if (g == 0 && !lo_col) {
+        wm[wave * kDecRows + n] = m_run;
+        wl[wave * kDecRows + n] = lacc_sum[0];
+    }
+    __syncthreads();
+    float mx = -INFINITY;
+    for (int w = 0; w < nw; ++w) mx = fmaxf(mx, wm[w * kDecRows + rn]);
+    const float mu = (mx == -INFINITY) ? 0.0f : mx;
+    const float fw = exp2f(m_run - mu);
+    for (int w = 0; w < nw; ++w) {
+        if (wave == w && !lo_col) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float *dst = ob + n * D + 8 * (4 * g + i) + k;
+                    const float v = oacc[k][i] * fw;
+                    *dst = (w == 0) ? v : (*dst + v);
+                }
+        }
+        __syncthreads();
+    }
+    const int64_t unit = (b * a.Hkv + hk) * a.n_rchunks + rc;
+    for (int s = tid; s < kDecRows * D; s += blockDim.x) {
+        const int rr = s / D, d = s % D;
+        const int64_t rr_rho = (int64_t)rc * kDecRows + rr;
+        if (rr_rho >= nrows_total) continue;
+        float rmx = -INFINITY;
+        for (int w = 0; w < nw; ++w) rmx = fmaxf(rmx, wm[w * kDecRows + rr]);
+        const float rmu = (rmx == -INFINITY) ? 0.0f : rmx;
+        float lsum = 0.0f;
+        for (int w = 0; w < nw; ++w) lsum = __builtin_fmaf(exp2f(wm[w * kDecRows + rr] - rmu), wl[w * kDecRows + rr], lsum);
+        const float osum = ob[rr * D + d];
+        if (a.splits == 1) {
+            const int64_t t = rr_rho / a.G;
+            const int hq = hk * a.G + (int)(rr_rho % a.G);
+            a.out[((b * a.Hq + hq) * a.T + t) * D + d] = osum / lsum;
+        } else {
+            float *wp = a.ws + ((unit * a.splits + split) * kDecRows + rr) * (D + 2);
+            wp[d] = osum;
+            if (d == 0) { wp[D] = rmx; wp[D + 1] = lsum; }
+        }
+    }
+}
+
 // ── launch planning ─────────────────────────────────────────────────────
 
 struct Plan {
-    int n_rchunks, splits, nw, ncopy;
+    bool dec128;       // D == 128: decode kernel with 8 query rows per block
+    int rows, n_rchunks, splits, nw, ncopy;
     int64_t split_len;
     size_t lds, ws_bytes;
 };
@@ -440,25 +875,37 @@ static int device_cus() {
     return cached[dev];
 }
 
+static int64_t clamp64(int64_t v, int64_t lo, int64_t hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
 static Plan make_plan(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int D) {
     Plan p;
     const int G = Hq / Hkv;
-    p.n_rchunks = (int)((T * G + kRows - 1) / kRows);
-    const int64_t units = B * (int64_t)Hkv * p.n_rchunks;
-    const int64_t tiles = (S + kTile - 1) / kTile;
     const int cus = device_cus();
-    int64_t splits = (2 * (int64_t)cus + units - 1) / (units > 0 ? units : 1);
-    const int64_t max_splits = tiles / (2 * kMaxWaves) > 1 ? tiles / (2 * kMaxWaves) : 1;
-    if (splits > max_splits) splits = max_splits;
-    if (splits < 1) splits = 1;
-    const int64_t tiles_per_split = (tiles + splits - 1) / splits;
-    p.splits = (int)splits;
-    p.split_len = tiles_per_split * kTile;
-    int nw = (int)((tiles_per_split + 1) / 2);
-    p.nw = nw < 1 ? 1 : (nw > kMaxWaves ? kMaxWaves : nw);
-    p.ncopy = tiles_per_split >= 64 ? 16 : (tiles_per_split >= 8 ? 4 : 1);
-    p.lds = D == 128 ? Lds<128>::total(p.ncopy, p.nw) : Lds<32>::total(p.ncopy, p.nw);
-    p.ws_bytes = p.splits > 1 ? (size_t)units * p.splits * kRows * (D + 2) * sizeof(float) : 0;
+    p.dec128 = (D == 128);
+    p.rows = p.dec128 ? kDecRows : kRows;
+    p.n_rchunks = (int)((T * G + p.rows - 1) / p.rows);
+    const int64_t units = B * (int64_t)Hkv * p.n_rchunks;
+    if (p.dec128) {
+        const int64_t tiles = (S + kDecTile - 1) / kDecTile;
+        int64_t splits = clamp64((cus + units - 1) / (units > 0 ? units : 1), 1, (tiles / 16) > 1 ? tiles / 16 : 1);
+        const int64_t tps = (tiles + splits - 1) / splits;
+        p.splits = (int)splits;
+        p.split_len = tps * kDecTile;
+        p.nw = (int)clamp64(tps / 2, 1, kDecWaves);
+        p.ncopy = tps >= 32 ? 32 : (tps >= 8 ? 8 : 1);
+        p.lds = kDecLdsBytes;
+    } else {
+        const int64_t tiles = (S + kTile - 1) / kTile;
+        int64_t splits = clamp64((2 * (int64_t)cus + units - 1) / (units > 0 ? units : 1), 1,
+                                 tiles / (2 * kMaxWaves) > 1 ? tiles / (2 * kMaxWaves) : 1);
+        const int64_t tps = (tiles + splits - 1) / splits;
+        p.splits = (int)splits;
+        p.split_len = tps * kTile;
+        p.nw = (int)clamp64((tps + 1) / 2, 1, kMaxWaves);
+        p.ncopy = tps >= 64 ? 16 : (tps >= 8 ? 4 : 1);
+        p.lds = D == 128 ? Lds<128>::total(p.ncopy, p.nw) : Lds<32>::total(p.ncopy, p.nw);
+    }
+    p.ws_bytes = p.splits > 1 ? (size_t)units * p.splits * p.rows * (D + 2) * sizeof(float) : 0;
     return p;
 }
 
@@ -486,6 +933,7 @@ extern "C" int omni_attn(const void *q, int q_dtype, const uint8_t *k_nib, const
     OMNI_CHECK_ARG(q && k_nib && v_nib && codebooks && out, "omni_attn: NULL pointer");
     OMNI_CHECK_ARG(!with_qjl || (k_qjl && k_norms && g_bits), "omni_attn: NULL QJL pointer");
     OMNI_CHECK_ARG(isfinite(scale), "omni_attn: scale must be finite");
+    OMNI_CHECK_ARG(S < (int64_t(1) << 26), "omni_attn: S must be < 2^26 tokens per sequence");
     Plan p = make_plan(B, Hq, Hkv, T, S, head_dim);
     OMNI_CHECK_ARG(Hkv <= 65535 && B * p.n_rchunks <= 2147483647LL && p.splits <= 2147483647,
                    "omni_attn: grid too large");
@@ -499,7 +947,7 @@ extern "C" int omni_attn(const void *q, int q_dtype, const uint8_t *k_nib, const
     a.ws = reinterpret_cast<float *>(workspace);
     a.T = T; a.S = S; a.split_len = p.split_len; a.causal_offset = causal_offset;
     a.q_dtype = q_dtype; a.per_head = per_head_codebook; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv;
-    a.n_rchunks = p.n_rchunks; a.splits = p.splits; a.ncopy = p.ncopy;
+    a.n_rchunks = p.n_rchunks; a.splits = p.splits; a.ncopy = p.ncopy; a.rows = p.rows;
     a.with_qjl = with_qjl; a.rotate_q = rotate_q;
     const double log2e = 1.4426950408889634;
     a.qscale = (float)((double)scale * log2e);
@@ -507,10 +955,14 @@ extern "C" int omni_attn(const void *q, int q_dtype, const uint8_t *k_nib, const
     a.wht_scale = inv_sqrt_dim_f32(head_dim);
     dim3 grid((unsigned)p.splits, (unsigned)Hkv, (unsigned)(B * p.n_rchunks));
     dim3 block(64 * p.nw);
-    if (head_dim == 128)
-        hipLaunchKernelGGL(attn_kernel<128>, grid, block, p.lds, as_stream(stream), a);
-    else
+    if (p.dec128) {
+        if (with_qjl)
+            hipLaunchKernelGGL((attn_decode128_kernel<true, kDecPrefetch>), grid, block, 0, as_stream(stream), a);
+        else
+            hipLaunchKernelGGL((attn_decode128_kernel<false, kDecPrefetch>), grid, block, 0, as_stream(stream), a);
+    } else {
         hipLaunchKernelGGL(attn_kernel<32>, grid, block, p.lds, as_stream(stream), a);
+    }
     OMNI_CHECK_LAUNCH("omni_attn");
     if (p.splits > 1) {
         dim3 g2(1, (unsigned)Hkv, (unsigned)(B * p.n_rchunks));
