@@ -36,6 +36,14 @@ for _p in (os.path.join(ROOT, "omnistack-rs_amd"), ROOT):
 HBM_PEAK_GBS = 8000.0
 BYTES_PER_TOKEN_HEAD = 64 + 8 + 4 + 64     # K nibbles + K signs + K norm (f32) + V nibbles
 
+# HBM traffic of one C3 decode launch, from two `rocprofv3 --pmc` passes
+# (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch) over this script, each
+# scaled by what the counter reads for the 256 MiB calibration copy below
+# (FETCH_SIZE reads half the copied bytes -> x2.0; WRITE_SIZE reads them
+# exactly -> x1.0).  Recorded in profiles/attn_decode128_c3.md; re-measure
+# after any change to the decode kernel.
+C3_TRAFFIC = {"fetch_kib": 143686.5, "fetch_scale": 2.0, "write_kib": 512.0, "write_scale": 1.0}
+
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
@@ -128,6 +136,16 @@ def main() -> int:
     props = torch.cuda.get_device_properties(dev)
     log(f"[bench] device {props.name} CUs={props.multi_processor_count}")
 
+    # Calibration copy of a known size: under `rocprofv3 --pmc FETCH_SIZE` /
+    # `WRITE_SIZE` its dispatch gives the counters' scale (bytes read and
+    # written should both equal COPY_BYTES).
+    COPY_BYTES = 256 << 20
+    cbuf = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev)
+    cbuf2 = torch.empty_like(cbuf)
+    cbuf2.copy_(cbuf)
+    torch.cuda.synchronize()
+    del cbuf, cbuf2
+
     uid, D = 42, 128
     sign = (torch.randint(0, 2, (D,), generator=torch.Generator().manual_seed(7)) * 2 - 1).to(torch.int8).to(dev)
     cb1 = calibrate_codebook(torch.randn(1 << 16, generator=torch.Generator().manual_seed(11)), max_iters=100)
@@ -149,6 +167,8 @@ def main() -> int:
     log(f"[bench] C3: {t_step * 1e6:.1f} us/step wall, {ev_mean * 1e6:.1f} us/call events -> "
         f"{value:.0f} GB/s ({value / HBM_PEAK_GBS:.1%} of peak)")
 
+    c3_traffic = round(1024 * (C3_TRAFFIC["fetch_kib"] * C3_TRAFFIC["fetch_scale"]
+                                + C3_TRAFFIC["write_kib"] * C3_TRAFFIC["write_scale"]))
     result = {
         "metric": "compressed-KV decode attn HBM GB/s (% peak) @8K ctx; users/sec @B=64,L=50",
         "value": round(value, 1),
@@ -166,7 +186,7 @@ def main() -> int:
                                "INT4 Lloyd-Max + 1-bit QJL K, INT4 V, bf16 query, rotate_q in-kernel",
                    "bytes_per_step": bytes_step, "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": c3_traffic,
                      "kernel": "omni::attn_decode128_kernel (+ attn_combine_kernel<128> when split-K)",
                      "avg_call_us_events": round(ev_mean * 1e6, 2)},
     }

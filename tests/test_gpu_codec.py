@@ -7,7 +7,9 @@ oracle.restate on the same seeded inputs.  Sign bits must equal the exact
 where |P|/||e|| < 1e-6 (boundary rule); norms must be within 1 ulp of the
 correctly rounded fp64 norm and 2 ulp of the oracle's fp32 torch norm.
 """
+import json
 import math
+import os
 
 import numpy as np
 import pytest
@@ -205,3 +207,40 @@ def test_rows_api_matches_oracle(device):
     out = dequantize_rows(nib, qjl, nrm, cb.to(device), base_head_idx=3, user_id=11).cpu()
     want = restate.dequantize_rows(nib.cpu(), qjl.cpu(), nrm.cpu(), cb, base_head_idx=3, user_id=11)
     assert (out - want).abs().max().item() < 1e-6
+
+
+def test_known_answers_through_the_kernels(device):
+    """The reference's known packing answers (tests/golden/known_answers.json)
+    through the GPU encoder and dequantizer: inputs equal to centroids give
+    those codes, and the packed bytes decode to the listed codes."""
+    from omnistack_rs.kernels.quantize import dequantize_heads, quantize_heads
+    with open(os.path.join(os.path.dirname(__file__), "golden", "known_answers.json")) as f:
+        ka = json.load(f)
+    cb = torch.linspace(-2.0, 2.0, 16)
+    for case in ka["pack"]:
+        codes = torch.zeros(128, dtype=torch.long)
+        if "codes_prefix" in case:
+            codes[:len(case["codes_prefix"])] = torch.tensor(case["codes_prefix"])
+        else:
+            codes[:] = case["codes_all"]
+        x = cb[codes].reshape(1, 1, 1, 128)
+        nib, qjl, nrm = quantize_heads(x.to(device), cb.to(device), user_id=3)
+        nib, qjl, nrm = nib.cpu(), qjl.cpu(), nrm.cpu()
+        if "byte0" in case:
+            assert nib[0, 0, 0, 0].item() == case["byte0"]
+        else:
+            assert (nib == case["bytes_all"]).all()
+        assert nrm.item() == 0.0 and (qjl == 0xFF).all()   # zero residual: every P = 0 >= 0
+    for case in ka["unpack"]:
+        packed = torch.zeros(1, 1, 1, 64, dtype=torch.uint8)
+        if "bytes_prefix" in case:
+            packed[..., :len(case["bytes_prefix"])] = torch.tensor(case["bytes_prefix"], dtype=torch.uint8)
+            want = cb[torch.tensor(case["codes_prefix"])]
+            n = len(case["codes_prefix"])
+        else:
+            packed[:] = case["bytes_all"]
+            want = cb[torch.full((128,), case["codes_all"])]
+            n = 128
+        out = dequantize_heads(packed.to(device), torch.zeros(1, 1, 1, 8, dtype=torch.uint8, device=device),
+                               torch.zeros(1, 1, 1, device=device), cb.to(device), with_qjl=False).cpu()
+        assert torch.equal(out[0, 0, 0, :n], want)

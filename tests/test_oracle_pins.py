@@ -7,7 +7,9 @@ test_hadamard.py of deepsheth3/Omnistack-RS), the textbook MT19937, the
 Sylvester Hadamard matrix, explicit first-index argmin, fp64 projections,
 fp64 brute-force softmax, and closed forms.
 """
+import json
 import math
+import os
 
 import numpy as np
 import pytest
@@ -16,13 +18,17 @@ import torch
 
 from oracle import exact, mt19937, restate
 
+with open(os.path.join(os.path.dirname(__file__), "golden", "known_answers.json")) as _f:
+    KA = json.load(_f)
+
 
 # ── MT19937 / G ─────────────────────────────────────────────────────────
 
 def test_mt19937_cpp_standard_value():
     # C++ [rand.predef]: the 10000th invocation of a default-constructed
     # std::mt19937 (seed 5489) produces 4123659995.
-    assert int(mt19937.raw(5489, 10000)[-1]) == 4123659995
+    m = KA["mt19937"]
+    assert int(mt19937.raw(m["seed"], m["draw"])[-1]) == m["value"] == 4123659995
 
 
 @pytest.mark.parametrize("seed", [0, 1, 7, 42, 45, 999, 1023, 42 ^ 7, 2047])
@@ -37,6 +43,8 @@ def test_qjl_g_head_dim_32():
 
 def test_seed_table():
     # reference tests/unit/test_quant.py:604-609 and :626-632
+    for uid, row, want in KA["seed"]["cases"]:
+        assert restate.make_qjl_seed(uid, row) == want
     assert restate.make_qjl_seed(0, 7) == 0 ^ 7
     assert restate.make_qjl_seed(1, 7) == 1 ^ 7
     assert restate.make_qjl_seed(1024, 7) == 0 ^ 7
@@ -58,7 +66,7 @@ def test_wht_matches_sylvester_matrix():
 def test_wht_h4_known_answer():
     # reference tests/unit/test_hadamard.py:166-188: H4 [1,2,3,4] / 2 = [5,-1,-2,0]
     H4 = scipy.linalg.hadamard(4)
-    assert np.allclose(H4 @ np.array([1.0, 2, 3, 4]) / 2.0, [5, -1, -2, 0])
+    assert np.allclose(H4 @ np.array(KA["wht4"]["x"]) / 2.0, KA["wht4"]["y"])
     # the same butterfly order on 128 dims restricted to an embedded 4-vector
     x = torch.zeros(128)
     x[:4] = torch.tensor([1.0, 2, 3, 4])
@@ -103,6 +111,25 @@ def test_quantize_int4_nan_codebook_entry():
     codes, _ = restate.quantize_int4(torch.from_numpy(x), torch.from_numpy(cb))
     assert np.array_equal(codes.numpy(), exact.argmin_first(x, cb))
     assert (codes.numpy() == 3).all()            # torch.argmin: NaN is the minimum
+
+
+def test_pack_known_answers_fixture():
+    for case in KA["pack"]:
+        codes = torch.zeros(1, 128, dtype=torch.uint8)
+        if "codes_prefix" in case:
+            codes[0, :len(case["codes_prefix"])] = torch.tensor(case["codes_prefix"], dtype=torch.uint8)
+            assert restate.pack_nibbles(codes)[0, 0].item() == case["byte0"]
+        else:
+            codes[:] = case["codes_all"]
+            assert (restate.pack_nibbles(codes) == case["bytes_all"]).all()
+    for case in KA["unpack"]:
+        packed = torch.zeros(1, 64, dtype=torch.uint8)
+        if "bytes_prefix" in case:
+            packed[0, :len(case["bytes_prefix"])] = torch.tensor(case["bytes_prefix"], dtype=torch.uint8)
+            assert restate.unpack_nibbles(packed)[0, :8].tolist() == case["codes_prefix"]
+        else:
+            packed[:] = case["bytes_all"]
+            assert (restate.unpack_nibbles(packed) == case["codes_all"]).all()
 
 
 def test_pack_known_answers():
