@@ -58,6 +58,7 @@ struct AttnArgs {
 };
 
 __device__ __forceinline__ int64_t imin64(int64_t x, int64_t y) { return x < y ? x : y; }
+__device__ __forceinline__ int imin(int x, int y) { return x < y ? x : y; }
 
 __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
     return (uint32_t)f32_to_f16_rne(a) | ((uint32_t)f32_to_f16_rne(b) << 16);
@@ -443,6 +444,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
 //                              LDS address (byte << 8) | (lane % 32) * 8
 //               [64K, 68K)     sign byte -> eight +-1.0 halves
 //               [68K, 74K)     query rows and G q (prologue)
+//               [74K, +64)     codebook as (fp16 hi, fp16 remainder) pairs
 constexpr int kDecRows = 8;
 constexpr int kDecWaves = 8;
 constexpr int kDecTile = 32;
@@ -452,7 +454,13 @@ constexpr int kLutBytes = 256 * 256;
 constexpr int kSlutOff = kLutBytes;
 constexpr int kSlutBytes = 256 * 16;
 constexpr int kDecQsOff = kSlutOff + kSlutBytes;
-constexpr int kDecLdsBytes = kDecQsOff + kDecRows * (128 + 64) * 4;
+constexpr int kDecCbOff = kDecQsOff + kDecRows * (128 + 64) * 4;
+constexpr int kDecLdsBytes = kDecCbOff + 16 * 4;
+// epilogue reuse of [0, 68K): per-wave O slabs (rows padded to 132 floats),
+// then per-wave running max and denominator
+constexpr int kObStride = 128 + 4;
+constexpr int kDecSlabBytes = kDecWaves * kDecRows * kObStride * 4;
+static_assert(kDecSlabBytes + 2 * kDecWaves * kDecRows * 4 <= kDecQsOff, "epilogue slabs overlap the query rows");
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 
@@ -491,30 +499,33 @@ struct DecBufs {
     __amdgpu_buffer_rsrc_t kn, vn, kq, kr;
 };
 
-// Lane-constant byte offsets; the tile offset goes in the scalar offset and
-// the sub-tile / token steps in the instruction's immediate offset.
+// Lane-constant byte offsets; the tile offset is added per tile and the
+// sub-tile / token steps go in the instruction's immediate offset.
 struct DecOffsets {
     uint32_t k, sg, nr, v;
 };
 
 template <bool QJL>
 __device__ __forceinline__ void dec_load(DecTileRaw &R, const DecBufs &P, const DecOffsets &O, int t0) {
+    // The tile offset goes into the per-lane offset, which the buffer range
+    // check covers: tiles past the split end read as 0 and touch no memory.
     const uint32_t t = (uint32_t)t0;
+    const uint32_t vk = O.k + t * 64u, vsg = O.sg + t * 8u, vnr = O.nr + t * 4u, vv = O.v + t * 64u;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-        const u32x4_t kv4 = __builtin_amdgcn_raw_buffer_load_b128(P.kn, O.k + 1024u * u, t * 64u, 0);
+        const u32x4_t kv4 = __builtin_amdgcn_raw_buffer_load_b128(P.kn, vk + 1024u * u, 0, 0);
         R.k[u] = make_uint4(kv4.x, kv4.y, kv4.z, kv4.w);
         if (QJL) {
-            const u32x2_t sv = __builtin_amdgcn_raw_buffer_load_b64(P.kq, O.sg + 128u * u, t * 8u, 0);
+            const u32x2_t sv = __builtin_amdgcn_raw_buffer_load_b64(P.kq, vsg + 128u * u, 0, 0);
             R.sg[u] = make_uint2(sv.x, sv.y);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                R.nr[u][i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(P.kr, O.nr + 4u * (16 * u + i), t * 4u, 0));
+                R.nr[u][i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(P.kr, vnr + 4u * (16 * u + i), 0, 0));
         }
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i)
-        R.v[i] = __builtin_amdgcn_raw_buffer_load_b32(P.vn, O.v + 64u * (16 * (i / 4) + (i % 4)), t * 64u, 0);
+        R.v[i] = __builtin_amdgcn_raw_buffer_load_b32(P.vn, vv + 64u * (16 * (i / 4) + (i % 4)), 0, 0);
 }
 
 __device__ __forceinline__ uint32_t cvt_pk_h2(float x, float y) {
@@ -531,12 +542,30 @@ __device__ __forceinline__ float max_over_groups(float m) {
     return fmaxf(__uint_as_float(u[0]), __uint_as_float(u[1]));
 }
 
+// One lane per (d, d + 64) of a 128-wide row: the normalized WHT of
+// _wht_torch (hadamard.py:51-85).  Stage h pairs element u (bit h clear)
+// with u + h: u <- x[u] + x[u+h], u + h <- x[u] - x[u+h], all fp32; stages
+// h = 1..32 cross lanes, h = 64 pairs the two values of a lane.
+__device__ __forceinline__ void wht128_lanes(float &lo, float &hi, int lane) {
+#pragma unroll
+    for (int h = 1; h < 64; h <<= 1) {
+        const float plo = __shfl_xor(lo, h), phi = __shfl_xor(hi, h);
+        const bool upper = (lane & h) != 0;
+        lo = upper ? plo - lo : lo + plo;
+        hi = upper ? phi - hi : hi + phi;
+    }
+    const float a = lo, b = hi;
+    lo = a + b;
+    hi = a - b;
+}
+
 template <bool QJL, int PF>
 __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs a) {
     constexpr int D = 128, QD = 64;
     __shared__ __attribute__((aligned(16))) unsigned char smem[kDecLdsBytes];
     float *qs = reinterpret_cast<float *>(smem + kDecQsOff);
     float *gq = qs + kDecRows * D;
+    uint32_t *cbh = reinterpret_cast<uint32_t *>(smem + kDecCbOff);
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -545,89 +574,156 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     const int64_t bz = blockIdx.z;
     const int64_t b = bz / a.n_rchunks;
     const int rc = (int)(bz % a.n_rchunks);
-    const int64_t nrows_total = a.T * a.G;
+    const int nrows_total = (int)(a.T * a.G);
     const int ncopy = a.ncopy;
+    const int n = lane & 15, g = lane >> 4;
 
-    // ── prologue: LUTs ────────────────────────────────────────────────
+    // ── cache stream descriptors ──────────────────────────────────────
+    const int s_begin = split * (int)a.split_len;
+    const int s_end = (int)imin64(a.S, (int64_t)s_begin + a.split_len);
+    const int64_t kv_base = (b * a.Hkv + hk) * a.S;
+    DecBufs P;
+    P.kn = __builtin_amdgcn_make_buffer_rsrc((void *)(a.k_nib + kv_base * 64), (short)0, s_end * 64, kBufWord3);
+    P.vn = __builtin_amdgcn_make_buffer_rsrc((void *)(a.v_nib + kv_base * 64), (short)0, s_end * 64, kBufWord3);
+    P.kq = __builtin_amdgcn_make_buffer_rsrc((void *)(QJL ? a.k_qjl + kv_base * 8 : a.k_nib), (short)0,
+                                             QJL ? s_end * 8 : 0, kBufWord3);
+    P.kr = __builtin_amdgcn_make_buffer_rsrc((void *)(QJL ? a.k_norms + kv_base : (const float *)a.k_nib), (short)0,
+                                             QJL ? s_end * 4 : 0, kBufWord3);
+    DecOffsets OFS;
+    OFS.k = (uint32_t)n * 64u + 16u * g;
+    OFS.sg = (uint32_t)n * 8u;
+    OFS.nr = 16u * g;
+    OFS.v = 256u * g + 4u * n;
+
+    // ── prologue loads (issued before the cache prefetch so that waiting
+    //    for them does not wait for the cache) ────────────────────────
     const float *cbp = a.codebooks + (a.per_head ? hk * 16 : 0);
-    float cbv[16];
+    const float cb_mine = tid < 16 ? cbp[tid] : 0.0f;
+    // query row r <-> flat (t, g) = rc * 8 + r; each wave takes rows
+    // wave, wave + nw, ... (raw bits now, converted after the prefetch)
+    const bool q32 = a.q_dtype == OMNI_F32;
+    uint32_t qraw[kDecRows][2];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) cbv[k] = cbp[k];          // uniform: scalar loads
-    for (int s = tid; s < 256 * ncopy; s += blockDim.x) {
-        const int e = s / ncopy, c = s % ncopy;
-        float c0 = cbv[0], c1 = cbv[0];
-#pragma unroll
-        for (int k = 1; k < 16; ++k) {
-            c0 = (e & 15) == k ? cbv[k] : c0;
-            c1 = (e >> 4) == k ? cbv[k] : c1;
+    for (int i = 0; i < kDecRows; ++i) {
+        qraw[i][0] = qraw[i][1] = 0u;
+        if (i * nw >= kDecRows) break;
+        const int rho = imin(rc * kDecRows + wave + i * nw, nrows_total - 1);
+        const int t = rho / a.G;
+        const int hq = hk * a.G + (rho - t * a.G);
+        const int64_t base = ((b * a.Hq + hq) * a.T + t) * D;
+        if (q32) {
+            qraw[i][0] = reinterpret_cast<const uint32_t *>(a.q)[base + lane];
+            qraw[i][1] = reinterpret_cast<const uint32_t *>(a.q)[base + 64 + lane];
+        } else {
+            qraw[i][0] = reinterpret_cast<const uint16_t *>(a.q)[base + lane];
+            qraw[i][1] = reinterpret_cast<const uint16_t *>(a.q)[base + 64 + lane];
         }
-        const float h0 = f16_to_f32(f32_to_f16_rne(c0)), h1 = f16_to_f32(f32_to_f16_rne(c1));
-        *reinterpret_cast<uint2 *>(smem + kLutOff + e * 256 + c * 8) =
-            make_uint2(pack_h2(c0, c1), pack_h2(c0 - h0, c1 - h1));
+    }
+    const bool use_flip = a.rotate_q && a.sign_flip;
+    int sf_lo = 1, sf_hi = 1;
+    if (use_flip) {
+        sf_lo = a.sign_flip[lane];
+        sf_hi = a.sign_flip[64 + lane];
+    }
+    const uint32_t *gh = a.g_bits + (int64_t)hk * QD * 4;
+    uint32_t gw0[4] = {0u, 0u, 0u, 0u};
+    if (QJL && wave < QD / 16) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) gw0[s] = gh[(16 * wave + n) * 4 + s];
+    }
+
+    // ── first cache tiles in flight.  Prefetches are unconditional (past
+    //    the split end they read 0), so the compiler counts outstanding
+    //    loads exactly and waits only for the tile it consumes. ────────
+    const int stride = nw * kDecTile;
+    DecTileRaw ring[PF];
+#pragma unroll
+    for (int p = 0; p < PF - 1; ++p) dec_load<QJL>(ring[p], P, OFS, s_begin + wave * kDecTile + p * stride);
+
+    // ── prologue: codebook halves, query rows, sign LUT ───────────────
+    if (tid < 16) {
+        const uint16_t h = f32_to_f16_rne(cb_mine);
+        cbh[tid] = (uint32_t)h | ((uint32_t)f32_to_f16_rne(cb_mine - f16_to_f32(h)) << 16);
+    }
+    {
+        const bool flip_lo = sf_lo < 0, flip_hi = sf_hi < 0;
+#pragma unroll
+        for (int i = 0; i < kDecRows; ++i) {
+            const int r = wave + i * nw;
+            if (r >= kDecRows) break;
+            float lo, hi;
+            if (q32) {
+                lo = __uint_as_float(qraw[i][0]);
+                hi = __uint_as_float(qraw[i][1]);
+            } else if (a.q_dtype == OMNI_BF16) {
+                lo = __uint_as_float(qraw[i][0] << 16);
+                hi = __uint_as_float(qraw[i][1] << 16);
+            } else {
+                lo = f16_to_f32((uint16_t)qraw[i][0]);
+                hi = f16_to_f32((uint16_t)qraw[i][1]);
+            }
+            if (rc * kDecRows + r >= nrows_total) lo = hi = 0.0f;
+            lo = flip_lo ? -lo : lo;
+            hi = flip_hi ? -hi : hi;
+            if (a.rotate_q) {
+                wht128_lanes(lo, hi, lane);
+                lo = round_to_dtype(lo * a.wht_scale, a.q_dtype);
+                hi = round_to_dtype(hi * a.wht_scale, a.q_dtype);
+            }
+            qs[r * D + lane] = lo;
+            qs[r * D + 64 + lane] = hi;
+        }
     }
     for (int e = tid; e < 256; e += blockDim.x) {
         uint32_t w[4];
+#pragma unroll
         for (int k = 0; k < 4; ++k)
             w[k] = (((e >> (2 * k)) & 1) ? 0x3C00u : 0xBC00u) | ((((e >> (2 * k + 1)) & 1) ? 0x3C00u : 0xBC00u) << 16);
         *reinterpret_cast<uint4 *>(smem + kSlutOff + e * 16) = make_uint4(w[0], w[1], w[2], w[3]);
     }
-    // ── prologue: query rows (row r <-> flat (t, gh) = rc*8 + r) ──────
-    for (int s = tid; s < kDecRows * D; s += blockDim.x) {
-        const int r = s / D, d = s % D;
-        const int64_t rho = (int64_t)rc * kDecRows + r;
-        float v = 0.0f;
-        if (rho < nrows_total) {
-            const int64_t t = rho / a.G;
-            const int hq = hk * a.G + (int)(rho % a.G);
-            v = load_as_f32(a.q, a.q_dtype, ((b * a.Hq + hq) * a.T + t) * D + d);
-            if (a.rotate_q && a.sign_flip && a.sign_flip[d] < 0) v = -v;
-        }
-        qs[s] = v;
-    }
     __syncthreads();
-    if (a.rotate_q) {
-        // rotate_queries in-kernel, all threads: butterfly stages h = 1..64 in
-        // the reference order (hadamard.py:51-85), then scale and round.
-        for (int h = 1; h < D; h <<= 1) {
-            for (int pidx = tid; pidx < kDecRows * (D / 2); pidx += blockDim.x) {
-                const int r = pidx / (D / 2), k = pidx % (D / 2);
-                const int u = (k / h) * 2 * h + (k % h);
-                float *row = qs + r * D;
-                const float x0 = row[u], x1 = row[u + h];
-                row[u] = x0 + x1;
-                row[u + h] = x0 - x1;
-            }
-            __syncthreads();
+
+    // ── byte LUT: entry e at e * 256, copy c at + 8c (two copies per store) ──
+    {
+        const int lpair = ncopy >= 2 ? __builtin_ctz((unsigned)ncopy) - 1 : 0;
+        const int per = 1 << lpair;                       // stores per entry
+        for (int s = tid; s < 256 * per; s += blockDim.x) {
+            const int e = s >> lpair, c2 = s & (per - 1);
+            const uint32_t w0 = cbh[e & 15], w1 = cbh[e >> 4];
+            // (hi(c0), hi(c1)) and (lo(c0), lo(c1))
+            const uint32_t hp = __builtin_amdgcn_perm(w1, w0, 0x05040100u);
+            const uint32_t lp = __builtin_amdgcn_perm(w1, w0, 0x07060302u);
+            if (ncopy >= 2)
+                *reinterpret_cast<uint4 *>(smem + kLutOff + e * 256 + c2 * 16) = make_uint4(hp, lp, hp, lp);
+            else
+                *reinterpret_cast<uint2 *>(smem + kLutOff + e * 256) = make_uint2(hp, lp);
         }
-        for (int s = tid; s < kDecRows * D; s += blockDim.x) qs[s] = round_to_dtype(qs[s] * a.wht_scale, a.q_dtype);
-        __syncthreads();
     }
-    if (QJL && wave == 0) {
-        // GQ (rows x 64) = Q (rows x 128) . G_h^T on MFMA: Q as fp16 hi + lo,
-        // G rows expanded 8 bits at a time through the sign LUT.
-        const int rr = lane & 15, gg = lane >> 4;
-        const uint32_t *gh = a.g_bits + (int64_t)hk * QD * 4;
-        half8_t ah[4], al[4];
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            uint32_t hw[4], lw[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float v0 = rr < kDecRows ? qs[rr * D + 32 * s + 8 * gg + 2 * j] : 0.0f;
-                const float v1 = rr < kDecRows ? qs[rr * D + 32 * s + 8 * gg + 2 * j + 1] : 0.0f;
-                hw[j] = pack_h2(v0, v1);
-                lw[j] = pack_h2(v0 - f16_to_f32(f32_to_f16_rne(v0)), v1 - f16_to_f32(f32_to_f16_rne(v1)));
-            }
-            ah[s] = as_half8(hw[0], hw[1], hw[2], hw[3]);
-            al[s] = as_half8(lw[0], lw[1], lw[2], lw[3]);
-        }
-#pragma unroll
-        for (int cb = 0; cb < QD / 16; ++cb) {
-            float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
-            const int o = 16 * cb + rr;
+    if (QJL) {
+        // GQ (rows x 64) = Q (rows x 128) . G_h^T on MFMA, one 16-column block
+        // per wave: Q as fp16 hi + lo, G rows expanded 8 bits at a time
+        // through the sign LUT.
+        for (int cb = wave; cb < QD / 16; cb += nw) {
+            half8_t ah[4], al[4];
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                const uint32_t byte = (gh[o * 4 + s] >> (8 * gg)) & 0xffu;
+                uint32_t hw[4], lw[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float v0 = n < kDecRows ? qs[n * D + 32 * s + 8 * g + 2 * j] : 0.0f;
+                    const float v1 = n < kDecRows ? qs[n * D + 32 * s + 8 * g + 2 * j + 1] : 0.0f;
+                    hw[j] = pack_h2(v0, v1);
+                    lw[j] = pack_h2(v0 - f16_to_f32(f32_to_f16_rne(v0)), v1 - f16_to_f32(f32_to_f16_rne(v1)));
+                }
+                ah[s] = as_half8(hw[0], hw[1], hw[2], hw[3]);
+                al[s] = as_half8(lw[0], lw[1], lw[2], lw[3]);
+            }
+            float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
+            const int o = 16 * cb + n;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const uint32_t word = cb == wave ? gw0[s] : gh[o * 4 + s];
+                const uint32_t byte = (word >> (8 * g)) & 0xffu;
                 const uint4 gv = *reinterpret_cast<const uint4 *>(smem + kSlutOff + byte * 16u);
                 const half8_t bg = as_half8(gv.x, gv.y, gv.z, gv.w);
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[s], bg, acc, 0, 0, 0);
@@ -635,13 +731,12 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                if (4 * gg + i < kDecRows) gq[(4 * gg + i) * QD + o] = acc[i];
+                if (4 * g + i < kDecRows) gq[(4 * g + i) * QD + o] = acc[i];
         }
     }
     __syncthreads();
 
     // ── per-lane B operands ───────────────────────────────────────────
-    const int n = lane & 15, g = lane >> 4;
     const bool lo_col = n >= kDecRows;           // columns 8-15
     const int rn = lo_col ? n - kDecRows : n;
     half8_t bk[8], bgq[2];
@@ -670,30 +765,15 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
         }
         bgq[s] = as_half8(w[0], w[1], w[2], w[3]);
     }
-    const int64_t rho_n = (int64_t)rc * kDecRows + rn;
+    const int rho_n = rc * kDecRows + rn;
     const int64_t key_limit64 = (a.causal_offset >= 0 && rho_n < nrows_total) ? a.causal_offset + rho_n / a.G
-                                                                               : INT64_MAX;
+                                                                             : INT64_MAX;
 
     // ── main loop ─────────────────────────────────────────────────────
-    const int s_begin = split * (int)a.split_len;
-    const int s_end = (int)imin64(a.S, (int64_t)s_begin + a.split_len);
     const int key_limit = (int)imin64(key_limit64, (int64_t)0x7fffffff);
     // tiles ending at or below min(s_end, first masked key of any row) need no masks
-    const int64_t min_limit64 = (a.causal_offset >= 0) ? a.causal_offset + ((int64_t)rc * kDecRows) / a.G : INT64_MAX;
+    const int64_t min_limit64 = (a.causal_offset >= 0) ? a.causal_offset + (rc * kDecRows) / a.G : INT64_MAX;
     const int full_end = (int)imin64((int64_t)s_end, min_limit64 + 1);
-    const int64_t kv_base = (b * a.Hkv + hk) * a.S;
-    DecBufs P;
-    P.kn = __builtin_amdgcn_make_buffer_rsrc((void *)(a.k_nib + kv_base * 64), (short)0, s_end * 64, kBufWord3);
-    P.vn = __builtin_amdgcn_make_buffer_rsrc((void *)(a.v_nib + kv_base * 64), (short)0, s_end * 64, kBufWord3);
-    P.kq = __builtin_amdgcn_make_buffer_rsrc((void *)(QJL ? a.k_qjl + kv_base * 8 : a.k_nib), (short)0,
-                                             QJL ? s_end * 8 : 0, kBufWord3);
-    P.kr = __builtin_amdgcn_make_buffer_rsrc((void *)(QJL ? a.k_norms + kv_base : (const float *)a.k_nib), (short)0,
-                                             QJL ? s_end * 4 : 0, kBufWord3);
-    DecOffsets OFS;
-    OFS.k = (uint32_t)n * 64u + 16u * g;
-    OFS.sg = (uint32_t)n * 8u;
-    OFS.nr = 16u * g;
-    OFS.v = 256u * g + 4u * n;
     const uint32_t laneoff = (uint32_t)(lane & (ncopy - 1)) * 8u;
     // ones on the hi slots of each (hi, lo) pair: sums every token's P once
     const half8_t ones = as_half8(0x3C003C00u, 0u, 0x3C003C00u, 0u);
@@ -705,146 +785,143 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     lacc_sum = float4_t{0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY;
 
-    const int stride = nw * kDecTile;
-    DecTileRaw ring[PF];
-#pragma unroll
-    for (int p = 0; p < PF - 1; ++p) {
-        const int tp = s_begin + wave * kDecTile + p * stride;
-        if (tp < s_end) dec_load<QJL>(ring[p], P, OFS, tp);
-    }
-    for (int base = s_begin + wave * kDecTile; base < s_end; base += PF * stride) {
-#pragma unroll
-        for (int p = 0; p < PF; ++p) {
-            const int tt = base + p * stride;
-            if (tt >= s_end) break;
-            const int tpre = tt + (PF - 1) * stride;
-            if (tpre < s_end) dec_load<QJL>(ring[(p + PF - 1) % PF], P, OFS, tpre);
-            DecTileRaw &R = ring[p];
-            const bool full = tt + kDecTile <= full_end;
+    // One 32-token tile: scores, online softmax, PV.
+    auto tile_step = [&](DecTileRaw &R, const int tt) {
+        const bool full = tt + kDecTile <= full_end;
 
-            // scores: lane (n, g) holds tokens tt + 16u + 4g + i
-            float sc[8];
+        // scores: lane (n, g) holds tokens tt + 16u + 4g + i
+        float sc[8];
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f}, qacc = float4_t{0.f, 0.f, 0.f, 0.f};
-                const uint32_t kw[4] = {R.k[u].x, R.k[u].y, R.k[u].z, R.k[u].w};
+        for (int u = 0; u < 2; ++u) {
+            float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f}, qacc = float4_t{0.f, 0.f, 0.f, 0.f};
+            const uint32_t kw[4] = {R.k[u].x, R.k[u].y, R.k[u].z, R.k[u].w};
 #pragma unroll
-                for (int s = 0; s < 8; ++s) {
-                    const uint2 e0 = *reinterpret_cast<const uint2 *>(lut + lut_addr(kw[s >> 1], laneoff, 2 * (s & 1)));
-                    const uint2 e1 = *reinterpret_cast<const uint2 *>(lut + lut_addr(kw[s >> 1], laneoff, 2 * (s & 1) + 1));
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pair_half8(e0, e1), bk[s], acc, 0, 0, 0);
-                }
-                if (QJL) {
+            for (int s = 0; s < 8; ++s) {
+                const uint2 e0 = *reinterpret_cast<const uint2 *>(lut + lut_addr(kw[s >> 1], laneoff, 2 * (s & 1)));
+                const uint2 e1 = *reinterpret_cast<const uint2 *>(lut + lut_addr(kw[s >> 1], laneoff, 2 * (s & 1) + 1));
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pair_half8(e0, e1), bk[s], acc, 0, 0, 0);
+            }
+            if (QJL) {
 #pragma unroll
-                    for (int s = 0; s < 2; ++s) {
-                        const uint32_t byte = ((s ? R.sg[u].y : R.sg[u].x) >> (8 * g)) & 0xffu;
-                        const uint4 sv = *reinterpret_cast<const uint4 *>(smem + kSlutOff + byte * 16u);
-                        qacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(sv.x, sv.y, sv.z, sv.w), bgq[s], qacc, 0, 0, 0);
-                    }
-                }
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    float v = acc[i] + dpp_row_shl8(acc[i]);
-                    if (QJL) v = __builtin_fmaf(R.nr[u][i] * a.alpha_c, qacc[i], v);
-                    sc[4 * u + i] = lo_col ? -INFINITY : v;
+                for (int s = 0; s < 2; ++s) {
+                    const uint32_t byte = ((s ? R.sg[u].y : R.sg[u].x) >> (8 * g)) & 0xffu;
+                    const uint4 sv = *reinterpret_cast<const uint4 *>(smem + kSlutOff + byte * 16u);
+                    qacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(sv.x, sv.y, sv.z, sv.w), bgq[s], qacc, 0, 0, 0);
                 }
             }
-            if (!full) {
 #pragma unroll
-                for (int u = 0; u < 2; ++u)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int tn = tt + 16 * u + 4 * g + i;
-                        if (tn >= s_end || tn > key_limit) sc[4 * u + i] = -INFINITY;
-                    }
-            }
-
-            // online softmax (exp2 domain), lazy rescale
-            float mt = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
-            mt = max_over_groups(mt);
-            const bool need = mt > m_run + 8.0f;
-            if (__builtin_amdgcn_ballot_w64(need)) {
-                const float f = need ? __builtin_amdgcn_exp2f(m_run - mt) : 1.0f;
-#pragma unroll
-                for (int k = 0; k < 8; ++k) oacc[k] *= f;
-                lacc_sum *= f;
-                m_run = need ? mt : m_run;
-            }
-            const float m_use = (m_run == -INFINITY) ? 0.0f : m_run;
-            half8_t pb[2];
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const uint32_t p01 = cvt_pk_h2(__builtin_amdgcn_exp2f(sc[4 * u] - m_use), __builtin_amdgcn_exp2f(sc[4 * u + 1] - m_use));
-                const uint32_t p23 = cvt_pk_h2(__builtin_amdgcn_exp2f(sc[4 * u + 2] - m_use), __builtin_amdgcn_exp2f(sc[4 * u + 3] - m_use));
-                pb[u] = as_half8(p01, p01, p23, p23);
-                lacc_sum = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb[u], lacc_sum, 0, 0, 0);
-            }
-
-            // PV: pair bytes interleave the nibbles of two tokens at one d, so
-            // each LUT entry is an MFMA-ready (hi pair, lo pair) for that d.
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                uint32_t ev[2], od[2];
-#pragma unroll
-                for (int pr = 0; pr < 2; ++pr) {
-                    const uint32_t va = R.v[4 * u + 2 * pr], vb = R.v[4 * u + 2 * pr + 1];
-                    ev[pr] = (va & 0x0F0F0F0Fu) | ((vb & 0x0F0F0F0Fu) << 4);
-                    od[pr] = ((va >> 4) & 0x0F0F0F0Fu) | (vb & 0xF0F0F0F0u);
-                }
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const uint2 e0 = *reinterpret_cast<const uint2 *>(lut + lut_addr(ev[0], laneoff, j));
-                    const uint2 e1 = *reinterpret_cast<const uint2 *>(lut + lut_addr(ev[1], laneoff, j));
-                    oacc[2 * j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pair_half8(e0, e1), pb[u], oacc[2 * j], 0, 0, 0);
-                    const uint2 f0 = *reinterpret_cast<const uint2 *>(lut + lut_addr(od[0], laneoff, j));
-                    const uint2 f1 = *reinterpret_cast<const uint2 *>(lut + lut_addr(od[1], laneoff, j));
-                    oacc[2 * j + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pair_half8(f0, f1), pb[u], oacc[2 * j + 1], 0, 0, 0);
-                }
+            for (int i = 0; i < 4; ++i) {
+                float v = acc[i] + dpp_row_shl8(acc[i]);
+                if (QJL) v = __builtin_fmaf(R.nr[u][i] * a.alpha_c, qacc[i], v);
+                sc[4 * u + i] = lo_col ? -INFINITY : v;
             }
         }
+        if (!full) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int tn = tt + 16 * u + 4 * g + i;
+                    if (tn >= s_end || tn > key_limit) sc[4 * u + i] = -INFINITY;
+                }
+        }
+
+        // online softmax (exp2 domain), lazy rescale
+        float mt = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+        mt = max_over_groups(mt);
+        const bool need = mt > m_run + 8.0f;
+        if (__builtin_amdgcn_ballot_w64(need)) {
+            const float f = need ? __builtin_amdgcn_exp2f(m_run - mt) : 1.0f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) oacc[k] *= f;
+            lacc_sum *= f;
+            m_run = need ? mt : m_run;
+        }
+        const float m_use = (m_run == -INFINITY) ? 0.0f : m_run;
+        half8_t pb[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const uint32_t p01 = cvt_pk_h2(__builtin_amdgcn_exp2f(sc[4 * u] - m_use), __builtin_amdgcn_exp2f(sc[4 * u + 1] - m_use));
+            const uint32_t p23 = cvt_pk_h2(__builtin_amdgcn_exp2f(sc[4 * u + 2] - m_use), __builtin_amdgcn_exp2f(sc[4 * u + 3] - m_use));
+            pb[u] = as_half8(p01, p01, p23, p23);
+            lacc_sum = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb[u], lacc_sum, 0, 0, 0);
+        }
+
+        // PV: pair bytes interleave the nibbles of two tokens at one d, so
+        // each LUT entry is an MFMA-ready (hi pair, lo pair) for that d.
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            uint32_t ev[2], od[2];
+#pragma unroll
+            for (int pr = 0; pr < 2; ++pr) {
+                const uint32_t va = R.v[4 * u + 2 * pr], vb = R.v[4 * u + 2 * pr + 1];
+                ev[pr] = (va & 0x0F0F0F0Fu) | ((vb & 0x0F0F0F0Fu) << 4);
+                od[pr] = ((va >> 4) & 0x0F0F0F0Fu) | (vb & 0xF0F0F0F0u);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint2 e0 = *reinterpret_cast<const uint2 *>(lut + lut_addr(ev[0], laneoff, j));
+                const uint2 e1 = *reinterpret_cast<const uint2 *>(lut + lut_addr(ev[1], laneoff, j));
+                oacc[2 * j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pair_half8(e0, e1), pb[u], oacc[2 * j], 0, 0, 0);
+                const uint2 f0 = *reinterpret_cast<const uint2 *>(lut + lut_addr(od[0], laneoff, j));
+                const uint2 f1 = *reinterpret_cast<const uint2 *>(lut + lut_addr(od[1], laneoff, j));
+                oacc[2 * j + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pair_half8(f0, f1), pb[u], oacc[2 * j + 1], 0, 0, 0);
+            }
+        }
+    };
+
+    // Full groups of PF tiles: each step first prefetches the tile PF - 1
+    // steps ahead (unconditionally), so the loop body never branches around
+    // a load and the compiler's wait counts keep PF - 1 tiles in flight.
+    int tt0 = s_begin + wave * kDecTile;
+    for (; tt0 + (PF - 1) * stride < s_end; tt0 += PF * stride) {
+#pragma unroll
+        for (int p = 0; p < PF; ++p) {
+            __builtin_amdgcn_sched_barrier(0);
+            dec_load<QJL>(ring[(p + PF - 1) % PF], P, OFS, tt0 + (p + PF - 1) * stride);
+            __builtin_amdgcn_sched_barrier(0);
+            tile_step(ring[p], tt0 + p * stride);
+        }
     }
+    // the last (up to PF - 1) tiles are already in ring[0 ..]
+#pragma unroll
+    for (int p = 0; p < PF - 1; ++p)
+        if (tt0 + p * stride < s_end) tile_step(ring[p], tt0 + p * stride);
 
     // ── combine waves (deterministic order) ──────────────────────────
     __syncthreads();   // LUTs are dead from here on
-    float *wm = reinterpret_cast<float *>(smem);
-    float *wl = wm + kDecWaves * kDecRows;
-    float *ob = wl + kDecWaves * kDecRows;          // [kDecRows][D]
-    if (g == 0 && !lo_col) {
-        wm[wave * kDecRows + n] = m_run;
-        wl[wave * kDecRows + n] = lacc_sum[0];
+    float *ob = reinterpret_cast<float *>(smem);                     // [nw][kDecRows][kObStride]
+    float *wm = reinterpret_cast<float *>(smem + kDecSlabBytes);     // [nw][kDecRows] running max
+    float *wl = wm + kDecWaves * kDecRows;                           // [nw][kDecRows] denominators
+    if (!lo_col) {
+        if (g == 0) {
+            wm[wave * kDecRows + n] = m_run;
+            wl[wave * kDecRows + n] = lacc_sum[0];
+        }
+        float *dst = ob + (wave * kDecRows + n) * kObStride;
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dst[8 * (4 * g + i) + k] = oacc[k][i];
     }
     __syncthreads();
-    float mx = -INFINITY;
-    for (int w = 0; w < nw; ++w) mx = fmaxf(mx, wm[w * kDecRows + rn]);
-    const float mu = (mx == -INFINITY) ? 0.0f : mx;
-    const float fw = exp2f(m_run - mu);
-    for (int w = 0; w < nw; ++w) {
-        if (wave == w && !lo_col) {
-#pragma unroll
-            for (int k = 0; k < 8; ++k)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    float *dst = ob + n * D + 8 * (4 * g + i) + k;
-                    const float v = oacc[k][i] * fw;
-                    *dst = (w == 0) ? v : (*dst + v);
-                }
-        }
-        __syncthreads();
-    }
     const int64_t unit = (b * a.Hkv + hk) * a.n_rchunks + rc;
     for (int s = tid; s < kDecRows * D; s += blockDim.x) {
         const int rr = s / D, d = s % D;
-        const int64_t rr_rho = (int64_t)rc * kDecRows + rr;
+        const int rr_rho = rc * kDecRows + rr;
         if (rr_rho >= nrows_total) continue;
         float rmx = -INFINITY;
         for (int w = 0; w < nw; ++w) rmx = fmaxf(rmx, wm[w * kDecRows + rr]);
         const float rmu = (rmx == -INFINITY) ? 0.0f : rmx;
-        float lsum = 0.0f;
-        for (int w = 0; w < nw; ++w) lsum = __builtin_fmaf(exp2f(wm[w * kDecRows + rr] - rmu), wl[w * kDecRows + rr], lsum);
-        const float osum = ob[rr * D + d];
+        float lsum = 0.0f, osum = 0.0f;
+        for (int w = 0; w < nw; ++w) {
+            const float f = exp2f(wm[w * kDecRows + rr] - rmu);
+            lsum = __builtin_fmaf(f, wl[w * kDecRows + rr], lsum);
+            osum = __builtin_fmaf(f, ob[(w * kDecRows + rr) * kObStride + d], osum);
+        }
         if (a.splits == 1) {
-            const int64_t t = rr_rho / a.G;
-            const int hq = hk * a.G + (int)(rr_rho % a.G);
+            const int t = rr_rho / a.G;
+            const int hq = hk * a.G + (rr_rho - t * a.G);
             a.out[((b * a.Hq + hq) * a.T + t) * D + d] = osum / lsum;
         } else {
             float *wp = a.ws + ((unit * a.splits + split) * kDecRows + rr) * (D + 2);
@@ -891,7 +968,7 @@ static Plan make_plan(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int D) {
         const int64_t tps = (tiles + splits - 1) / splits;
         p.splits = (int)splits;
         p.split_len = tps * kDecTile;
-        p.nw = (int)clamp64(tps / 2, 1, kDecWaves);
+        p.nw = (int)clamp64(tps, 1, kDecWaves);
         p.ncopy = tps >= 32 ? 32 : (tps >= 8 ? 8 : 1);
         p.lds = kDecLdsBytes;
     } else {
@@ -933,7 +1010,8 @@ extern "C" int omni_attn(const void *q, int q_dtype, const uint8_t *k_nib, const
     OMNI_CHECK_ARG(q && k_nib && v_nib && codebooks && out, "omni_attn: NULL pointer");
     OMNI_CHECK_ARG(!with_qjl || (k_qjl && k_norms && g_bits), "omni_attn: NULL QJL pointer");
     OMNI_CHECK_ARG(isfinite(scale), "omni_attn: scale must be finite");
-    OMNI_CHECK_ARG(S < (int64_t(1) << 26), "omni_attn: S must be < 2^26 tokens per sequence");
+    OMNI_CHECK_ARG(S < (int64_t(1) << 25), "omni_attn: S must be < 2^25 tokens per sequence");
+    OMNI_CHECK_ARG(T * (Hq / Hkv) < (int64_t(1) << 31), "omni_attn: T * (n_heads / n_kv_heads) must be < 2^31");
     Plan p = make_plan(B, Hq, Hkv, T, S, head_dim);
     OMNI_CHECK_ARG(Hkv <= 65535 && B * p.n_rchunks <= 2147483647LL && p.splits <= 2147483647,
                    "omni_attn: grid too large");
