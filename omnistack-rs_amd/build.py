@@ -39,6 +39,10 @@ def common_flags() -> list[str]:
         "-O3", "-fPIC", "-std=c++17", f"--offload-arch={ARCH}",
         "-ffp-contract=off",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # keep private arrays in registers: the backend would otherwise move
+        # small per-thread arrays into LDS (the decode kernel sizes its LDS
+        # explicitly)
+        "-mllvm", "-disable-promote-alloca-to-lds",
         "-Wall", "-Wno-unused-function",
         f"-I{INCLUDE}", f"-I{CSRC}",
     ]

@@ -444,7 +444,10 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
 //                              LDS address (byte << 8) | (lane % 32) * 8
 //               [64K, 68K)     sign byte -> eight +-1.0 halves
 //               [68K, 74K)     query rows and G q (prologue)
-//               [74K, +64)     codebook as (fp16 hi, fp16 remainder) pairs
+//               [74K, 86K)     query rows as MFMA operands: (scale q) hi/lo
+//                              B images for the scores, q hi/lo A images
+//                              for G q
+//               [86K, +64)     codebook as (fp16 hi, fp16 remainder) pairs
 constexpr int kDecRows = 8;
 constexpr int kDecWaves = 8;
 constexpr int kDecTile = 32;
@@ -453,8 +456,11 @@ constexpr int kLutOff = 0;
 constexpr int kLutBytes = 256 * 256;
 constexpr int kSlutOff = kLutBytes;
 constexpr int kSlutBytes = 256 * 16;
+static_assert((kSlutOff & (kSlutOff - 1)) == 0 && kSlutOff >= kSlutBytes, "sign LUT address is formed with an OR");
 constexpr int kDecQsOff = kSlutOff + kSlutBytes;
-constexpr int kDecCbOff = kDecQsOff + kDecRows * (128 + 64) * 4;
+constexpr int kDecBkOff = kDecQsOff + kDecRows * (128 + 64) * 4;   // [row][quad][hi, lo] 16 B
+constexpr int kDecGaOff = kDecBkOff + kDecRows * 32 * 2 * 16;        // [row][8-dim group][hi, lo] 16 B
+constexpr int kDecCbOff = kDecGaOff + kDecRows * 16 * 2 * 16;       // 16 x (fp16 hi | remainder << 16)
 constexpr int kDecLdsBytes = kDecCbOff + 16 * 4;
 // epilogue reuse of [0, 68K): per-wave O slabs (rows padded to 132 floats),
 // then per-wave running max and denominator
@@ -546,14 +552,54 @@ __device__ __forceinline__ float max_over_groups(float m) {
 // _wht_torch (hadamard.py:51-85).  Stage h pairs element u (bit h clear)
 // with u + h: u <- x[u] + x[u+h], u + h <- x[u] - x[u+h], all fp32; stages
 // h = 1..32 cross lanes, h = 64 pairs the two values of a lane.
-__device__ __forceinline__ void wht128_lanes(float &lo, float &hi, int lane) {
-#pragma unroll
-    for (int h = 1; h < 64; h <<= 1) {
-        const float plo = __shfl_xor(lo, h), phi = __shfl_xor(hi, h);
-        const bool upper = (lane & h) != 0;
-        lo = upper ? plo - lo : lo + plo;
-        hi = upper ? phi - hi : hi + phi;
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// x[lane ^ H] without LDS: DPP quad permutes (H = 1, 2), row rotates
+// (H = 4, 8; lane i reads lane i - k mod 16 for row_ror:k) and the gfx950
+// row / half-wave swaps (H = 16, 32).
+template <int H>
+__device__ __forceinline__ float xor_partner(float x, int lane) {
+    if constexpr (H == 1) {
+        return dpp_mov<0xB1>(x);                                  // quad_perm [1,0,3,2]
+    } else if constexpr (H == 2) {
+        return dpp_mov<0x4E>(x);                                  // quad_perm [2,3,0,1]
+    } else if constexpr (H == 4) {
+        const float up = dpp_mov<0x12C>(x), dn = dpp_mov<0x124>(x);  // row_ror:12 / row_ror:4
+        return (lane & 4) ? dn : up;
+    } else if constexpr (H == 8) {
+        return dpp_mov<0x128>(x);                                 // row_ror:8
+    } else if constexpr (H == 16) {
+        const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        return __uint_as_float((lane & 16) ? t[0] : t[1]);
+    } else {
+        const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        return __uint_as_float((lane & 32) ? t[0] : t[1]);
     }
+}
+
+template <int H>
+__device__ __forceinline__ void wht_stage(float &lo, float &hi, int lane) {
+    // element u (bit H clear) <- x[u] + x[u+H]; u + H <- x[u] - x[u+H]
+    const float sgn = (lane & H) ? -1.0f : 1.0f;
+    lo = __builtin_fmaf(sgn, lo, xor_partner<H>(lo, lane));
+    hi = __builtin_fmaf(sgn, hi, xor_partner<H>(hi, lane));
+}
+
+// One lane per (d, d + 64) of a 128-wide row: the normalized WHT of
+// _wht_torch (hadamard.py:51-85).  Stage h pairs element u (bit h clear)
+// with u + h: u <- x[u] + x[u+h], u + h <- x[u] - x[u+h], all fp32 (an fma
+// with +-1 rounds exactly as the add / subtract); stages h = 1..32 cross
+// lanes, h = 64 pairs the two values of a lane.
+__device__ __forceinline__ void wht128_lanes(float &lo, float &hi, int lane) {
+    wht_stage<1>(lo, hi, lane);
+    wht_stage<2>(lo, hi, lane);
+    wht_stage<4>(lo, hi, lane);
+    wht_stage<8>(lo, hi, lane);
+    wht_stage<16>(lo, hi, lane);
+    wht_stage<32>(lo, hi, lane);
     const float a = lo, b = hi;
     lo = a + b;
     hi = a - b;
@@ -562,20 +608,18 @@ __device__ __forceinline__ void wht128_lanes(float &lo, float &hi, int lane) {
 template <bool QJL, int PF>
 __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs a) {
     constexpr int D = 128, QD = 64;
+    constexpr int nw = kDecWaves;
     __shared__ __attribute__((aligned(16))) unsigned char smem[kDecLdsBytes];
     float *qs = reinterpret_cast<float *>(smem + kDecQsOff);
     float *gq = qs + kDecRows * D;
-    uint32_t *cbh = reinterpret_cast<uint32_t *>(smem + kDecCbOff);
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int nw = blockDim.x >> 6;
     const int split = blockIdx.x, hk = blockIdx.y;
     const int64_t bz = blockIdx.z;
     const int64_t b = bz / a.n_rchunks;
     const int rc = (int)(bz % a.n_rchunks);
     const int nrows_total = (int)(a.T * a.G);
-    const int ncopy = a.ncopy;
     const int n = lane & 15, g = lane >> 4;
 
     // ── cache stream descriptors ──────────────────────────────────────
@@ -595,42 +639,37 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     OFS.nr = 16u * g;
     OFS.v = 256u * g + 4u * n;
 
-    // ── prologue loads (issued before the cache prefetch so that waiting
-    //    for them does not wait for the cache) ────────────────────────
-    const float *cbp = a.codebooks + (a.per_head ? hk * 16 : 0);
-    const float cb_mine = tid < 16 ? cbp[tid] : 0.0f;
-    // query row r <-> flat (t, g) = rc * 8 + r; each wave takes rows
-    // wave, wave + nw, ... (raw bits now, converted after the prefetch)
+    // ── prologue loads: branch-free buffer loads (an absent input gets a
+    //    zero-size descriptor and reads 0), issued before the cache
+    //    prefetch so that waiting for them does not wait for the cache ──
+    // this wave's query row: flat (t, g) = rc * 8 + wave
+    const int rho = rc * kDecRows + wave;
+    const bool row_ok = rho < nrows_total;
+    const int rho_c = row_ok ? rho : nrows_total - 1;
+    const int t_q = rho_c / a.G;
+    const int hq_q = hk * a.G + (rho_c - t_q * a.G);
     const bool q32 = a.q_dtype == OMNI_F32;
-    uint32_t qraw[kDecRows][2];
-#pragma unroll
-    for (int i = 0; i < kDecRows; ++i) {
-        qraw[i][0] = qraw[i][1] = 0u;
-        if (i * nw >= kDecRows) break;
-        const int rho = imin(rc * kDecRows + wave + i * nw, nrows_total - 1);
-        const int t = rho / a.G;
-        const int hq = hk * a.G + (rho - t * a.G);
-        const int64_t base = ((b * a.Hq + hq) * a.T + t) * D;
-        if (q32) {
-            qraw[i][0] = reinterpret_cast<const uint32_t *>(a.q)[base + lane];
-            qraw[i][1] = reinterpret_cast<const uint32_t *>(a.q)[base + 64 + lane];
-        } else {
-            qraw[i][0] = reinterpret_cast<const uint16_t *>(a.q)[base + lane];
-            qraw[i][1] = reinterpret_cast<const uint16_t *>(a.q)[base + 64 + lane];
-        }
-    }
+    const int esz = q32 ? 4 : 2;
+    const __amdgpu_buffer_rsrc_t QR = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(reinterpret_cast<const char *>(a.q) + ((b * a.Hq + hq_q) * a.T + t_q) * (int64_t)(D * esz)),
+        (short)0, D * esz, kBufWord3);
+    const uint32_t q32_lo = __builtin_amdgcn_raw_buffer_load_b32(QR, 4u * lane, 0, 0);
+    const uint32_t q32_hi = __builtin_amdgcn_raw_buffer_load_b32(QR, 4u * (64 + lane), 0, 0);
+    const uint32_t q16_lo = __builtin_amdgcn_raw_buffer_load_b16(QR, 2u * lane, 0, 0);
+    const uint32_t q16_hi = __builtin_amdgcn_raw_buffer_load_b16(QR, 2u * (64 + lane), 0, 0);
     const bool use_flip = a.rotate_q && a.sign_flip;
-    int sf_lo = 1, sf_hi = 1;
-    if (use_flip) {
-        sf_lo = a.sign_flip[lane];
-        sf_hi = a.sign_flip[64 + lane];
-    }
-    const uint32_t *gh = a.g_bits + (int64_t)hk * QD * 4;
-    uint32_t gw0[4] = {0u, 0u, 0u, 0u};
-    if (QJL && wave < QD / 16) {
-#pragma unroll
-        for (int s = 0; s < 4; ++s) gw0[s] = gh[(16 * wave + n) * 4 + s];
-    }
+    const __amdgpu_buffer_rsrc_t SF = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(use_flip ? (const void *)a.sign_flip : (const void *)a.codebooks), (short)0, use_flip ? D : 0, kBufWord3);
+    const uint32_t sf_lo = __builtin_amdgcn_raw_buffer_load_b8(SF, (uint32_t)lane, 0, 0);
+    const uint32_t sf_hi = __builtin_amdgcn_raw_buffer_load_b8(SF, (uint32_t)(64 + lane), 0, 0);
+    // codebook entry lane % 16 (threads 0-15 publish it as fp16 hi / remainder)
+    const __amdgpu_buffer_rsrc_t CB = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(a.codebooks + (a.per_head ? hk * 16 : 0)), (short)0, 16 * 4, kBufWord3);
+    const float cb_mine = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(CB, 4u * (lane & 15), 0, 0));
+    // G rows 16 * wave + n (waves 0-3 compute that 16-column block of G q)
+    const __amdgpu_buffer_rsrc_t GB = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(a.g_bits + (QJL ? (int64_t)hk * QD * 4 : 0)), (short)0, (QJL && wave < QD / 16) ? QD * 16 : 0, kBufWord3);
+    const u32x4_t gw = __builtin_amdgcn_raw_buffer_load_b128(GB, (uint32_t)(16 * wave + n) * 16u, 0, 0);
 
     // ── first cache tiles in flight.  Prefetches are unconditional (past
     //    the split end they read 0), so the compiler counts outstanding
@@ -640,99 +679,124 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
 #pragma unroll
     for (int p = 0; p < PF - 1; ++p) dec_load<QJL>(ring[p], P, OFS, s_begin + wave * kDecTile + p * stride);
 
-    // ── prologue: codebook halves, query rows, sign LUT ───────────────
-    if (tid < 16) {
-        const uint16_t h = f32_to_f16_rne(cb_mine);
-        cbh[tid] = (uint32_t)h | ((uint32_t)f32_to_f16_rne(cb_mine - f16_to_f32(h)) << 16);
-    }
+    // ── codebook as (fp16 hi, fp16 remainder) pairs (every lane stores
+    //    entry lane % 16: same values, no branch) ──────────────────────
     {
-        const bool flip_lo = sf_lo < 0, flip_hi = sf_hi < 0;
-#pragma unroll
-        for (int i = 0; i < kDecRows; ++i) {
-            const int r = wave + i * nw;
-            if (r >= kDecRows) break;
-            float lo, hi;
-            if (q32) {
-                lo = __uint_as_float(qraw[i][0]);
-                hi = __uint_as_float(qraw[i][1]);
-            } else if (a.q_dtype == OMNI_BF16) {
-                lo = __uint_as_float(qraw[i][0] << 16);
-                hi = __uint_as_float(qraw[i][1] << 16);
-            } else {
-                lo = f16_to_f32((uint16_t)qraw[i][0]);
-                hi = f16_to_f32((uint16_t)qraw[i][1]);
-            }
-            if (rc * kDecRows + r >= nrows_total) lo = hi = 0.0f;
-            lo = flip_lo ? -lo : lo;
-            hi = flip_hi ? -hi : hi;
-            if (a.rotate_q) {
-                wht128_lanes(lo, hi, lane);
-                lo = round_to_dtype(lo * a.wht_scale, a.q_dtype);
-                hi = round_to_dtype(hi * a.wht_scale, a.q_dtype);
-            }
-            qs[r * D + lane] = lo;
-            qs[r * D + 64 + lane] = hi;
-        }
+        const uint16_t h = f32_to_f16_rne(cb_mine);
+        *reinterpret_cast<uint32_t *>(smem + kDecCbOff + 4 * (lane & 15)) =
+            (uint32_t)h | ((uint32_t)f32_to_f16_rne(cb_mine - f16_to_f32(h)) << 16);
     }
-    for (int e = tid; e < 256; e += blockDim.x) {
+    // ── sign byte -> eight +-1.0 halves (threads 0..255) ──────────────
+    if (tid < 256) {
+        const int e = tid;
         uint32_t w[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k)
             w[k] = (((e >> (2 * k)) & 1) ? 0x3C00u : 0xBC00u) | ((((e >> (2 * k + 1)) & 1) ? 0x3C00u : 0xBC00u) << 16);
         *reinterpret_cast<uint4 *>(smem + kSlutOff + e * 16) = make_uint4(w[0], w[1], w[2], w[3]);
     }
+    // ── this wave's query row: (sign flip,) WHT, round to the q dtype ──
+    {
+        float lo, hi;
+        if (q32) {
+            lo = __uint_as_float(q32_lo);
+            hi = __uint_as_float(q32_hi);
+        } else if (a.q_dtype == OMNI_BF16) {
+            lo = __uint_as_float(q16_lo << 16);
+            hi = __uint_as_float(q16_hi << 16);
+        } else {
+            lo = f16_to_f32((uint16_t)q16_lo);
+            hi = f16_to_f32((uint16_t)q16_hi);
+        }
+        lo = (sf_lo & 0x80u) ? -lo : lo;
+        hi = (sf_hi & 0x80u) ? -hi : hi;
+        if (a.rotate_q) {
+            wht128_lanes(lo, hi, lane);
+            lo = round_to_dtype(lo * a.wht_scale, a.q_dtype);
+            hi = round_to_dtype(hi * a.wht_scale, a.q_dtype);
+        }
+        qs[wave * D + lane] = row_ok ? lo : 0.0f;
+        qs[wave * D + 64 + lane] = row_ok ? hi : 0.0f;
+    }
+    // MFMA operand images of this row (read back by the same wave):
+    //   lanes 0-31, quad j = dims 4j..4j+3 of scale q: B slots
+    //     hi [h0 h1 h0 h1 h2 h3 h2 h3], lo [l0 l1 0 0 l2 l3 0 0]
+    //   lanes 32-47, group j = dims 8j..8j+7 of q: A slots hi / lo
+    if (lane < 32) {
+        const float4 v = *reinterpret_cast<const float4 *>(qs + wave * D + 4 * lane);
+        const float h[4] = {v.x * a.qscale, v.y * a.qscale, v.z * a.qscale, v.w * a.qscale};
+        float l[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) l[j] = h[j] - f16_to_f32(f32_to_f16_rne(h[j]));
+        uint4 *dst = reinterpret_cast<uint4 *>(smem + kDecBkOff + (wave * 32 + lane) * 32);
+        dst[0] = make_uint4(pack_h2(h[0], h[1]), pack_h2(h[0], h[1]), pack_h2(h[2], h[3]), pack_h2(h[2], h[3]));
+        dst[1] = make_uint4(pack_h2(l[0], l[1]), 0u, pack_h2(l[2], l[3]), 0u);
+    } else if (QJL && lane < 48) {
+        const int j = lane - 32;
+        const float4 v0 = *reinterpret_cast<const float4 *>(qs + wave * D + 8 * j);
+        const float4 v1 = *reinterpret_cast<const float4 *>(qs + wave * D + 8 * j + 4);
+        const float x[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        uint32_t hw[4], lw[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            hw[k] = pack_h2(x[2 * k], x[2 * k + 1]);
+            lw[k] = pack_h2(x[2 * k] - f16_to_f32(f32_to_f16_rne(x[2 * k])),
+                            x[2 * k + 1] - f16_to_f32(f32_to_f16_rne(x[2 * k + 1])));
+        }
+        uint4 *dst = reinterpret_cast<uint4 *>(smem + kDecGaOff + (wave * 16 + j) * 32);
+        dst[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        dst[1] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    }
     __syncthreads();
 
-    // ── byte LUT: entry e at e * 256, copy c at + 8c (two copies per store) ──
+    // ── byte LUT: entry e at e * 256, 32 copies of (hi pair, lo pair);
+    //    thread t writes 16-byte chunk t % 16 of entries (t >> 4) + 32 i ──
     {
-        const int lpair = ncopy >= 2 ? __builtin_ctz((unsigned)ncopy) - 1 : 0;
-        const int per = 1 << lpair;                       // stores per entry
-        for (int s = tid; s < 256 * per; s += blockDim.x) {
-            const int e = s >> lpair, c2 = s & (per - 1);
-            const uint32_t w0 = cbh[e & 15], w1 = cbh[e >> 4];
-            // (hi(c0), hi(c1)) and (lo(c0), lo(c1))
-            const uint32_t hp = __builtin_amdgcn_perm(w1, w0, 0x05040100u);
-            const uint32_t lp = __builtin_amdgcn_perm(w1, w0, 0x07060302u);
-            if (ncopy >= 2)
-                *reinterpret_cast<uint4 *>(smem + kLutOff + e * 256 + c2 * 16) = make_uint4(hp, lp, hp, lp);
-            else
-                *reinterpret_cast<uint2 *>(smem + kLutOff + e * 256) = make_uint2(hp, lp);
+        const uint32_t *cbh = reinterpret_cast<const uint32_t *>(smem + kDecCbOff);
+        const uint32_t w0 = cbh[(tid >> 4) & 15];           // low nibble, same for all i
+        uint32_t w1[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w1[i] = cbh[(tid >> 8) + 2 * i];   // high nibble (e >> 4)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int e = (tid >> 4) + 32 * i;
+            const uint32_t hp = __builtin_amdgcn_perm(w1[i], w0, 0x05040100u);   // (hi c0, hi c1)
+            const uint32_t lp = __builtin_amdgcn_perm(w1[i], w0, 0x07060302u);   // (lo c0, lo c1)
+            *reinterpret_cast<uint4 *>(smem + kLutOff + e * 256 + (tid & 15) * 16) = make_uint4(hp, lp, hp, lp);
         }
     }
-    if (QJL) {
+
+    if (QJL && wave < QD / 16) {
         // GQ (rows x 64) = Q (rows x 128) . G_h^T on MFMA, one 16-column block
         // per wave: Q as fp16 hi + lo, G rows expanded 8 bits at a time
         // through the sign LUT.
-        for (int cb = wave; cb < QD / 16; cb += nw) {
-            half8_t ah[4], al[4];
+        const int cb = wave;
+        half8_t ah[4], al[4];
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                uint32_t hw[4], lw[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float v0 = n < kDecRows ? qs[n * D + 32 * s + 8 * g + 2 * j] : 0.0f;
-                    const float v1 = n < kDecRows ? qs[n * D + 32 * s + 8 * g + 2 * j + 1] : 0.0f;
-                    hw[j] = pack_h2(v0, v1);
-                    lw[j] = pack_h2(v0 - f16_to_f32(f32_to_f16_rne(v0)), v1 - f16_to_f32(f32_to_f16_rne(v1)));
-                }
-                ah[s] = as_half8(hw[0], hw[1], hw[2], hw[3]);
-                al[s] = as_half8(lw[0], lw[1], lw[2], lw[3]);
+        for (int s = 0; s < 4; ++s) {
+            uint4 hv = make_uint4(0u, 0u, 0u, 0u), lv = hv;
+            if (n < kDecRows) {
+                const uint4 *src = reinterpret_cast<const uint4 *>(smem + kDecGaOff + (n * 16 + 4 * s + g) * 32);
+                hv = src[0];
+                lv = src[1];
             }
-            float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
-            const int o = 16 * cb + n;
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const uint32_t word = cb == wave ? gw0[s] : gh[o * 4 + s];
-                const uint32_t byte = (word >> (8 * g)) & 0xffu;
-                const uint4 gv = *reinterpret_cast<const uint4 *>(smem + kSlutOff + byte * 16u);
-                const half8_t bg = as_half8(gv.x, gv.y, gv.z, gv.w);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[s], bg, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[s], bg, acc, 0, 0, 0);
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (4 * g + i < kDecRows) gq[(4 * g + i) * QD + o] = acc[i];
+            ah[s] = as_half8(hv.x, hv.y, hv.z, hv.w);
+            al[s] = as_half8(lv.x, lv.y, lv.z, lv.w);
         }
+        float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
+        const int o = 16 * cb + n;
+        const uint32_t gws[4] = {gw.x, gw.y, gw.z, gw.w};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const uint32_t byte = (gws[s] >> (8 * g)) & 0xffu;
+            const uint4 gv = *reinterpret_cast<const uint4 *>(smem + kSlutOff + byte * 16u);
+            const half8_t bg = as_half8(gv.x, gv.y, gv.z, gv.w);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[s], bg, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[s], bg, acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (4 * g + i < kDecRows) gq[(4 * g + i) * QD + o] = acc[i];
     }
     __syncthreads();
 
@@ -742,26 +806,20 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     half8_t bk[8], bgq[2];
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-        // slots: [hi d0 d1 | lo d0 d1 | hi d2 d3 | lo d2 d3], d0 = 32g + 4s
-        const float *row = qs + rn * D + 32 * g + 4 * s;
-        float h[4], l[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            h[j] = row[j] * a.qscale;
-            l[j] = h[j] - f16_to_f32(f32_to_f16_rne(h[j]));
-        }
-        if (lo_col)
-            bk[s] = as_half8(pack_h2(l[0], l[1]), 0u, pack_h2(l[2], l[3]), 0u);
-        else
-            bk[s] = as_half8(pack_h2(h[0], h[1]), pack_h2(h[0], h[1]), pack_h2(h[2], h[3]), pack_h2(h[2], h[3]));
+        // quad 8g + s of row rn: columns 0-7 take the hi image, 8-15 the lo image
+        const uint4 v = *reinterpret_cast<const uint4 *>(smem + kDecBkOff + ((rn * 32 + 8 * g + s) * 2 + (lo_col ? 1 : 0)) * 16);
+        bk[s] = as_half8(v.x, v.y, v.z, v.w);
     }
+    // QJL B operand carries scale * log2(e) * sqrt(2/pi) / D, so a score
+    // needs only norm * (signs . B)
+    const float gscale = a.qscale * a.alpha_c;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
         uint32_t w[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const float *row = gq + rn * QD + 32 * s + 8 * g + 2 * j;
-            w[j] = (!lo_col && QJL) ? pack_h2(row[0] * a.qscale, row[1] * a.qscale) : 0u;
+            w[j] = (!lo_col && QJL) ? pack_h2(row[0] * gscale, row[1] * gscale) : 0u;
         }
         bgq[s] = as_half8(w[0], w[1], w[2], w[3]);
     }
@@ -774,7 +832,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     // tiles ending at or below min(s_end, first masked key of any row) need no masks
     const int64_t min_limit64 = (a.causal_offset >= 0) ? a.causal_offset + (rc * kDecRows) / a.G : INT64_MAX;
     const int full_end = (int)imin64((int64_t)s_end, min_limit64 + 1);
-    const uint32_t laneoff = (uint32_t)(lane & (ncopy - 1)) * 8u;
+    const uint32_t laneoff = (uint32_t)(lane & 31) * 8u;
     // ones on the hi slots of each (hi, lo) pair: sums every token's P once
     const half8_t ones = as_half8(0x3C003C00u, 0u, 0x3C003C00u, 0u);
     const unsigned char *lut = smem + kLutOff;
@@ -804,16 +862,19 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
             if (QJL) {
 #pragma unroll
                 for (int s = 0; s < 2; ++s) {
-                    const uint32_t byte = ((s ? R.sg[u].y : R.sg[u].x) >> (8 * g)) & 0xffu;
-                    const uint4 sv = *reinterpret_cast<const uint4 *>(smem + kSlutOff + byte * 16u);
+                    // LDS address kSlutOff | byte << 4 (kSlutOff is a power of two above 4K)
+                    const uint32_t byte = __builtin_amdgcn_ubfe(s ? R.sg[u].y : R.sg[u].x, 8u * g, 8u);
+                    const uint4 sv = *reinterpret_cast<const uint4 *>(smem + ((byte << 4) | (uint32_t)kSlutOff));
                     qacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(sv.x, sv.y, sv.z, sv.w), bgq[s], qacc, 0, 0, 0);
                 }
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
+                // columns 8-15 compute finite junk that never reaches
+                // columns 0-7 (MFMA columns are independent) nor the output
                 float v = acc[i] + dpp_row_shl8(acc[i]);
-                if (QJL) v = __builtin_fmaf(R.nr[u][i] * a.alpha_c, qacc[i], v);
-                sc[4 * u + i] = lo_col ? -INFINITY : v;
+                if (QJL) v = __builtin_fmaf(R.nr[u][i], qacc[i], v);
+                sc[4 * u + i] = v;
             }
         }
         if (!full) {
@@ -827,7 +888,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
         }
 
         // online softmax (exp2 domain), lazy rescale
-        float mt = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+        float mt = fmaxf(fmaxf(fmaxf(fmaxf(sc[0], sc[1]), sc[2]), fmaxf(fmaxf(sc[3], sc[4]), sc[5])), fmaxf(sc[6], sc[7]));
         mt = max_over_groups(mt);
         const bool need = mt > m_run + 8.0f;
         if (__builtin_amdgcn_ballot_w64(need)) {
@@ -855,8 +916,8 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
 #pragma unroll
             for (int pr = 0; pr < 2; ++pr) {
                 const uint32_t va = R.v[4 * u + 2 * pr], vb = R.v[4 * u + 2 * pr + 1];
-                ev[pr] = (va & 0x0F0F0F0Fu) | ((vb & 0x0F0F0F0Fu) << 4);
-                od[pr] = ((va >> 4) & 0x0F0F0F0Fu) | (vb & 0xF0F0F0F0u);
+                ev[pr] = ((vb << 4) & 0xF0F0F0F0u) | (va & 0x0F0F0F0Fu);
+                od[pr] = (vb & 0xF0F0F0F0u) | ((va >> 4) & 0x0F0F0F0Fu);
             }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -968,8 +1029,8 @@ static Plan make_plan(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int D) {
         const int64_t tps = (tiles + splits - 1) / splits;
         p.splits = (int)splits;
         p.split_len = tps * kDecTile;
-        p.nw = (int)clamp64(tps, 1, kDecWaves);
-        p.ncopy = tps >= 32 ? 32 : (tps >= 8 ? 8 : 1);
+        p.nw = kDecWaves;          // one query row per wave in the prologue
+        p.ncopy = 32;
         p.lds = kDecLdsBytes;
     } else {
         const int64_t tiles = (S + kTile - 1) / kTile;
