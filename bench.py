@@ -7,7 +7,7 @@ tokens, 32 q heads / 8 kv heads, head_dim 128, one bf16 query per
 sequence, QJL on, query rotation (sign-flipped WHT) applied in-kernel.
 A step is one attention call over the whole batch; `value` is algorithmic
 bytes per call (140 B per cached (token, kv head) + q + out) / wall time per
-call with inputs resident in HBM.
+call with inputs resident in HBM (K back-to-back calls).
 
 Also reported (extra keys): C2 serving (B=64, S=50, 32q/8kv, 256-adapter
 rank-8 LoRA gather on Q) p50/p99 latency and users/s; C4 encode GB/s
@@ -66,23 +66,61 @@ def make_cache(B, Hkv, S, D, dev, seed, uid, cb, sign):
     return kn, kq, kr, vn
 
 
-def timed(fn, steps, warmup, stream):
-    """Wall time over `steps` back-to-back calls (synchronized both sides) and
-    per-call HIP event durations on the launch stream."""
+def per_call_events(fn, steps, warmup, stream):
+    """Eager calls, each bracketed by HIP events on the launch stream; returns
+    the per-call device durations (s)."""
     import torch
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-    t0 = time.perf_counter()
     for s, e in evs:
         s.record(stream)
         fn()
         e.record(stream)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    per = [s.elapsed_time(e) * 1e-3 for s, e in evs]
-    return wall, per
+    return [s.elapsed_time(e) * 1e-3 for s, e in evs]
+
+
+def wall_eager(fn, steps, warmup):
+    """Wall time per call over `steps` back-to-back eager calls (synchronized
+    on both sides, no per-call events)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def wall_graph(fn, steps, warmup):
+    """The `steps` calls captured once as a HIP graph (every call reads inputs
+    already in HBM and enqueues its kernels; no allocation or memset inside),
+    replayed once untimed, then once timed between two synchronizations.
+    Returns the wall time per call."""
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(max(1, warmup)):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(steps):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    g.replay()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    del g
+    return dt
 
 
 def cpu_baseline_c3(kn, kq, kr, vn, cb, q, sign, uid, budget_s):
@@ -159,13 +197,17 @@ def main() -> int:
     att = PackedKVAttention(kn, kq, kr, vn, cb, n_heads=Hq, user_id=uid, rotate_q=True, sign_flip=sign)
     bytes_step = B * Hkv * S * BYTES_PER_TOKEN_HEAD + q.numel() * 2 + B * Hq * D * 4 + Hkv * 16 * 4 + Hkv * 64 * 16
     log(f"[bench] C3: timing {args.steps} steps (warmup {args.warmup}); split-K workspace {att.ws_bytes} B")
-    wall, per = timed(lambda: att.run(q), args.steps, args.warmup, stream)
-    t_step = wall / args.steps
+    # One call is long enough that back-to-back eager launches keep the GPU
+    # busy; `value` uses them (a graph of the same steps is reported too).
+    step = lambda: att.run(q)
+    t_step = wall_eager(step, args.steps, args.warmup)
+    t_graph = wall_graph(step, args.steps, args.warmup)
+    per = per_call_events(step, args.steps, 2, stream)
     value = bytes_step / t_step / 1e9
     ev_mean = statistics.fmean(per)
     achieved = bytes_step / ev_mean / 1e9
-    log(f"[bench] C3: {t_step * 1e6:.1f} us/step wall, {ev_mean * 1e6:.1f} us/call events -> "
-        f"{value:.0f} GB/s ({value / HBM_PEAK_GBS:.1%} of peak)")
+    log(f"[bench] C3: {t_step * 1e6:.1f} us/step (eager), {t_graph * 1e6:.1f} us/step (graph), "
+        f"{ev_mean * 1e6:.1f} us/call (events) -> {value:.0f} GB/s ({value / HBM_PEAK_GBS:.1%} of peak)")
 
     c3_traffic = round(1024 * (C3_TRAFFIC["fetch_kib"] * C3_TRAFFIC["fetch_scale"]
                                 + C3_TRAFFIC["write_kib"] * C3_TRAFFIC["write_scale"]))
@@ -184,7 +226,8 @@ def main() -> int:
         "data": "synthetic",
         "config": {"workload": "C3 decode: 32 seq x 8192 cached tokens, 32 q / 8 kv heads, head_dim 128, "
                                "INT4 Lloyd-Max + 1-bit QJL K, INT4 V, bf16 query, rotate_q in-kernel",
-                   "bytes_per_step": bytes_step, "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2)},
+                   "bytes_per_step": bytes_step, "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+                   "launch": "K back-to-back eager calls", "graph_us_per_step": round(t_graph * 1e6, 2)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": c3_traffic,
                      "kernel": "omni::attn_decode128_kernel (+ attn_combine_kernel<128> when split-K)",
@@ -202,18 +245,21 @@ def main() -> int:
         ids = torch.randint(0, L2, (B2,), generator=torch.Generator().manual_seed(45), dtype=torch.int32).to(dev)
         xh = torch.randn(B2, 1, HID, generator=g2, device=dev).to(torch.bfloat16)
         q2 = torch.randn(B2, Hq, 1, D, generator=g2, device=dev).to(torch.bfloat16)
-        att2 = PackedKVAttention(kn2, kq2, kr2, vn2, cb, n_heads=Hq, user_id=uid, rotate_q=True, sign_flip=sign)
-        serve = lambda: att2.run(_apply_lora_to_q(q2, xh, la, lb, ids, 1.0, validate=False))
+        att2 = PackedKVAttention(kn2, kq2, kr2, vn2, cb, n_heads=Hq, user_id=uid, rotate_q=True, sign_flip=sign,
+                                 lora_a=la, lora_b=lb, lora_alpha=1.0)
+        serve = lambda: att2.run(q2, xh, ids)
         steps2 = max(args.steps, 100)
-        wall2, per2 = timed(serve, steps2, args.warmup, stream)
+        per2 = per_call_events(serve, steps2, args.warmup, stream)
+        t2 = wall_graph(serve, steps2, args.warmup)
         per2s = sorted(per2)
         p50, p99 = per2s[len(per2s) // 2], per2s[min(len(per2s) - 1, int(0.99 * len(per2s)))]
         result["serving_c2"] = {"p50_us": round(p50 * 1e6, 2), "p99_us": round(p99 * 1e6, 2),
-                                "users_per_s_gpu": round(B2 / statistics.fmean(per2), 1),
-                                "users_per_s_wall": round(B2 * steps2 / wall2, 1),
-                                "note": "per-call GPU latency from HIP events (LoRA kernel + attention)"}
-        log(f"[bench] C2: p50 {p50 * 1e6:.1f} us p99 {p99 * 1e6:.1f} us, "
-            f"{B2 / statistics.fmean(per2):.0f} users/s (GPU), {B2 * steps2 / wall2:.0f} users/s (wall)")
+                                "users_per_s": round(B2 / t2, 1),
+                                "us_per_step_graph": round(t2 * 1e6, 2),
+                                "note": "one step = LoRA gather-apply + rotate_q + decode attention for 64 users; "
+                                        "p50/p99 from HIP events per eager call, users/s from a HIP graph of steps"}
+        log(f"[bench] C2: p50 {p50 * 1e6:.1f} us p99 {p99 * 1e6:.1f} us (events), "
+            f"{t2 * 1e6:.1f} us/step graph -> {B2 / t2:.0f} users/s")
 
         B4, T4 = 16, 4096
         log("[bench] C4: encode 16 x 4096 x 8 K and V")
@@ -221,10 +267,9 @@ def main() -> int:
         k4 = torch.randn(B4, Hkv, T4, D, generator=g4, device=dev).to(torch.bfloat16)
         v4 = torch.randn(B4, Hkv, T4, D, generator=g4, device=dev).to(torch.bfloat16)
         enc = lambda: (encode_kv(k4, cb, user_id=uid, sign_flip=sign), encode_kv(v4, cb, user_id=uid, sign_flip=sign))
-        wall4, per4 = timed(enc, max(5, args.steps // 5), 2, stream)
+        t4 = wall_eager(enc, max(5, args.steps // 5), 2)
         rows = 2 * B4 * Hkv * T4
         bytes4 = rows * (D * 2 + 64 + 8 + 4)
-        t4 = wall4 / max(5, args.steps // 5)
         result["encode_c4"] = {"GB_s": round(bytes4 / t4 / 1e9, 1), "us_per_call": round(t4 * 1e6, 1),
                                "bytes": bytes4, "pct_of_hbm_peak": round(100 * bytes4 / t4 / 1e9 / HBM_PEAK_GBS, 2)}
         log(f"[bench] C4: {t4 * 1e6:.0f} us -> {bytes4 / t4 / 1e9:.0f} GB/s")

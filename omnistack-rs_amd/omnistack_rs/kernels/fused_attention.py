@@ -181,14 +181,20 @@ class PackedKVAttention:
     Validates shapes, converts codebooks, uploads G and allocates the output
     and split-K workspace once; ``run(q)`` then enqueues a single
     ``omni_attn`` on the current stream and returns the (reused) float32
-    output buffer.  Safe to capture in a HIP graph (no allocation, no host
-    sync, no memset inside ``run``).
+    output buffer.  With a LoRA bank (``lora_a``, ``lora_b``, ``lora_alpha``)
+    ``run(q, x, lora_indices)`` first enqueues ``omni_lora_apply`` into a
+    preallocated q buffer (the semantics of ``_apply_lora_to_q``; indices are
+    not range-checked on the host, an index past the bank gives NaN rows).
+    Safe to capture in a HIP graph (no allocation, no host sync, no memset
+    inside ``run``).
     """
 
     def __init__(self, k_nibbles, k_qjl, k_norms, v_nibbles, codebooks, n_heads: int, q_tokens: int = 1,
                  user_id: int = 0, scale: Optional[float] = None, with_qjl: bool = True,
                  q_dtype: torch.dtype = torch.bfloat16, rotate_q: bool = False,
-                 sign_flip: Optional[torch.Tensor] = None, causal_offset: Optional[int] = None):
+                 sign_flip: Optional[torch.Tensor] = None, causal_offset: Optional[int] = None,
+                 lora_a: Optional[torch.Tensor] = None, lora_b: Optional[torch.Tensor] = None,
+                 lora_alpha: float = 1.0):
         B, Hkv, S, nb = k_nibbles.shape
         D = 2 * nb
         if n_heads % Hkv:
@@ -219,11 +225,48 @@ class PackedKVAttention:
                       -1 if causal_offset is None else int(causal_offset), int(rotate_q), _lib.ptr(self.sf),
                       _lib.ptr(self.out), _lib.ptr(self.ws), self.ws_bytes)
         self._qcode = _lib.dtype_code(q_dtype)
+        self.lora = None
+        if (lora_a is None) != (lora_b is None):
+            raise ValueError("lora_a and lora_b must be given together")
+        if lora_a is not None:
+            n_loras, rank, hidden = lora_a.shape
+            if tuple(lora_b.shape) != (n_loras, n_heads * D, rank):
+                raise ValueError(f"lora_b must be ({n_loras}, {n_heads * D}, {rank}), got {tuple(lora_b.shape)}")
+            wdt = torch.promote_types(lora_a.dtype, lora_b.dtype)
+            if wdt not in _lib.DTYPE_CODE:
+                wdt = torch.float32
+            self._la = lora_a.to(device=dev, dtype=wdt).contiguous()
+            self._lb = lora_b.to(device=dev, dtype=wdt).contiguous()
+            self.q_eff = torch.empty(self.shape, dtype=q_dtype, device=dev)
+            self.lora = (n_loras, rank, hidden, wdt)
+            self._lora_fn = L.omni_lora_apply
+            self._lora_tail = (_lib.ptr(self._la), _lib.ptr(self._lb), _lib.dtype_code(wdt))
+            self._lora_shape = (B, n_heads, q_tokens, D, hidden, rank, n_loras, float(lora_alpha),
+                                _lib.ptr(self.q_eff))
 
-    def run(self, q: torch.Tensor) -> torch.Tensor:
+    def run(self, q: torch.Tensor, x: Optional[torch.Tensor] = None,
+            lora_indices: Optional[torch.Tensor] = None) -> torch.Tensor:
         if tuple(q.shape) != self.shape or q.dtype != self.q_dtype or not q.is_contiguous():
             raise ValueError(f"q must be a contiguous {self.q_dtype} tensor of shape {self.shape}")
-        rc = self._fn(q.data_ptr(), self._qcode, *self._args, torch.cuda.current_stream(self.device).cuda_stream)
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        qp = q.data_ptr()
+        if x is not None:
+            if self.lora is None:
+                raise ValueError("run(q, x, ...) needs a LoRA bank at construction")
+            n_loras, rank, hidden, wdt = self.lora
+            B, Hq, T, D = self.shape
+            if tuple(x.shape) != (B, T, hidden) or x.dtype != wdt or not x.is_contiguous():
+                raise ValueError(f"x must be a contiguous {wdt} tensor of shape {(B, T, hidden)}")
+            if (lora_indices is None or lora_indices.dtype != torch.int32 or lora_indices.numel() != B
+                    or not lora_indices.is_contiguous()):
+                raise ValueError(f"lora_indices must be a contiguous int32 tensor of {B} entries")
+            la, lb, wcode = self._lora_tail
+            rc = self._lora_fn(qp, self._qcode, x.data_ptr(), la, lb, wcode, lora_indices.data_ptr(),
+                               *self._lora_shape, stream)
+            if rc:
+                _lib.check(rc)
+            qp = self.q_eff.data_ptr()
+        rc = self._fn(qp, self._qcode, *self._args, stream)
         if rc:
             _lib.check(rc)
         return self.out

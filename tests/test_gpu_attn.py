@@ -177,3 +177,58 @@ def test_attn_rejects_bad_shapes(device):
         _run(device, torch.randn(1, 3, 1, 128), kn, kq, kr, vn, cb, 0)
     with pytest.raises(ValueError):
         _run(device, torch.randn(1, 4, 1, 128), kn, kq, kr, vn[:, :, :8], cb, 0)
+
+
+def _prepared(device, B=4, Hq=32, Hkv=8, S=300, uid=9, L=16, rank=8, hidden=128):
+    from omnistack_rs.kernels.fused_attention import PackedKVAttention
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=40, user_id=uid)
+    a, b = _data.lora_bank(L, rank, hidden, Hq * 128, seed=41)
+    a, b = a.to(torch.bfloat16), b.to(torch.bfloat16)
+    s = _data.sign_flip()
+    att = PackedKVAttention(*(t.to(device) for t in (kn, kq, kr, vn, cb)), n_heads=Hq, user_id=uid,
+                            rotate_q=True, sign_flip=s.to(device), lora_a=a.to(device), lora_b=b.to(device),
+                            lora_alpha=0.75)
+    q = _data.query((B, Hq, 1, 128), seed=42).to(device)
+    x = torch.randn(B, 1, hidden, generator=_data.gen(43)).to(torch.bfloat16).to(device)
+    ids = _data.lora_ids(B, L).to(device)
+    ids[1] = -1
+    return att, (kn, kq, kr, vn, cb, s, a, b), q, x, ids
+
+
+def test_prepared_lora_matches_omni_attn(device):
+    from omnistack_rs.kernels.fused_attention import omni_attn
+    att, (kn, kq, kr, vn, cb, s, a, b), q, x, ids = _prepared(device)
+    got = att.run(q, x, ids).clone()
+    want = omni_attn(q, *(t.to(device) for t in (kn, kq, kr, vn, cb)), user_id=9, x=x, lora_a=a.to(device),
+                     lora_b=b.to(device), lora_indices=ids, lora_alpha=0.75, rotate_q=True, sign_flip=s.to(device))
+    assert torch.equal(got, want)
+    # and against the CPU oracle: LoRA in fp32 then bf16, rotation, reference attention
+    q_eff = restate.apply_lora_to_q(q.cpu(), x.cpu(), a, b, ids.cpu(), 0.75)
+    ref = restate.fused_attn_python(restate.rotate(q_eff, s).float(), kn, kq, kr, vn, cb, 9, 1 / math.sqrt(128), True)
+    _assert_close(got, ref, "prepared lora")
+
+
+def test_prepared_run_replays_in_hip_graph(device):
+    """One LoRA + attention step captured in a HIP graph: every replay, with
+    eager work and host syncs between replays, equals the eager result."""
+    att, _, q, x, ids = _prepared(device)
+    eager = att.run(q, x, ids).clone()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        att.run(q, x, ids)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        att.run(q, x, ids)
+    other = _data.query(tuple(q.shape), seed=44).to(device)
+    for i in range(4):
+        att.out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(att.out, eager), f"replay {i} differs from the eager result"
+        att.run(other, x, ids)                        # eager work between replays
+        torch.cuda.synchronize()
