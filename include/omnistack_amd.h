@@ -77,6 +77,7 @@ int omni_wht_rotate(const void *x, int dtype, int64_t rows, int head_dim,
  *   bit_i   = [sum_j G_h[i][j] e_j >= 0] (exact sign), packed LSB-first
  * codebooks: (H,16) when per_head_codebook, else (16,).
  * g_bits: (H, D/2, D/32) words for seeds (user_id % 1024) ^ h.
+ * workspace: omni_encode_workspace_size(...) bytes of device memory.
  * Replaces quantize_heads (omnistack_rs/kernels/quantize.py:542-590) and,
  * with rotate=1, the bake's _wht_torch + quantize_heads
  * (scripts/run_criteo_benchmark.py:355, :367).
@@ -85,7 +86,17 @@ int omni_encode(const void *x, int x_dtype, int64_t B, int H, int64_t T, int hea
                 int rotate, const int8_t *sign_flip,
                 const float *codebooks, int per_head_codebook,
                 const uint32_t *g_bits,
-                uint8_t *nibbles, uint8_t *qjl, float *norms, void *stream);
+                uint8_t *nibbles, uint8_t *qjl, float *norms,
+                void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * Device workspace bytes omni_encode needs for these arguments (0: none).
+ * 16-bit inputs at head_dim 128 use one 64 KB code table per codebook
+ * (value bits -> code), rebuilt by every call; OMNI_EWORKSPACE if absent.
+ * No reference counterpart (the reference encoder runs on the CPU).
+ */
+size_t omni_encode_workspace_size(int64_t B, int H, int64_t T, int head_dim, int x_dtype,
+                                  int per_head_codebook);
 
 /*
  * Dequantize packed rows to f32 (B, H, T, D):

@@ -232,6 +232,465 @@ __global__ __launch_bounds__(kRowsPerBlock) void encode_kernel(
     norms[row] = nrm;
 }
 
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t cvt_pk_f16(float x, float y) {
+    typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+    typedef float f2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2_t){x, y}, h2_t));
+}
+
+// ── fast encoder: 16-bit input, D = 128 ─────────────────────────────────
+//
+// Same contract as encode_kernel, organised for gfx950:
+//   * 16 rows per wave-iteration; lane (n, g) holds elements 32 s + 8 g + i
+//     (s < 4, i < 8) of row n.  The WHT runs in registers (h = 1, 2, 4, 32,
+//     64) and by paired v_permlane16/32_swap butterflies (h = 8, 16), in the
+//     reference stage order with the reference's fp32 operations.
+//   * Codes come from a 64 KB LDS table indexed by the rotated value's
+//     16-bit pattern, built exactly (brute-force first-index argmin with the
+//     NaN rule) by code_table_kernel into the caller's workspace.
+//   * QJL projections P = E G^T on v_mfma_f32_16x16x32_bf16: each residual
+//     is split exactly into three truncated bf16 parts (8 + 8 + 8 bits), G is
+//     exactly +-1, so the only error is fp32 accumulation, bounded by
+//     1024 * 2^-24 * sum|e| (+ 2^-100 for flushed denormals).  Signs outside
+//     the bound are certain; the rare rest are recomputed in fp64 with
+//     compensated sums.  Rows with a non-finite residual take the
+//     order-free sign of the reference's fp32 sum (NaN if it meets NaN or
+//     both infinities, else the sign of the infinity).
+//   * With A = G rows and B = the residual rows, lane (n, g) receives
+//     P[n][16 cb + 4 g + i]: every value a lane needs for its row is local
+//     or one 4-lane reduction away.
+
+constexpr int kEncWaves = 8;
+constexpr int kEncTab = 65536;                            // u8 code table (both nibbles = code)
+constexpr int kEncCentOff = kEncTab;                      // f32 centroid by table byte (256 slots)
+constexpr int kEncGimgOff = kEncCentOff + 256 * 4;        // [cb][s][lane] uint4: 8 bf16 +-1 of G
+constexpr int kEncGbitsOff = kEncGimgOff + 4 * 4 * 64 * 16;   // G rows as bits, 64 x 4 words
+constexpr int kEncFlipOff = kEncGbitsOff + 64 * 4 * 4;       // [lane][16] u32: sign-bit xor of the raw 16-bit words
+constexpr int kEncStageOff = kEncFlipOff + 64 * 16 * 4;      // [wave][16 rows][128] f32 residuals (rare paths)
+constexpr int kEncLdsBytes = kEncStageOff + kEncWaves * 16 * 128 * 4;
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+
+struct EncArgs {
+    const void *x;
+    const uint8_t *table;        // n_tables x 65536
+    const float *codebooks;
+    const uint32_t *g_bits;
+    const int8_t *sign_flip;
+    uint8_t *nibbles, *qjl;
+    float *norms;
+    int64_t T, nrows_head, rows_per_block;
+    int H, per_head, rotate;
+    float scale;
+};
+
+template <int XDT>
+__global__ __launch_bounds__(256) void code_table_kernel(const float *codebooks, int per_head, uint8_t *table) {
+    const int h = blockIdx.y;
+    const uint32_t u = blockIdx.x * 256u + threadIdx.x;
+    const float v = XDT == OMNI_BF16 ? bf16_to_f32((uint16_t)u) : f16_to_f32((uint16_t)u);
+    const float *cbp = codebooks + (per_head ? h * 16 : 0);
+    float cb[16];
+    bool cb_nan = false;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) { cb[k] = cbp[k]; cb_nan |= (cb[k] != cb[k]); }
+    float best = fabsf(v - cb[0]);
+    int code = 0;
+#pragma unroll
+    for (int k = 1; k < 16; ++k) {
+        const float dk = fabsf(v - cb[k]);
+        bool take = dk < best;
+        if (cb_nan) take = take || ((dk != dk) && (best == best));
+        best = take ? dk : best;
+        code = take ? k : code;
+    }
+    table[(int64_t)h * kEncTab + u] = (uint8_t)(code | (code << 4));
+}
+
+// (a, b) <- butterfly with the partner lane across bit 4 (row parity) or 5
+// (half): lanes with the bit clear hold the lower element of each pair.
+// Two swaps and one add/sub pair cover two elements.
+template <int HALF>
+__device__ __forceinline__ void xlane_pair_butterfly(float &a, float &b) {
+    uint32_t t0, t1, u0, u1;
+    if constexpr (HALF == 16) {
+        const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+        t0 = t[0]; t1 = t[1];
+    } else {
+        const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+        t0 = t[0]; t1 = t[1];
+    }
+    const float lo = __uint_as_float(t0), hi = __uint_as_float(t1);
+    const float s = lo + hi, d = lo - hi;
+    if constexpr (HALF == 16) {
+        const auto u = __builtin_amdgcn_permlane16_swap(__float_as_uint(s), __float_as_uint(d), false, false);
+        u0 = u[0]; u1 = u[1];
+    } else {
+        const auto u = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(d), false, false);
+        u0 = u[0]; u1 = u[1];
+    }
+    a = __uint_as_float(u0);
+    b = __uint_as_float(u1);
+}
+
+template <int HALF>
+__device__ __forceinline__ double xlane_sum_f64(double v) {
+    const uint64_t bits = __builtin_bit_cast(uint64_t, v);
+    uint32_t lo = (uint32_t)bits, hi = (uint32_t)(bits >> 32), plo, phi;
+    if constexpr (HALF == 16) {
+        const auto a = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+        const auto b = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+        const bool odd = (__lane_id() & 16) != 0;
+        plo = odd ? a[0] : a[1];
+        phi = odd ? b[0] : b[1];
+    } else {
+        const auto a = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+        const auto b = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+        const bool up = (__lane_id() & 32) != 0;
+        plo = up ? a[0] : a[1];
+        phi = up ? b[0] : b[1];
+    }
+    return v + __builtin_bit_cast(double, ((uint64_t)phi << 32) | plo);
+}
+
+template <int HALF>
+__device__ __forceinline__ uint32_t xlane_u32(uint32_t v) {
+    if constexpr (HALF == 16) {
+        const auto a = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (__lane_id() & 16) ? a[0] : a[1];
+    } else {
+        const auto a = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (__lane_id() & 32) ? a[0] : a[1];
+    }
+}
+
+__device__ __forceinline__ float xlane_sum_f32(float v) {
+    v += __uint_as_float(xlane_u32<16>(__float_as_uint(v)));
+    return v + __uint_as_float(xlane_u32<32>(__float_as_uint(v)));
+}
+
+// sum over this lane's 32 elements of s_j e_j in fp64 (Neumaier), for G row
+// `grow` (4 words); `row` is the residual row staged in LDS.  The 4 lanes of
+// a row then combine their (sum, compensation) pairs.
+__device__ __noinline__ double exact_partial(const float *row, const uint32_t *grow, int g, double &comp) {
+    double s = 0.0, c = 0.0;
+#pragma unroll 1
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t byte = (grow[q] >> (8 * g)) & 0xffu;
+#pragma unroll 1
+        for (int i = 0; i < 8; ++i) {
+            double y = (double)row[32 * q + 8 * g + i];
+            y = ((byte >> i) & 1u) ? y : -y;
+            const double t = s + y;
+            c += (fabs(s) >= fabs(y)) ? ((s - t) + y) : ((y - t) + s);
+            s = t;
+        }
+    }
+    comp = c;
+    return s;
+}
+
+// order-free classes of this lane's 32 terms s_j e_j: 1 NaN, 2 +inf, 4 -inf
+__device__ __noinline__ uint32_t nonfinite_flags(const float *row, const uint32_t *grow, int g) {
+    uint32_t fl = 0u;
+#pragma unroll 1
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t byte = (grow[q] >> (8 * g)) & 0xffu;
+#pragma unroll 1
+        for (int i = 0; i < 8; ++i) {
+            const float e = row[32 * q + 8 * g + i];
+            const float y = ((byte >> i) & 1u) ? e : -e;
+            fl |= (y != y) ? 1u : (y == INFINITY ? 2u : (y == -INFINITY ? 4u : 0u));
+        }
+    }
+    return fl;
+}
+
+template <int XDT>
+__global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
+    __shared__ __attribute__((aligned(16))) unsigned char smem[kEncLdsBytes];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n = lane & 15, g = lane >> 4;
+    const int h = blockIdx.y;
+    const int64_t v_begin = (int64_t)blockIdx.x * a.rows_per_block;
+    const int64_t v_end = v_begin + a.rows_per_block < a.nrows_head ? v_begin + a.rows_per_block : a.nrows_head;
+
+    // ── prologue: code table, centroids, G bits and bf16 images ───────
+    {
+        const uint4 *src = reinterpret_cast<const uint4 *>(a.table + (int64_t)(a.per_head ? h : 0) * kEncTab);
+        uint4 *dst = reinterpret_cast<uint4 *>(smem);
+#pragma unroll
+        for (int k = 0; k < kEncTab / 16 / (64 * kEncWaves); ++k) dst[tid + k * 64 * kEncWaves] = src[tid + k * 64 * kEncWaves];
+    }
+    const float *cbp = a.codebooks + (a.per_head ? h * 16 : 0);
+    if (tid < 16) reinterpret_cast<float *>(smem + kEncCentOff)[tid | (tid << 4)] = cbp[tid];
+    const uint32_t *gh = a.g_bits + (int64_t)h * 64 * 4;
+    if (tid < 256) reinterpret_cast<uint32_t *>(smem + kEncGbitsOff)[tid] = gh[tid];
+    for (int m = tid; m < 4 * 4 * 64; m += 64 * kEncWaves) {
+        const int cb = m >> 8, s = (m >> 6) & 3, l = m & 63;
+        const uint32_t byte = (gh[(16 * cb + (l & 15)) * 4 + s] >> (8 * (l >> 4))) & 0xffu;
+        uint32_t w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            w[k] = (((byte >> (2 * k)) & 1u) ? 0x3F80u : 0xBF80u) | ((((byte >> (2 * k + 1)) & 1u) ? 0x3F80u : 0xBF80u) << 16);
+        reinterpret_cast<uint4 *>(smem + kEncGimgOff)[m] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+    // sign flip as an xor on the raw 16-bit words: word j of chunk (s, g)
+    // holds elements 32 s + 8 g + 2 j (low half) and + 1 (high half)
+    for (int k = tid; k < 64 * 16; k += 64 * kEncWaves) {
+        const int l = k >> 4, q = k & 15, sq = q >> 2, j = q & 3;
+        uint32_t m = 0u;
+        if (a.rotate && a.sign_flip) {
+            const int e0 = 32 * sq + 8 * (l >> 4) + 2 * j;
+            m = (a.sign_flip[e0] < 0 ? 0x8000u : 0u) | (a.sign_flip[e0 + 1] < 0 ? 0x80000000u : 0u);
+        }
+        reinterpret_cast<uint32_t *>(smem + kEncFlipOff)[k] = m;
+    }
+    __syncthreads();
+
+    const unsigned char *tab = smem;
+    const float *cent = reinterpret_cast<const float *>(smem + kEncCentOff);
+    const uint32_t *gbits = reinterpret_cast<const uint32_t *>(smem + kEncGbitsOff);
+
+    for (int64_t v0 = v_begin + 16 * wave; v0 < v_end; v0 += 16 * kEncWaves) {
+        // row of lane n: virtual v = v0 + n (clamped) -> (b, t) -> memory row
+        const int64_t b0 = v0 / a.T;                         // uniform
+        int64_t t = (v0 - b0 * a.T) + (v0 + n < v_end ? n : (v_end - 1 - v0));
+        int64_t bq = b0;
+        while (t >= a.T) { t -= a.T; ++bq; }                 // at most 16 / T + 1 steps
+        const int64_t mrow = (bq * a.H + h) * a.T + t;
+        const bool store = v0 + n < v_end && g == 0;
+
+        // load (8 x 16-bit per chunk), flip signs on the raw words, widen
+        float x[4][8];
+        uint32_t nib[4];
+        double ss = 0.0;
+        float as = 0.0f;
+        {
+            const uint4 *src = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(a.x) + mrow * 128);
+            const uint4 *fmk = reinterpret_cast<const uint4 *>(smem + kEncFlipOff) + lane * 4;
+            uint4 w4[4];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) w4[s] = src[4 * s + g];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const uint4 f = fmk[s];
+                const uint32_t w[4] = {w4[s].x ^ f.x, w4[s].y ^ f.y, w4[s].z ^ f.z, w4[s].w ^ f.w};
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const uint32_t u = (i & 1) ? (w[i >> 1] >> 16) : (w[i >> 1] & 0xffffu);
+                    x[s][i] = XDT == OMNI_BF16 ? __uint_as_float(u << 16) : f16_to_f32((uint16_t)u);
+                }
+            }
+        }
+        if (a.rotate) {
+            // h = 1, 2, 4 inside each 8-element chunk
+#pragma unroll
+            for (int hh = 1; hh < 8; hh <<= 1)
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+#pragma unroll
+                    for (int i = 0; i < 8; ++i)
+                        if (!(i & hh)) {
+                            const float u = x[s][i], l = x[s][i + hh];
+                            x[s][i] = u + l;
+                            x[s][i + hh] = u - l;
+                        }
+            // h = 8 (lanes l ^ 16), h = 16 (lanes l ^ 32)
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int i = 0; i < 8; i += 2) xlane_pair_butterfly<16>(x[s][i], x[s][i + 1]);
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int i = 0; i < 8; i += 2) xlane_pair_butterfly<32>(x[s][i], x[s][i + 1]);
+            // h = 32 (s ^ 1), h = 64 (s ^ 2)
+#pragma unroll
+            for (int hs = 1; hs < 4; hs <<= 1)
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+                    if (!(s & hs)) {
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) {
+                            const float u = x[s][i], l = x[s + hs][i];
+                            x[s][i] = u + l;
+                            x[s + hs][i] = u - l;
+                        }
+                    }
+        }
+        // per element pair: (scale, round to the input dtype,) code from the
+        // table, residual, norm and |e| partial sums, nibble byte
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            uint32_t wn = 0u;
+#pragma unroll
+            for (int i = 0; i < 8; i += 2) {
+                uint32_t b0, b1;
+                if (a.rotate) {
+                    const float p = x[s][i] * a.scale, q = x[s][i + 1] * a.scale;
+                    uint32_t pk;
+                    if (XDT == OMNI_BF16) {
+                        typedef __bf16 bf2_t __attribute__((ext_vector_type(2)));
+                        typedef float f2_t __attribute__((ext_vector_type(2)));
+                        pk = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2_t){p, q}, bf2_t));
+                        x[s][i] = __uint_as_float(pk << 16);
+                        x[s][i + 1] = __uint_as_float(pk & 0xffff0000u);
+                    } else {
+                        pk = cvt_pk_f16(p, q);
+                        x[s][i] = f16_to_f32((uint16_t)(pk & 0xffffu));
+                        x[s][i + 1] = f16_to_f32((uint16_t)(pk >> 16));
+                    }
+                    b0 = pk & 0xffffu;
+                    b1 = pk >> 16;
+                } else if (XDT == OMNI_BF16) {
+                    b0 = __float_as_uint(x[s][i]) >> 16;
+                    b1 = __float_as_uint(x[s][i + 1]) >> 16;
+                } else {
+                    b0 = f32_to_f16_rne(x[s][i]);       // exact: the value came from f16
+                    b1 = f32_to_f16_rne(x[s][i + 1]);
+                }
+                const uint32_t t0 = tab[b0], t1 = tab[b1];
+                const float e0 = x[s][i] - cent[t0], e1 = x[s][i + 1] - cent[t1];
+                x[s][i] = e0;
+                x[s][i + 1] = e1;
+                ss += (double)__fmul_rn(e0, e0);
+                ss += (double)__fmul_rn(e1, e1);
+                as += fabsf(e0);
+                as += fabsf(e1);
+                wn |= ((t0 & 0x0Fu) | (t1 & 0xF0u)) << (4 * i);
+            }
+            nib[s] = wn;
+        }
+        ss = xlane_sum_f64<16>(ss);
+        ss = xlane_sum_f64<32>(ss);
+        as = xlane_sum_f32(as);
+
+        // projections: P^T = G . E^T on MFMA, three exact bf16 parts of E
+        float4_t acc[4];
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) acc[cb] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            uint32_t ph[4], pm[4], pl[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float e0 = x[s][2 * j], e1 = x[s][2 * j + 1];
+                const float r0 = e0 - __uint_as_float(__float_as_uint(e0) & 0xffff0000u);
+                const float r1 = e1 - __uint_as_float(__float_as_uint(e1) & 0xffff0000u);
+                const float q0 = r0 - __uint_as_float(__float_as_uint(r0) & 0xffff0000u);
+                const float q1 = r1 - __uint_as_float(__float_as_uint(r1) & 0xffff0000u);
+                ph[j] = __builtin_amdgcn_perm(__float_as_uint(e1), __float_as_uint(e0), 0x07060302u);
+                pm[j] = __builtin_amdgcn_perm(__float_as_uint(r1), __float_as_uint(r0), 0x07060302u);
+                pl[j] = __builtin_amdgcn_perm(__float_as_uint(q1), __float_as_uint(q0), 0x07060302u);
+            }
+            const bf16x8_t bh = __builtin_bit_cast(bf16x8_t, make_uint4(ph[0], ph[1], ph[2], ph[3]));
+            const bf16x8_t bm = __builtin_bit_cast(bf16x8_t, make_uint4(pm[0], pm[1], pm[2], pm[3]));
+            const bf16x8_t bl = __builtin_bit_cast(bf16x8_t, make_uint4(pl[0], pl[1], pl[2], pl[3]));
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb) {
+                const uint4 gv = reinterpret_cast<const uint4 *>(smem + kEncGimgOff)[(cb * 4 + s) * 64 + lane];
+                const bf16x8_t ga = __builtin_bit_cast(bf16x8_t, gv);
+                acc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ga, bh, acc[cb], 0, 0, 0);
+                acc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ga, bm, acc[cb], 0, 0, 0);
+                acc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ga, bl, acc[cb], 0, 0, 0);
+            }
+        }
+
+        // signs: lane (n, g) holds P[n][16 cb + 4 g + i]
+        const bool finite_row = isfinite(as);
+        const float bound = as * 6.103515625e-05f + 7.888609052210118e-31f;   // 1024 * 2^-24, 2^-100
+        uint32_t slo = 0u, shi = 0u, unc = 0u;
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t bit = acc[cb][i] >= 0.0f ? 1u : 0u;
+                const int pos = 16 * (cb & 1) + 4 * g + i;
+                if (cb < 2) slo |= bit << pos; else shi |= bit << pos;
+                if (finite_row && !(fabsf(acc[cb][i]) > bound)) unc |= 1u << (4 * cb + i);
+            }
+        // rare: uncertain signs of finite rows (recomputed exactly: the 4
+        // lanes of the row each sum their 32 elements, then combine) and
+        // rows whose residual is not finite (or whose |e| sum overflows)
+        const bool nf = !finite_row && v0 + n < v_end;
+        if (__builtin_amdgcn_ballot_w64(unc != 0u || nf)) {
+            float *st = reinterpret_cast<float *>(smem + kEncStageOff) + wave * 16 * 128;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) st[n * 128 + 32 * q + 8 * g + i] = x[q][i];
+            const float *myrow = st + n * 128;
+            uint64_t pend = __builtin_amdgcn_ballot_w64(unc != 0u);
+            while (pend) {
+                const int L = __builtin_ctzll(pend);
+                const uint32_t uL = __builtin_amdgcn_readlane(unc, L);
+                const int item = __builtin_ctz(uL);
+                const int o = 16 * (item >> 2) + 4 * (L >> 4) + (item & 3);
+                double comp;
+                double part = exact_partial(myrow, gbits + o * 4, g, comp);
+                if (n != (L & 15)) { part = 0.0; comp = 0.0; }     // other rows contribute nothing
+                const double tot = xlane_sum_f64<32>(xlane_sum_f64<16>(part)) + xlane_sum_f64<32>(xlane_sum_f64<16>(comp));
+                if (lane == L) {
+                    unc &= ~(1u << item);
+                    const uint32_t bit = tot >= 0.0 ? 1u : 0u;
+                    const int pos = 16 * ((item >> 2) & 1) + 4 * g + (item & 3);
+                    if ((item >> 2) < 2) slo = (slo & ~(1u << pos)) | (bit << pos);
+                    else shi = (shi & ~(1u << pos)) | (bit << pos);
+                }
+                pend = __builtin_amdgcn_ballot_w64(unc != 0u);
+            }
+            uint64_t nfm = __builtin_amdgcn_ballot_w64(nf && g == 0);
+            while (nfm) {
+                const int r = __builtin_ctzll(nfm);
+                nfm &= nfm - 1;
+#pragma unroll 1
+                for (int o = 0; o < 64; ++o) {
+                    // order-free sign of the fp32 sum: a NaN term or both
+                    // infinities -> NaN -> 0; one infinity -> its sign; all
+                    // finite (only the |e| sum overflowed) -> exact fp64 sign
+                    const uint32_t *grow = gbits + o * 4;
+                    uint32_t fl = n == r ? nonfinite_flags(myrow, grow, g) : 0u;
+                    fl |= xlane_u32<16>(fl);
+                    fl |= xlane_u32<32>(fl);
+                    double comp;
+                    double part = exact_partial(myrow, grow, g, comp);
+                    if (n != r) { part = 0.0; comp = 0.0; }
+                    const double tot = xlane_sum_f64<32>(xlane_sum_f64<16>(part)) + xlane_sum_f64<32>(xlane_sum_f64<16>(comp));
+                    uint32_t bit;
+                    if ((fl & 1u) || (fl & 6u) == 6u) bit = 0u;
+                    else if (fl & 2u) bit = 1u;
+                    else if (fl & 4u) bit = 0u;
+                    else bit = tot >= 0.0 ? 1u : 0u;
+                    if (n == r && g == ((o & 15) >> 2)) {
+                        const int pos = 16 * ((o >> 4) & 1) + 4 * g + (o & 3);
+                        if ((o >> 4) < 2) slo = (slo & ~(1u << pos)) | (bit << pos);
+                        else shi = (shi & ~(1u << pos)) | (bit << pos);
+                    }
+                }
+            }
+        }
+        slo |= xlane_u32<16>(slo);
+        slo |= xlane_u32<32>(slo);
+        shi |= xlane_u32<16>(shi);
+        shi |= xlane_u32<32>(shi);
+
+        // stores: nibble dword s of lane (n, g) is bytes 16 s + 4 g .. + 3
+        if (v0 + n < v_end) {
+            uint32_t *np = reinterpret_cast<uint32_t *>(a.nibbles + mrow * 64);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) np[4 * s + g] = nib[s];
+        }
+        if (store) {
+            reinterpret_cast<uint2 *>(a.qjl + mrow * 8)[0] = make_uint2(slo, shi);
+            a.norms[mrow] = ss > 3.4028234663852886e38 ? INFINITY : (float)sqrt(ss);
+        }
+    }
+}
+
 // ── omni_dequantize ─────────────────────────────────────────────────────
 //
 // k_hat_d = fl(cb[code_d] + fl(s_d * fl(norm * c))), c = fp32(sqrt(2/pi)/D),
@@ -314,23 +773,79 @@ extern "C" int omni_wht_rotate(const void *x, int dtype, int64_t rows, int head_
     return OMNI_OK;
 }
 
+// The table-driven wave kernel serves 16-bit inputs at D = 128 when each head
+// has enough rows to amortise its 64 KB table; the rest (f32 inputs, D = 32,
+// one-row "heads" of the row-seeded API) take the lane-per-row kernel.
+static bool enc_fast(int64_t B, int64_t T, int head_dim, int x_dtype) {
+    return head_dim == 128 && (x_dtype == OMNI_BF16 || x_dtype == OMNI_F16) && B * T >= 64;
+}
+
+extern "C" size_t omni_encode_workspace_size(int64_t B, int H, int64_t T, int head_dim, int x_dtype,
+                                             int per_head_codebook) {
+    if (B <= 0 || H <= 0 || T <= 0 || !enc_fast(B, T, head_dim, x_dtype)) return 0;
+    return (size_t)(per_head_codebook ? H : 1) * kEncTab;
+}
+
 extern "C" int omni_encode(const void *x, int x_dtype, int64_t B, int H, int64_t T, int head_dim,
                            int rotate, const int8_t *sign_flip, const float *codebooks,
                            int per_head_codebook, const uint32_t *g_bits,
-                           uint8_t *nibbles, uint8_t *qjl, float *norms, void *stream) {
+                           uint8_t *nibbles, uint8_t *qjl, float *norms,
+                           void *workspace, size_t workspace_bytes, void *stream) {
     OMNI_CHECK_ARG(dtype_ok(x_dtype), "omni_encode: bad dtype %d", x_dtype);
     OMNI_CHECK_ARG(head_dim_ok(head_dim), "omni_encode: head_dim must be 128 or 32, got %d", head_dim);
     OMNI_CHECK_ARG(B >= 0 && H >= 0 && T >= 0, "omni_encode: negative shape");
     if (B == 0 || H == 0 || T == 0) return OMNI_OK;
     OMNI_CHECK_ARG(x && codebooks && g_bits && nibbles && qjl && norms, "omni_encode: NULL pointer");
     OMNI_CHECK_ARG(B <= 65535 && H <= 65535, "omni_encode: B and H must be <= 65535");
-    dim3 grid((unsigned)((T + kRowsPerBlock - 1) / kRowsPerBlock), (unsigned)H, (unsigned)B);
     const float s = inv_sqrt_dim_f32(head_dim);
+    hipStream_t st = as_stream(stream);
+    if (enc_fast(B, T, head_dim, x_dtype)) {
+        const size_t need = omni_encode_workspace_size(B, H, T, head_dim, x_dtype, per_head_codebook);
+        if (workspace == nullptr || workspace_bytes < need) {
+            set_error("omni_encode: workspace of %zu bytes required, %zu given", need, workspace_bytes);
+            return OMNI_EWORKSPACE;
+        }
+        uint8_t *table = reinterpret_cast<uint8_t *>(workspace);
+        const int n_tab = per_head_codebook ? H : 1;
+        if (x_dtype == OMNI_BF16)
+            hipLaunchKernelGGL(code_table_kernel<OMNI_BF16>, dim3(kEncTab / 256, n_tab), dim3(256), 0, st, codebooks,
+                               per_head_codebook, table);
+        else
+            hipLaunchKernelGGL(code_table_kernel<OMNI_F16>, dim3(kEncTab / 256, n_tab), dim3(256), 0, st, codebooks,
+                               per_head_codebook, table);
+        OMNI_CHECK_LAUNCH("omni_encode (code table)");
+        EncArgs a;
+        a.x = x; a.table = table; a.codebooks = codebooks; a.g_bits = g_bits;
+        a.sign_flip = sign_flip; a.nibbles = nibbles; a.qjl = qjl; a.norms = norms;
+        a.T = T; a.nrows_head = B * T; a.H = H; a.per_head = per_head_codebook; a.rotate = rotate; a.scale = s;
+        // about one block per CU across the heads; each block a run of rows of one head
+        int cus = 256;
+        {
+            int dev = 0;
+            hipDeviceProp_t p;
+            if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&p, dev) == hipSuccess && p.multiProcessorCount > 0)
+                cus = p.multiProcessorCount;
+        }
+        const int64_t per_head_blocks = (cus + H - 1) / H;
+        const int64_t grp = 16 * kEncWaves;
+        int64_t rpb = (a.nrows_head + per_head_blocks - 1) / per_head_blocks;
+        rpb = (rpb + grp - 1) / grp * grp;
+        a.rows_per_block = rpb;
+        const int64_t nx = (a.nrows_head + rpb - 1) / rpb;
+        OMNI_CHECK_ARG(nx <= 2147483647LL, "omni_encode: grid too large");
+        if (x_dtype == OMNI_BF16)
+            hipLaunchKernelGGL(encode128_kernel<OMNI_BF16>, dim3((unsigned)nx, (unsigned)H), dim3(64 * kEncWaves), 0, st, a);
+        else
+            hipLaunchKernelGGL(encode128_kernel<OMNI_F16>, dim3((unsigned)nx, (unsigned)H), dim3(64 * kEncWaves), 0, st, a);
+        OMNI_CHECK_LAUNCH("omni_encode");
+        return OMNI_OK;
+    }
+    dim3 grid((unsigned)((T + kRowsPerBlock - 1) / kRowsPerBlock), (unsigned)H, (unsigned)B);
     if (head_dim == 128)
-        hipLaunchKernelGGL(encode_kernel<128>, grid, dim3(kRowsPerBlock), 0, as_stream(stream), x, x_dtype, T, H,
+        hipLaunchKernelGGL(encode_kernel<128>, grid, dim3(kRowsPerBlock), 0, st, x, x_dtype, T, H,
                            rotate, sign_flip, codebooks, per_head_codebook, g_bits, nibbles, qjl, norms, s);
     else
-        hipLaunchKernelGGL(encode_kernel<32>, grid, dim3(kRowsPerBlock), 0, as_stream(stream), x, x_dtype, T, H,
+        hipLaunchKernelGGL(encode_kernel<32>, grid, dim3(kRowsPerBlock), 0, st, x, x_dtype, T, H,
                            rotate, sign_flip, codebooks, per_head_codebook, g_bits, nibbles, qjl, norms, s);
     OMNI_CHECK_LAUNCH("omni_encode");
     return OMNI_OK;

@@ -29,7 +29,8 @@ SIGNATURES = {
     "omni_qjl_g_bits": (_c_int, [_c_u32, _c_int, _vp]),
     "omni_wht_rotate": (_c_int, [_vp, _c_int, _c_i64, _c_int, _vp, _vp, _vp]),
     "omni_encode": (_c_int, [_vp, _c_int, _c_i64, _c_int, _c_i64, _c_int, _c_int, _vp, _vp, _c_int,
-                             _vp, _vp, _vp, _vp, _vp]),
+                             _vp, _vp, _vp, _vp, _vp, _c_sz, _vp]),
+    "omni_encode_workspace_size": (_c_sz, [_c_i64, _c_int, _c_i64, _c_int, _c_int, _c_int]),
     "omni_dequantize": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _vp, _c_i64, _c_int, _c_i64, _c_int,
                                  _c_int, _vp, _vp]),
     "omni_lora_apply": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _c_int, _vp, _c_i64, _c_int, _c_i64,

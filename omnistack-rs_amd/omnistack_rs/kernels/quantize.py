@@ -105,10 +105,14 @@ def _encode(x: torch.Tensor, codebooks: torch.Tensor, user_id: int, rotate: bool
         if sign_flip.numel() != D:
             raise ValueError(f"sign_flip must have {D} entries, got {sign_flip.numel()}")
         sf = torch.where(sign_flip.reshape(-1) < 0, -1, 1).to(torch.int8).to(dev).contiguous()
-    _lib.check(_lib.lib().omni_encode(
-        _lib.ptr(xc), _lib.dtype_code(xc.dtype), B, H, T, D, int(rotate), _lib.ptr(sf),
+    L = _lib.lib()
+    code = _lib.dtype_code(xc.dtype)
+    ws_n = L.omni_encode_workspace_size(B, H, T, D, code, per_head)
+    ws = torch.empty(ws_n, dtype=torch.uint8, device=dev) if ws_n else None
+    _lib.check(L.omni_encode(
+        _lib.ptr(xc), code, B, H, T, D, int(rotate), _lib.ptr(sf),
         _lib.ptr(cb), per_head, _lib.ptr(gb), _lib.ptr(nib), _lib.ptr(qjl), _lib.ptr(nrm),
-        _lib.stream_of(dev)))
+        _lib.ptr(ws), ws_n, _lib.stream_of(dev)))
     return nib, qjl, nrm
 
 
@@ -178,7 +182,7 @@ def quantize_rows(x: torch.Tensor, codebook: torch.Tensor, base_head_idx: int = 
         _lib.check(_lib.lib().omni_encode(
             _lib.ptr(xc), _lib.dtype_code(xc.dtype), 1, e - s, 1, D, 0, None, _lib.ptr(cbd), 0,
             _lib.ptr(gb), _lib.ptr(nib[s:e]), _lib.ptr(qjl[s:e]), _lib.ptr(nrm[s:e]),
-            _lib.stream_of(dev)))
+            None, 0, _lib.stream_of(dev)))
     batch = x.shape[:-1]
     return nib.reshape(*batch, D // 2), qjl.reshape(*batch, D // 16), nrm.reshape(*batch)
 

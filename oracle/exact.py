@@ -44,6 +44,33 @@ def projections_fp64(error: np.ndarray, G: np.ndarray) -> np.ndarray:
     return np.asarray(error, dtype=np.float64) @ np.asarray(G, dtype=np.float64).T
 
 
+def projection_signs_exact(error: np.ndarray, G: np.ndarray) -> np.ndarray:
+    """[e . G_i >= 0] for fp32 residual rows and +-1 rows of G, exactly: the
+    fp64 product decides where |P| exceeds its rounding bound
+    (256 * 2^-53 * sum|e|, any summation order), exact rational arithmetic
+    decides the rest (e.g. +-1e30 entries that cancel, leaving small terms a
+    blocked fp64 sum absorbs).  Rows with non-finite entries keep the fp64
+    result (their sums are order-free: +-inf or NaN)."""
+    e = np.asarray(error, dtype=np.float32)
+    Gd = np.asarray(G, dtype=np.float64)
+    P = projections_fp64(e, Gd)
+    absum = np.abs(e.astype(np.float64)).sum(axis=-1, keepdims=True)
+    bits = P >= 0
+    unsure = ~(np.abs(P) > 256.0 * 2.0 ** -53 * absum) & np.isfinite(absum)
+    for r, i in zip(*np.nonzero(unsure)):
+        bits[r, i] = exact_dot(e[r], Gd[i]) >= 0
+    return bits
+
+
+def exact_dot(e_row: np.ndarray, g_row: np.ndarray):
+    """sum_j g_j e_j as an exact rational (fp32 values convert exactly)."""
+    from fractions import Fraction
+    total = Fraction(0)
+    for v, s in zip(np.asarray(e_row, dtype=np.float32).tolist(), np.asarray(g_row).tolist()):
+        total += Fraction(v) if s > 0 else -Fraction(v)
+    return total
+
+
 def pack_bits_lsb(bits: np.ndarray) -> np.ndarray:
     """(N, 8k) 0/1 -> (N, k) bytes, bit b of byte m = bits[8m + b]."""
     N, nb = bits.shape

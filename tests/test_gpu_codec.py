@@ -35,8 +35,9 @@ def _check_encode(x_rot_cpu, cb_cpu, user_id, nib, qjl, nrm, tag=""):
         xh = x_rot_cpu[:, h].reshape(-1, D).float()
         _, deq = restate.quantize_int4(xh, cb)
         e = (xh - deq).numpy()
-        P = exact.projections_fp64(e, exact.g_from_mt(restate.make_qjl_seed(user_id, h), D))
-        ebits = exact.pack_bits_lsb((P >= 0).astype(np.uint8))
+        Gh = exact.g_from_mt(restate.make_qjl_seed(user_id, h), D)
+        P = exact.projections_fp64(e, Gh)
+        ebits = exact.pack_bits_lsb(exact.projection_signs_exact(e, Gh).astype(np.uint8))
         g = qjl[:, h].reshape(-1, D // 16).numpy()
         finite = np.isfinite(e).all(axis=1)
         assert np.array_equal(g[finite], ebits[finite]), f"{tag}: sign bits differ from exact sign (head {h})"
@@ -244,3 +245,66 @@ def test_known_answers_through_the_kernels(device):
         out = dequantize_heads(packed.to(device), torch.zeros(1, 1, 1, 8, dtype=torch.uint8, device=device),
                                torch.zeros(1, 1, 1, device=device), cb.to(device), with_qjl=False).cpu()
         assert torch.equal(out[0, 0, 0, :n], want)
+
+
+# ── the table-driven wave encoder (16-bit input, D = 128, >= 64 rows/head) ──
+
+def test_fast_encoder_edge_rows_bf16(device):
+    from omnistack_rs.kernels.quantize import quantize_heads
+    cb = _data.gaussian_codebook(2).clone()
+    cb[1, 7] = cb[1, 8]                                  # duplicate centroid (ties) in head 1
+    x = torch.randn(1, 2, 96, 128, generator=_data.gen(31))
+    for h in range(2):
+        x[0, h, 0] = 0.0
+        x[0, h, 1, :16] = cb[h]                          # centroid hits (as bf16 below)
+        x[0, h, 2, :15] = (cb[h, :-1] + cb[h, 1:]) / 2   # midpoints
+        x[0, h, 3] = cb[h, 3]                            # zero residual in fp32 only if cb is bf16-exact
+        x[0, h, 4, :5] = torch.tensor([1e30, -1e30, 1e-30, -1e-30, 0.0])
+        x[0, h, 5] = 100.0
+        x[0, h, 6] = 1e-38                               # subnormal-scale residuals
+    x = x.to(torch.bfloat16)
+    nib, qjl, nrm = quantize_heads(x.to(device), cb.to(device), user_id=3)
+    print(f"[encode] fast edge rows bf16", flush=True)
+    _check_encode(x, cb, 3, nib, qjl, nrm, tag="fast-edge")
+
+
+def test_fast_encoder_nonfinite_rows(device):
+    from omnistack_rs.kernels.quantize import quantize_heads
+    cb = _data.gaussian_codebook(1)[0]
+    x = torch.randn(1, 1, 80, 128, generator=_data.gen(32))
+    x[0, 0, 0, 5] = float("nan")
+    x[0, 0, 1, 9] = float("inf")
+    x[0, 0, 2, 9], x[0, 0, 2, 10] = float("inf"), float("-inf")
+    x[0, 0, 3, :] = float("-inf")
+    x = x.to(torch.bfloat16)
+    nib, qjl, nrm = quantize_heads(x.to(device), cb.to(device), user_id=1)
+    r_nib, r_qjl, r_nrm = restate.quantize_heads(x, cb, user_id=1)
+    assert torch.equal(nib.cpu(), r_nib)
+    assert torch.equal(qjl.cpu()[0, 0, :4], r_qjl[0, 0, :4])          # order-free signs
+    assert torch.isnan(nrm[0, 0, 0]).item() and torch.isinf(nrm[0, 0, 1]).item()
+    _check_encode(x[:, :, 4:], cb, 1, nib[:, :, 4:], qjl[:, :, 4:], nrm[:, :, 4:], tag="fast-finite-rest")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fast_encoder_rows_straddle_sequences(device, dtype):
+    """T = 13 < 16: every 16-row group of a head spans several sequences."""
+    from omnistack_rs.kernels.quantize import encode_kv
+    B, H, T = 10, 3, 13
+    x = _data.kv((B, H, T, 128), seed=33, dtype=dtype)
+    s = _data.sign_flip()
+    cb = _data.gaussian_codebook(H) * torch.linspace(0.9, 1.3, H).reshape(H, 1)
+    nib, qjl, nrm = encode_kv(x.to(device), cb.to(device), user_id=77, sign_flip=s.to(device))
+    print(f"[encode] straddle {dtype}", flush=True)
+    _check_encode(restate.rotate(x, s), cb, 77, nib, qjl, nrm, tag=f"straddle-{dtype}")
+
+
+def test_fast_encoder_matches_row_kernel(device):
+    """The wave encoder and the lane-per-row encoder agree bit for bit on the
+    same rows (a head with >= 64 rows vs the same rows fed one head at a time)."""
+    from omnistack_rs.kernels.quantize import quantize_heads
+    x = restate.wht(_data.kv((1, 1, 64, 128), seed=34, dtype=torch.float32)).to(torch.bfloat16)
+    cb = _data.gaussian_codebook(1)[0]
+    fast = quantize_heads(x.to(device), cb.to(device), user_id=5)
+    slow = [quantize_heads(x[:, :, i:i + 1].to(device), cb.to(device), user_id=5) for i in range(64)]
+    for k in range(3):
+        assert torch.equal(fast[k].cpu(), torch.cat([t[k].cpu() for t in slow], dim=2)), f"output {k}"

@@ -56,7 +56,7 @@ def test_host_g_bits_equal_torch_randint(seed, D):
 
 def test_validation_errors_before_any_device_work(L):
     from omnistack_rs import _lib
-    rc = L.omni_encode(None, 0, 1, 1, 1, 64, 0, None, None, 0, None, None, None, None, None)
+    rc = L.omni_encode(None, 0, 1, 1, 1, 64, 0, None, None, 0, None, None, None, None, None, 0, None)
     assert rc == _lib.OMNI_EINVAL and "head_dim" in _lib.last_error()
     rc = L.omni_attn(None, 0, None, None, None, None, None, 0, None, 1, 6, 4, 1, 1, 128, 1.0, 0, -1, 0,
                      None, None, None, 0, None)
@@ -71,10 +71,28 @@ def test_validation_errors_before_any_device_work(L):
 
 
 def test_empty_shapes_are_noops(L):
-    assert L.omni_encode(None, 2, 0, 8, 0, 128, 0, None, None, 0, None, None, None, None, None) == 0
+    assert L.omni_encode(None, 2, 0, 8, 0, 128, 0, None, None, 0, None, None, None, None, None, 0, None) == 0
     assert L.omni_dequantize(None, None, None, None, 0, None, 0, 8, 10, 128, 1, None, None) == 0
     assert L.omni_attn(None, 2, None, None, None, None, None, 0, None, 0, 4, 2, 1, 10, 128, 1.0, 1, -1, 0,
                        None, None, None, 0, None) == 0
+
+
+def test_encode_workspace_size_host_only(L):
+    # 16-bit inputs at D = 128 with >= 64 rows per head: one 64 KB code table per codebook
+    assert L.omni_encode_workspace_size(16, 8, 4096, 128, 2, 1) == 8 * 65536
+    assert L.omni_encode_workspace_size(16, 8, 4096, 128, 1, 0) == 65536
+    assert L.omni_encode_workspace_size(16, 8, 4096, 128, 0, 1) == 0      # f32 input
+    assert L.omni_encode_workspace_size(16, 8, 4096, 32, 2, 1) == 0       # head_dim 32
+    assert L.omni_encode_workspace_size(1, 8, 3, 128, 2, 1) == 0          # 3 rows per head
+    assert L.omni_encode_workspace_size(0, 8, 3, 128, 2, 1) == 0
+
+
+def test_encode_missing_workspace_is_an_error(L):
+    from omnistack_rs import _lib
+    # rejected before any pointer is dereferenced on the device
+    dummy = 4096
+    rc = L.omni_encode(dummy, 2, 1, 1, 64, 128, 0, None, dummy, 0, dummy, dummy, dummy, dummy, None, 0, None)
+    assert rc == _lib.OMNI_EWORKSPACE and "workspace" in _lib.last_error()
 
 
 def test_workspace_size_host_only(L):

@@ -301,3 +301,18 @@ def test_lora_merged_weight_closed_form():
         W = (Bw[idx[b]].double() @ A[idx[b]].double())            # (H*D, hid)
         want = q[b].double() + (x[b].double() @ W.T).reshape(T, H, D).permute(1, 0, 2) * 0.5
         assert (out[b].double() - want).abs().max().item() < 1e-5
+
+
+def test_exact_projection_signs_survive_cancellation():
+    # +-1e30 cancel; the remaining small terms decide the sign.  A blocked
+    # fp64 dot product can absorb them into 1e30 and report 0.
+    e = np.zeros((2, 128), dtype=np.float32)
+    e[:, 0], e[:, 1] = 1e30, -1e30
+    e[0, 2:6] = [1.0, -0.5, 2.0 ** -20, 0.0]     # exact sum 0.5 + 2^-20 > 0
+    e[1, 2:6] = [-1.0, 0.5, -(2.0 ** -20), 0.0]  # exact sum < 0
+    G = np.ones((3, 128))
+    G[2, 1:] = -1.0                                # 1e30 + 1e30 + ...: no cancellation
+    bits = exact.projection_signs_exact(e, G)
+    assert bits[0].tolist() == [True, True, True]
+    assert bits[1].tolist() == [False, False, True]
+    assert exact.exact_dot(e[0], G[0]) == 0.5 + 2.0 ** -20
