@@ -262,14 +262,14 @@ __device__ __forceinline__ uint32_t cvt_pk_f16(float x, float y) {
 //     P[n][16 cb + 4 g + i]: every value a lane needs for its row is local
 //     or one 4-lane reduction away.
 
-constexpr int kEncWaves = 8;
+constexpr int kEncWaves = 12;
 constexpr int kEncTab = 65536;                            // u8 code table (both nibbles = code)
 constexpr int kEncCentOff = kEncTab;                      // f32 centroid by table byte (256 slots)
 constexpr int kEncGimgOff = kEncCentOff + 256 * 4;        // [cb][s][lane] uint4: 8 bf16 +-1 of G
 constexpr int kEncGbitsOff = kEncGimgOff + 4 * 4 * 64 * 16;   // G rows as bits, 64 x 4 words
 constexpr int kEncFlipOff = kEncGbitsOff + 64 * 4 * 4;       // [lane][16] u32: sign-bit xor of the raw 16-bit words
-constexpr int kEncStageOff = kEncFlipOff + 64 * 16 * 4;      // [wave][16 rows][128] f32 residuals (rare paths)
-constexpr int kEncLdsBytes = kEncStageOff + kEncWaves * 16 * 128 * 4;
+constexpr int kEncStageOff = kEncFlipOff + 64 * 16 * 4;      // [wave][128] f32: one residual row (rare paths)
+constexpr int kEncLdsBytes = kEncStageOff + kEncWaves * 128 * 4;
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
@@ -408,7 +408,7 @@ __device__ __noinline__ uint32_t nonfinite_flags(const float *row, const uint32_
     return fl;
 }
 
-template <int XDT>
+template <int XDT, bool ROT>
 __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
     __shared__ __attribute__((aligned(16))) unsigned char smem[kEncLdsBytes];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -422,8 +422,7 @@ __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
     {
         const uint4 *src = reinterpret_cast<const uint4 *>(a.table + (int64_t)(a.per_head ? h : 0) * kEncTab);
         uint4 *dst = reinterpret_cast<uint4 *>(smem);
-#pragma unroll
-        for (int k = 0; k < kEncTab / 16 / (64 * kEncWaves); ++k) dst[tid + k * 64 * kEncWaves] = src[tid + k * 64 * kEncWaves];
+        for (int k = tid; k < kEncTab / 16; k += 64 * kEncWaves) dst[k] = src[k];
     }
     const float *cbp = a.codebooks + (a.per_head ? h * 16 : 0);
     if (tid < 16) reinterpret_cast<float *>(smem + kEncCentOff)[tid | (tid << 4)] = cbp[tid];
@@ -443,7 +442,7 @@ __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
     for (int k = tid; k < 64 * 16; k += 64 * kEncWaves) {
         const int l = k >> 4, q = k & 15, sq = q >> 2, j = q & 3;
         uint32_t m = 0u;
-        if (a.rotate && a.sign_flip) {
+        if (ROT && a.sign_flip) {
             const int e0 = 32 * sq + 8 * (l >> 4) + 2 * j;
             m = (a.sign_flip[e0] < 0 ? 0x8000u : 0u) | (a.sign_flip[e0 + 1] < 0 ? 0x80000000u : 0u);
         }
@@ -477,7 +476,7 @@ __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
             for (int s = 0; s < 4; ++s) w4[s] = src[4 * s + g];
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                const uint4 f = fmk[s];
+                const uint4 f = ROT ? fmk[s] : make_uint4(0u, 0u, 0u, 0u);
                 const uint32_t w[4] = {w4[s].x ^ f.x, w4[s].y ^ f.y, w4[s].z ^ f.z, w4[s].w ^ f.w};
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
@@ -486,7 +485,7 @@ __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
                 }
             }
         }
-        if (a.rotate) {
+        if (ROT) {
             // h = 1, 2, 4 inside each 8-element chunk
 #pragma unroll
             for (int hh = 1; hh < 8; hh <<= 1)
@@ -522,15 +521,13 @@ __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
                         }
                     }
         }
-        // per element pair: (scale, round to the input dtype,) code from the
-        // table, residual, norm and |e| partial sums, nibble byte
+        // value bits of each element ((scaled and) rounded to the input dtype)
+        uint32_t vb[4][8];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            uint32_t wn = 0u;
+        for (int s = 0; s < 4; ++s)
 #pragma unroll
             for (int i = 0; i < 8; i += 2) {
-                uint32_t b0, b1;
-                if (a.rotate) {
+                if (ROT) {
                     const float p = x[s][i] * a.scale, q = x[s][i + 1] * a.scale;
                     uint32_t pk;
                     if (XDT == OMNI_BF16) {
@@ -544,27 +541,44 @@ __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
                         x[s][i] = f16_to_f32((uint16_t)(pk & 0xffffu));
                         x[s][i + 1] = f16_to_f32((uint16_t)(pk >> 16));
                     }
-                    b0 = pk & 0xffffu;
-                    b1 = pk >> 16;
+                    vb[s][i] = pk & 0xffffu;
+                    vb[s][i + 1] = pk >> 16;
                 } else if (XDT == OMNI_BF16) {
-                    b0 = __float_as_uint(x[s][i]) >> 16;
-                    b1 = __float_as_uint(x[s][i + 1]) >> 16;
+                    vb[s][i] = __float_as_uint(x[s][i]) >> 16;
+                    vb[s][i + 1] = __float_as_uint(x[s][i + 1]) >> 16;
                 } else {
-                    b0 = f32_to_f16_rne(x[s][i]);       // exact: the value came from f16
-                    b1 = f32_to_f16_rne(x[s][i + 1]);
+                    vb[s][i] = f32_to_f16_rne(x[s][i]);          // exact: the value came from f16
+                    vb[s][i + 1] = f32_to_f16_rne(x[s][i + 1]);
                 }
-                const uint32_t t0 = tab[b0], t1 = tab[b1];
-                const float e0 = x[s][i] - cent[t0], e1 = x[s][i + 1] - cent[t1];
-                x[s][i] = e0;
-                x[s][i + 1] = e1;
-                ss += (double)__fmul_rn(e0, e0);
-                ss += (double)__fmul_rn(e1, e1);
-                as += fabsf(e0);
-                as += fabsf(e1);
-                wn |= ((t0 & 0x0Fu) | (t1 & 0xF0u)) << (4 * i);
             }
+        // codes (all table reads issued together), then centroids
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) vb[s][i] = tab[vb[s][i]];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            uint32_t wn = 0u;
+#pragma unroll
+            for (int i = 0; i < 8; i += 2)
+                wn |= ((vb[s][i] & 0x0Fu) | (vb[s][i + 1] & 0xF0u)) << (4 * i);
             nib[s] = wn;
         }
+        float cv[4][8];
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) cv[s][i] = cent[vb[s][i]];
+        // residuals, norm and |e| partial sums
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float e = x[s][i] - cv[s][i];
+                x[s][i] = e;
+                ss += (double)__fmul_rn(e, e);
+                as += fabsf(e);
+            }
         ss = xlane_sum_f64<16>(ss);
         ss = xlane_sum_f64<32>(ss);
         as = xlane_sum_f32(as);
@@ -618,21 +632,29 @@ __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
         // rows whose residual is not finite (or whose |e| sum overflows)
         const bool nf = !finite_row && v0 + n < v_end;
         if (__builtin_amdgcn_ballot_w64(unc != 0u || nf)) {
-            float *st = reinterpret_cast<float *>(smem + kEncStageOff) + wave * 16 * 128;
+            // one residual row at a time goes through this wave's LDS row
+            float *st = reinterpret_cast<float *>(smem + kEncStageOff) + wave * 128;
+            int staged = -1;
+            auto stage = [&](int r) {
+                if (r == staged) return;
+                if (n == r) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
+                    for (int q = 0; q < 4; ++q)
 #pragma unroll
-                for (int i = 0; i < 8; ++i) st[n * 128 + 32 * q + 8 * g + i] = x[q][i];
-            const float *myrow = st + n * 128;
+                        for (int i = 0; i < 8; ++i) st[32 * q + 8 * g + i] = x[q][i];
+                }
+                staged = r;
+            };
             uint64_t pend = __builtin_amdgcn_ballot_w64(unc != 0u);
             while (pend) {
                 const int L = __builtin_ctzll(pend);
                 const uint32_t uL = __builtin_amdgcn_readlane(unc, L);
                 const int item = __builtin_ctz(uL);
                 const int o = 16 * (item >> 2) + 4 * (L >> 4) + (item & 3);
+                stage(L & 15);
                 double comp;
-                double part = exact_partial(myrow, gbits + o * 4, g, comp);
-                if (n != (L & 15)) { part = 0.0; comp = 0.0; }     // other rows contribute nothing
+                double part = exact_partial(st, gbits + o * 4, g, comp);
+                if (n != (L & 15)) { part = 0.0; comp = 0.0; }     // lanes of other rows contribute nothing
                 const double tot = xlane_sum_f64<32>(xlane_sum_f64<16>(part)) + xlane_sum_f64<32>(xlane_sum_f64<16>(comp));
                 if (lane == L) {
                     unc &= ~(1u << item);
@@ -647,17 +669,18 @@ __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
             while (nfm) {
                 const int r = __builtin_ctzll(nfm);
                 nfm &= nfm - 1;
+                stage(r);
 #pragma unroll 1
                 for (int o = 0; o < 64; ++o) {
                     // order-free sign of the fp32 sum: a NaN term or both
                     // infinities -> NaN -> 0; one infinity -> its sign; all
                     // finite (only the |e| sum overflowed) -> exact fp64 sign
                     const uint32_t *grow = gbits + o * 4;
-                    uint32_t fl = n == r ? nonfinite_flags(myrow, grow, g) : 0u;
+                    uint32_t fl = n == r ? nonfinite_flags(st, grow, g) : 0u;
                     fl |= xlane_u32<16>(fl);
                     fl |= xlane_u32<32>(fl);
                     double comp;
-                    double part = exact_partial(myrow, grow, g, comp);
+                    double part = exact_partial(st, grow, g, comp);
                     if (n != r) { part = 0.0; comp = 0.0; }
                     const double tot = xlane_sum_f64<32>(xlane_sum_f64<16>(part)) + xlane_sum_f64<32>(xlane_sum_f64<16>(comp));
                     uint32_t bit;
@@ -833,10 +856,14 @@ extern "C" int omni_encode(const void *x, int x_dtype, int64_t B, int H, int64_t
         a.rows_per_block = rpb;
         const int64_t nx = (a.nrows_head + rpb - 1) / rpb;
         OMNI_CHECK_ARG(nx <= 2147483647LL, "omni_encode: grid too large");
-        if (x_dtype == OMNI_BF16)
-            hipLaunchKernelGGL(encode128_kernel<OMNI_BF16>, dim3((unsigned)nx, (unsigned)H), dim3(64 * kEncWaves), 0, st, a);
-        else
-            hipLaunchKernelGGL(encode128_kernel<OMNI_F16>, dim3((unsigned)nx, (unsigned)H), dim3(64 * kEncWaves), 0, st, a);
+        const dim3 eg((unsigned)nx, (unsigned)H), eb(64 * kEncWaves);
+        if (x_dtype == OMNI_BF16) {
+            if (rotate) hipLaunchKernelGGL((encode128_kernel<OMNI_BF16, true>), eg, eb, 0, st, a);
+            else hipLaunchKernelGGL((encode128_kernel<OMNI_BF16, false>), eg, eb, 0, st, a);
+        } else {
+            if (rotate) hipLaunchKernelGGL((encode128_kernel<OMNI_F16, true>), eg, eb, 0, st, a);
+            else hipLaunchKernelGGL((encode128_kernel<OMNI_F16, false>), eg, eb, 0, st, a);
+        }
         OMNI_CHECK_LAUNCH("omni_encode");
         return OMNI_OK;
     }
