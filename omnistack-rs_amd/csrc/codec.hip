@@ -371,41 +371,35 @@ __device__ __forceinline__ float xlane_sum_f32(float v) {
     return v + __uint_as_float(xlane_u32<32>(__float_as_uint(v)));
 }
 
-// sum over this lane's 32 elements of s_j e_j in fp64 (Neumaier), for G row
-// `grow` (4 words); `row` is the residual row staged in LDS.  The 4 lanes of
-// a row then combine their (sum, compensation) pairs.
-__device__ __noinline__ double exact_partial(const float *row, const uint32_t *grow, int g, double &comp) {
-    double s = 0.0, c = 0.0;
-#pragma unroll 1
-    for (int q = 0; q < 4; ++q) {
-        const uint32_t byte = (grow[q] >> (8 * g)) & 0xffu;
-#pragma unroll 1
-        for (int i = 0; i < 8; ++i) {
-            double y = (double)row[32 * q + 8 * g + i];
-            y = ((byte >> i) & 1u) ? y : -y;
-            const double t = s + y;
-            c += (fabs(s) >= fabs(y)) ? ((s - t) + y) : ((y - t) + s);
-            s = t;
-        }
+// sum_j s_j e_j over one staged residual row (128 floats in LDS) for G row
+// `grow` (4 words): each lane takes elements lane and lane + 64 in fp64 and
+// the wave reduces (sum, error) pairs with TwoSum, so the result is the exact
+// sum up to ~1e-30 relative.  Commutative steps: every lane gets the same
+// value.  `fl` collects the order-free classes of the terms (1 NaN, 2 +inf,
+// 4 -inf), OR-reduced over the wave.
+__device__ __forceinline__ double wave_row_dot(const float *st, const uint32_t *grow, int lane, uint32_t &fl) {
+    const float e1 = st[lane], e2 = st[lane + 64];
+    const uint32_t b1 = (grow[lane >> 5] >> (lane & 31)) & 1u, b2 = (grow[2 + (lane >> 5)] >> (lane & 31)) & 1u;
+    const float f1 = b1 ? e1 : -e1, f2 = b2 ? e2 : -e2;
+    uint32_t cls = 0u;
+    cls |= (f1 != f1) ? 1u : (f1 == INFINITY ? 2u : (f1 == -INFINITY ? 4u : 0u));
+    cls |= (f2 != f2) ? 1u : (f2 == INFINITY ? 2u : (f2 == -INFINITY ? 4u : 0u));
+    fl = (__builtin_amdgcn_ballot_w64((cls & 1u) != 0u) ? 1u : 0u) | (__builtin_amdgcn_ballot_w64((cls & 2u) != 0u) ? 2u : 0u) |
+         (__builtin_amdgcn_ballot_w64((cls & 4u) != 0u) ? 4u : 0u);
+    const double y1 = (double)f1, y2 = (double)f2;
+    double s = y1 + y2;
+    double bp = s - y1;
+    double c = (y1 - (s - bp)) + (y2 - bp);
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const double so = __shfl_xor(s, m), co = __shfl_xor(c, m);
+        const double t = s + so;
+        bp = t - s;
+        const double err = (s - (t - bp)) + (so - bp);
+        s = t;
+        c = (c + co) + err;
     }
-    comp = c;
-    return s;
-}
-
-// order-free classes of this lane's 32 terms s_j e_j: 1 NaN, 2 +inf, 4 -inf
-__device__ __noinline__ uint32_t nonfinite_flags(const float *row, const uint32_t *grow, int g) {
-    uint32_t fl = 0u;
-#pragma unroll 1
-    for (int q = 0; q < 4; ++q) {
-        const uint32_t byte = (grow[q] >> (8 * g)) & 0xffu;
-#pragma unroll 1
-        for (int i = 0; i < 8; ++i) {
-            const float e = row[32 * q + 8 * g + i];
-            const float y = ((byte >> i) & 1u) ? e : -e;
-            fl |= (y != y) ? 1u : (y == INFINITY ? 2u : (y == -INFINITY ? 4u : 0u));
-        }
-    }
-    return fl;
+    return s + c;
 }
 
 template <int XDT, bool ROT>
@@ -652,10 +646,8 @@ __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
                 const int item = __builtin_ctz(uL);
                 const int o = 16 * (item >> 2) + 4 * (L >> 4) + (item & 3);
                 stage(L & 15);
-                double comp;
-                double part = exact_partial(st, gbits + o * 4, g, comp);
-                if (n != (L & 15)) { part = 0.0; comp = 0.0; }     // lanes of other rows contribute nothing
-                const double tot = xlane_sum_f64<32>(xlane_sum_f64<16>(part)) + xlane_sum_f64<32>(xlane_sum_f64<16>(comp));
+                uint32_t fl;
+                const double tot = wave_row_dot(st, gbits + o * 4, lane, fl);
                 if (lane == L) {
                     unc &= ~(1u << item);
                     const uint32_t bit = tot >= 0.0 ? 1u : 0u;
@@ -675,14 +667,8 @@ __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
                     // order-free sign of the fp32 sum: a NaN term or both
                     // infinities -> NaN -> 0; one infinity -> its sign; all
                     // finite (only the |e| sum overflowed) -> exact fp64 sign
-                    const uint32_t *grow = gbits + o * 4;
-                    uint32_t fl = n == r ? nonfinite_flags(st, grow, g) : 0u;
-                    fl |= xlane_u32<16>(fl);
-                    fl |= xlane_u32<32>(fl);
-                    double comp;
-                    double part = exact_partial(st, grow, g, comp);
-                    if (n != r) { part = 0.0; comp = 0.0; }
-                    const double tot = xlane_sum_f64<32>(xlane_sum_f64<16>(part)) + xlane_sum_f64<32>(xlane_sum_f64<16>(comp));
+                    uint32_t fl;
+                    const double tot = wave_row_dot(st, gbits + o * 4, lane, fl);
                     uint32_t bit;
                     if ((fl & 1u) || (fl & 6u) == 6u) bit = 0u;
                     else if (fl & 2u) bit = 1u;
