@@ -273,6 +273,27 @@ def main() -> int:
         result["encode_c4"] = {"GB_s": round(bytes4 / t4 / 1e9, 1), "us_per_call": round(t4 * 1e6, 1),
                                "bytes": bytes4, "pct_of_hbm_peak": round(100 * bytes4 / t4 / 1e9 / HBM_PEAK_GBS, 2)}
         log(f"[bench] C4: {t4 * 1e6:.0f} us -> {bytes4 / t4 / 1e9:.0f} GB/s")
+        del k4, v4
+
+        # C5: chunked prefill, a 512-token bf16 query chunk at the end of a
+        # 16384-token cache (query t sees keys 0 .. 15872 + t)
+        B5, T5, S5 = 8, 512, 16384
+        off5 = S5 - T5
+        log("[bench] C5: prefill 8 x 512 queries over 8 x 16384 cached tokens (causal)")
+        kn5, kq5, kr5, vn5 = make_cache(B5, Hkv, S5, D, dev, 55, uid, cb, sign)
+        q5 = torch.randn(B5, Hq, T5, D, generator=torch.Generator(device=dev).manual_seed(56), device=dev).to(torch.bfloat16)
+        att5 = PackedKVAttention(kn5, kq5, kr5, vn5, cb, n_heads=Hq, q_tokens=T5, user_id=uid, causal_offset=off5)
+        t5 = wall_eager(lambda: att5.run(q5), max(3, args.steps // 10), 1)
+        keys = T5 * off5 + T5 * (T5 + 1) // 2            # visible (query, key) pairs per (b, q head)
+        fl_qkpv = 2 * 2 * B5 * Hq * keys * D             # Q.K and P.V
+        fl_qjl = 2 * B5 * Hq * keys * (D // 2)           # signs . (G q) score correction
+        tf5 = (fl_qkpv + fl_qjl) / t5 / 1e12
+        result["prefill_c5"] = {"us_per_call": round(t5 * 1e6, 1), "TFLOP_s": round(tf5, 2),
+                                "flops_per_call": fl_qkpv + fl_qjl,
+                                "frac_of_fp16_dense_peak": round(tf5 / 2500.0, 4),
+                                "note": "useful flops (QK, PV, QJL correction) over the causally visible keys"}
+        log(f"[bench] C5: {t5 * 1e6:.0f} us -> {tf5:.1f} TFLOP/s ({tf5 / 2500:.1%} of fp16 dense MFMA peak)")
+        del kn5, kq5, kr5, vn5, att5
 
     # ── CPU baseline (reference CPU path restated in oracle/) ────────────
     if not args.no_cpu:

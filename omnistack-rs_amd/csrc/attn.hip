@@ -992,10 +992,415 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     }
 }
 
+// ── chunked-prefill kernel (many query rows per (batch, kv head)) ────────
+//
+// Same math as the decode kernel, organised for T > 1: each wave owns 16 * NCB
+// query rows (NCB MFMA column blocks) and streams every key tile for them, so
+// each K / V operand decoded from the LUT feeds NCB column blocks; eight
+// waves (128 * NCB rows) share one block's LUTs.  q enters the MFMA exactly:
+// the rows are bf16 / f16, scaled per row by a power of two into fp16 range,
+// and the softmax scale is applied to the fp32 score (score =
+// acc * scale / 2^k + norm * (signs . Gq')), so K (fp16 hi + remainder on the
+// k axis) and q carry no extra rounding.  f32 queries (QLO) add a second B
+// operand with the fp16 remainder of the scaled q.  V is the decode kernel's pair-byte
+// (hi, lo) operand.  Rows past T * G, or keys past a row's causal limit,
+// are masked.
+constexpr int kPreWaves = 8;
+constexpr int kPrefillMinRows = 32;                              // T * (Hq / Hkv) above this takes this kernel
+constexpr int kPreNcb = 2;                                       // column blocks per wave for 16-bit q (f32 q: 1)
+constexpr int kPreCbOff = kSlutOff + kSlutBytes;                 // 16 x (fp16 hi | remainder << 16)
+constexpr int kPreStageOff = kPreCbOff + 64;                     // per wave: q rows fp16, then G q fp32
+constexpr int kPreQsrOff = kPreStageOff + kPreWaves * 32 * 128 * 2;   // per wave: 32 x f32 score scales
+constexpr int kPreLdsBytes = kPreQsrOff + kPreWaves * 32 * 4;
+
+// Prefill tile: as DecTileRaw, but the norms are those of the A-operand rows
+// (token t0 + 16 u + (lane % 16)): the QJL sign rows are scaled by them.
+struct PreTileRaw {
+    uint4 k[2];
+    uint2 sg[2];
+    float nr[2];
+    uint32_t v[8];
+};
+
+template <bool QJL>
+__device__ __forceinline__ void pre_load(PreTileRaw &R, const DecBufs &P, const DecOffsets &O, int t0) {
+    const uint32_t t = (uint32_t)t0;
+    const uint32_t vk = O.k + t * 64u, vsg = O.sg + t * 8u, vnr = O.nr + t * 4u, vv = O.v + t * 64u;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const u32x4_t kv4 = __builtin_amdgcn_raw_buffer_load_b128(P.kn, vk + 1024u * u, 0, 0);
+        R.k[u] = make_uint4(kv4.x, kv4.y, kv4.z, kv4.w);
+        if (QJL) {
+            const u32x2_t sv = __builtin_amdgcn_raw_buffer_load_b64(P.kq, vsg + 128u * u, 0, 0);
+            R.sg[u] = make_uint2(sv.x, sv.y);
+            R.nr[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(P.kr, vnr + 64u * u, 0, 0));
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        R.v[i] = __builtin_amdgcn_raw_buffer_load_b32(P.vn, vv + 64u * (16 * (i / 4) + (i % 4)), 0, 0);
+}
+
+template <bool QJL, int NCB, int PF, bool QLO>
+__global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArgs a) {
+    constexpr int D = 128, QD = 64, RW = 16 * NCB;      // rows per wave
+    static_assert(!QLO || NCB == 1, "the f32 remainder plane shares the 32-row stage area");
+    __shared__ __attribute__((aligned(16))) unsigned char smem[kPreLdsBytes];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n = lane & 15, g = lane >> 4;
+    const int split = blockIdx.x, hk = blockIdx.y;
+    const int64_t bz = blockIdx.z;
+    const int64_t b = bz / a.n_rchunks;
+    const int rc = (int)(bz % a.n_rchunks);
+    const int nrows_total = (int)(a.T * a.G);
+    const int row0 = rc * a.rows + wave * RW;                  // first flat row of this wave
+    unsigned char *stage = smem + kPreStageOff + wave * 32 * 128 * 2;
+    float *qsr_l = reinterpret_cast<float *>(smem + kPreQsrOff) + wave * 32;
+
+    // ── LUTs (as the decode kernel) ───────────────────────────────────
+    {
+        const __amdgpu_buffer_rsrc_t CB = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(a.codebooks + (a.per_head ? hk * 16 : 0)), (short)0, 16 * 4, kBufWord3);
+        const float c = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(CB, 4u * (lane & 15), 0, 0));
+        const uint16_t h = f32_to_f16_rne(c);
+        *reinterpret_cast<uint32_t *>(smem + kPreCbOff + 4 * (lane & 15)) =
+            (uint32_t)h | ((uint32_t)f32_to_f16_rne(c - f16_to_f32(h)) << 16);
+    }
+    if (tid < 256) {
+        const int e = tid;
+        uint32_t w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            w[k] = (((e >> (2 * k)) & 1) ? 0x3C00u : 0xBC00u) | ((((e >> (2 * k + 1)) & 1) ? 0x3C00u : 0xBC00u) << 16);
+        *reinterpret_cast<uint4 *>(smem + kSlutOff + e * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+
+    // ── this wave's query rows: (sign flip,) WHT, round; per-row power-of-2
+    //    scale into fp16 range; staged as fp16 ───────────────────────────
+    {
+        const bool use_flip = a.rotate_q && a.sign_flip;
+        const bool flip_lo = use_flip && a.sign_flip[lane] < 0, flip_hi = use_flip && a.sign_flip[64 + lane] < 0;
+        for (int rr = 0; rr < RW; ++rr) {
+            const int rho = row0 + rr;
+            const bool ok = rho < nrows_total;
+            const int rc_ = ok ? rho : nrows_total - 1;
+            const int t = rc_ / a.G, hq = hk * a.G + (rc_ - t * a.G);
+            const int64_t base = ((b * a.Hq + hq) * a.T + t) * D;
+            float lo = load_as_f32(a.q, a.q_dtype, base + lane), hi = load_as_f32(a.q, a.q_dtype, base + 64 + lane);
+            lo = flip_lo ? -lo : lo;
+            hi = flip_hi ? -hi : hi;
+            if (a.rotate_q) {
+                wht128_lanes(lo, hi, lane);
+                lo = round_to_dtype(lo * a.wht_scale, a.q_dtype);
+                hi = round_to_dtype(hi * a.wht_scale, a.q_dtype);
+            }
+            if (!ok) lo = hi = 0.0f;
+            // row max |q| -> 2^k with max * 2^k in [2^14, 2^15)
+            float m = fmaxf(fabsf(lo), fabsf(hi));
+#pragma unroll
+            for (int sh = 32; sh >= 1; sh >>= 1) m = fmaxf(m, __shfl_xor(m, sh));
+            int ex = 0;
+            if (m > 0.0f && m < INFINITY) { frexpf(m, &ex); }
+            const float sr = ldexpf(1.0f, 15 - ex);       // m * sr in [2^14, 2^15)
+            const uint16_t l16 = f32_to_f16_rne(lo * sr), h16 = f32_to_f16_rne(hi * sr);
+            reinterpret_cast<uint16_t *>(stage)[rr * D + lane] = l16;
+            reinterpret_cast<uint16_t *>(stage)[rr * D + 64 + lane] = h16;
+            if constexpr (QLO) {
+                // second plane: fp16 remainder of the scaled f32 row
+                uint16_t *lop = reinterpret_cast<uint16_t *>(stage) + 16 * D;
+                lop[rr * D + lane] = f32_to_f16_rne(lo * sr - f16_to_f32(l16));
+                lop[rr * D + 64 + lane] = f32_to_f16_rne(hi * sr - f16_to_f32(h16));
+            }
+            if (lane == 0) qsr_l[rr] = a.qscale / sr;
+        }
+    }
+    __syncthreads();
+
+    // ── byte LUT (after the codebook table is visible) ───────────────────
+    {
+        const uint32_t *cbh = reinterpret_cast<const uint32_t *>(smem + kPreCbOff);
+        const uint32_t w0 = cbh[(tid >> 4) & 15];
+        uint32_t w1[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w1[i] = cbh[(tid >> 8) + 2 * i];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int e = (tid >> 4) + 32 * i;
+            const uint32_t hp = __builtin_amdgcn_perm(w1[i], w0, 0x05040100u);
+            const uint32_t lp = __builtin_amdgcn_perm(w1[i], w0, 0x07060302u);
+            *reinterpret_cast<uint4 *>(smem + kLutOff + e * 256 + (tid & 15) * 16) = make_uint4(hp, lp, hp, lp);
+        }
+    }
+
+    // ── per-lane B operands: q (exact fp16) for the scores ───────────────
+    half8_t bk[NCB][8], bgq[NCB][2], bkl[QLO ? NCB : 1][8];
+    float qsr[NCB];
+#pragma unroll
+    for (int c = 0; c < NCB; ++c) {
+        const uint16_t *qrow = reinterpret_cast<const uint16_t *>(stage) + (16 * c + n) * D;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const uint2 w = *reinterpret_cast<const uint2 *>(qrow + 32 * g + 4 * s);
+            bk[c][s] = as_half8(w.x, w.x, w.y, w.y);
+        }
+        qsr[c] = qsr_l[16 * c + n];
+        if constexpr (QLO) {
+            const uint16_t *lrow = reinterpret_cast<const uint16_t *>(stage) + 16 * D + (16 * c + n) * D;
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                const uint2 w = *reinterpret_cast<const uint2 *>(lrow + 32 * g + 4 * s);
+                bkl[c][s] = as_half8(w.x, w.x, w.y, w.y);
+            }
+        }
+    }
+    // G q (staged scale) on MFMA: A = q rows, B = G rows expanded by the sign LUT
+    __syncthreads();   // sign LUT visible
+    float4_t gacc[NCB][4];
+#pragma unroll
+    for (int c = 0; c < NCB; ++c)
+#pragma unroll
+        for (int ob = 0; ob < 4; ++ob) gacc[c][ob] = float4_t{0.f, 0.f, 0.f, 0.f};
+    if (QJL) {
+        const uint32_t *gh = a.g_bits + (int64_t)hk * QD * 4;
+#pragma unroll
+        for (int ob = 0; ob < 4; ++ob) {
+            const uint4 gw = *reinterpret_cast<const uint4 *>(gh + (16 * ob + n) * 4);
+            const uint32_t gws[4] = {gw.x, gw.y, gw.z, gw.w};
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const uint32_t byte = (gws[s] >> (8 * g)) & 0xffu;
+                const uint4 gv = *reinterpret_cast<const uint4 *>(smem + kSlutOff + byte * 16u);
+                const half8_t bg = as_half8(gv.x, gv.y, gv.z, gv.w);
+#pragma unroll
+                for (int c = 0; c < NCB; ++c) {
+                    const uint4 qv = *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(stage) +
+                                                                     (16 * c + n) * D + 32 * s + 8 * g);
+                    gacc[c][ob] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(qv.x, qv.y, qv.z, qv.w), bg,
+                                                                        gacc[c][ob], 0, 0, 0);
+                }
+            }
+        }
+    }
+    // gacc[c][ob][i] = (staged) G q for row 16 c + 4 g + i, output 16 ob + n:
+    // through the stage area (q is no longer needed) into B layout
+    float *gqs = reinterpret_cast<float *>(stage);     // [RW][64]
+#pragma unroll
+    for (int c = 0; c < NCB; ++c)
+#pragma unroll
+        for (int ob = 0; ob < 4; ++ob)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) gqs[(16 * c + 4 * g + i) * QD + 16 * ob + n] = gacc[c][ob][i];
+#pragma unroll
+    for (int c = 0; c < NCB; ++c) {
+        // B carries sqrt(2/pi) / D * 2^4 on the staged (2^k-scaled) G q; the
+        // A rows are signs * norm * 2^-4, so the QJL term lands in the score
+        // accumulator beside K . q and both take the row's scale * 2^-k
+        const float gsc = a.alpha_c * 16.0f;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const float *row = gqs + (16 * c + n) * QD + 32 * s + 8 * g;
+            uint32_t w[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) w[j] = QJL ? pack_h2(row[2 * j] * gsc, row[2 * j + 1] * gsc) : 0u;
+            bgq[c][s] = as_half8(w[0], w[1], w[2], w[3]);
+        }
+    }
+    __syncthreads();   // byte LUT complete
+
+    // ── key range of this wave: causal limits of its rows ─────────────────
+    const int s_begin = split * (int)a.split_len;
+    int s_end = (int)imin64(a.S, (int64_t)s_begin + a.split_len);
+    int lim[NCB];
+    bool rowok[NCB];
+#pragma unroll
+    for (int c = 0; c < NCB; ++c) {
+        const int rho = row0 + 16 * c + n;
+        rowok[c] = rho < nrows_total;
+        lim[c] = (a.causal_offset >= 0) ? (int)imin64(a.causal_offset + (rowok[c] ? rho : 0) / a.G, 0x7fffffff)
+                                        : 0x7fffffff;
+    }
+    int full_end = s_end;
+    if (a.causal_offset >= 0) {
+        const int rlo = imin(row0, nrows_total - 1), rhi = imin(row0 + RW - 1, nrows_total - 1);
+        const int64_t lo_lim = a.causal_offset + rlo / a.G, hi_lim = a.causal_offset + rhi / a.G;
+        full_end = (int)imin64((int64_t)s_end, lo_lim + 1);
+        s_end = (int)imin64((int64_t)s_end, hi_lim + 1);
+    }
+    const int64_t kv_base = (b * a.Hkv + hk) * a.S;
+    DecBufs P;
+    P.kn = __builtin_amdgcn_make_buffer_rsrc((void *)(a.k_nib + kv_base * 64), (short)0, s_end * 64, kBufWord3);
+    P.vn = __builtin_amdgcn_make_buffer_rsrc((void *)(a.v_nib + kv_base * 64), (short)0, s_end * 64, kBufWord3);
+    P.kq = __builtin_amdgcn_make_buffer_rsrc((void *)(QJL ? a.k_qjl + kv_base * 8 : a.k_nib), (short)0,
+                                             QJL ? s_end * 8 : 0, kBufWord3);
+    P.kr = __builtin_amdgcn_make_buffer_rsrc((void *)(QJL ? a.k_norms + kv_base : (const float *)a.k_nib), (short)0,
+                                             QJL ? s_end * 4 : 0, kBufWord3);
+    DecOffsets OFS;
+    OFS.k = (uint32_t)n * 64u + 16u * g;
+    OFS.sg = (uint32_t)n * 8u;
+    OFS.nr = 4u * n;
+    OFS.v = 256u * g + 4u * n;
+    const uint32_t laneoff = (uint32_t)(lane & 31) * 8u;
+    const half8_t ones = as_half8(0x3C003C00u, 0u, 0x3C003C00u, 0u);
+    const unsigned char *lut = smem + kLutOff;
+
+    float4_t oacc[NCB][8], lacc[NCB];
+    float m_run[NCB];
+#pragma unroll
+    for (int c = 0; c < NCB; ++c) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) oacc[c][k] = float4_t{0.f, 0.f, 0.f, 0.f};
+        lacc[c] = float4_t{0.f, 0.f, 0.f, 0.f};
+        m_run[c] = -INFINITY;
+    }
+
+    auto tile_step = [&](PreTileRaw &R, const int tt) {
+        const bool full = tt + kDecTile <= full_end;
+        float4_t acc[NCB][2];
+#pragma unroll
+        for (int c = 0; c < NCB; ++c)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) acc[c][u] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const uint32_t kw[4] = {R.k[u].x, R.k[u].y, R.k[u].z, R.k[u].w};
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                const uint2 e0 = *reinterpret_cast<const uint2 *>(lut + lut_addr(kw[s >> 1], laneoff, 2 * (s & 1)));
+                const uint2 e1 = *reinterpret_cast<const uint2 *>(lut + lut_addr(kw[s >> 1], laneoff, 2 * (s & 1) + 1));
+                const half8_t ak = pair_half8(e0, e1);
+#pragma unroll
+                for (int c = 0; c < NCB; ++c) {
+                    acc[c][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak, bk[c][s], acc[c][u], 0, 0, 0);
+                    if constexpr (QLO) acc[c][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak, bkl[c][s], acc[c][u], 0, 0, 0);
+                }
+            }
+            if (QJL) {
+                const _Float16 nh = (_Float16)(R.nr[u] * 0.0625f);
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    const uint32_t byte = __builtin_amdgcn_ubfe(s ? R.sg[u].y : R.sg[u].x, 8u * g, 8u);
+                    const uint4 sv = *reinterpret_cast<const uint4 *>(smem + ((byte << 4) | (uint32_t)kSlutOff));
+                    const half8_t as_ = as_half8(sv.x, sv.y, sv.z, sv.w) * nh;
+#pragma unroll
+                    for (int c = 0; c < NCB; ++c)
+                        acc[c][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_, bgq[c][s], acc[c][u], 0, 0, 0);
+                }
+            }
+        }
+        half8_t pb[NCB][2];
+#pragma unroll
+        for (int c = 0; c < NCB; ++c) {
+            float sc[8];
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    sc[4 * u + i] = acc[c][u][i] * qsr[c];
+            if (!full) {
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int tn = tt + 16 * u + 4 * g + i;
+                        if (tn >= s_end || tn > lim[c]) sc[4 * u + i] = -INFINITY;
+                    }
+            }
+            float mt = fmaxf(fmaxf(fmaxf(fmaxf(sc[0], sc[1]), sc[2]), fmaxf(fmaxf(sc[3], sc[4]), sc[5])), fmaxf(sc[6], sc[7]));
+            mt = max_over_groups(mt);
+            const bool need = mt > m_run[c] + 8.0f;
+            if (__builtin_amdgcn_ballot_w64(need)) {
+                const float f = need ? __builtin_amdgcn_exp2f(m_run[c] - mt) : 1.0f;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) oacc[c][k] *= f;
+                lacc[c] *= f;
+                m_run[c] = need ? mt : m_run[c];
+            }
+            const float m_use = (m_run[c] == -INFINITY) ? 0.0f : m_run[c];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const uint32_t p01 = cvt_pk_h2(__builtin_amdgcn_exp2f(sc[4 * u] - m_use), __builtin_amdgcn_exp2f(sc[4 * u + 1] - m_use));
+                const uint32_t p23 = cvt_pk_h2(__builtin_amdgcn_exp2f(sc[4 * u + 2] - m_use), __builtin_amdgcn_exp2f(sc[4 * u + 3] - m_use));
+                pb[c][u] = as_half8(p01, p01, p23, p23);
+                lacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb[c][u], lacc[c], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            uint32_t ev[2], od[2];
+#pragma unroll
+            for (int pr = 0; pr < 2; ++pr) {
+                const uint32_t va = R.v[4 * u + 2 * pr], vb = R.v[4 * u + 2 * pr + 1];
+                ev[pr] = ((vb << 4) & 0xF0F0F0F0u) | (va & 0x0F0F0F0Fu);
+                od[pr] = (vb & 0xF0F0F0F0u) | ((va >> 4) & 0x0F0F0F0Fu);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint2 e0 = *reinterpret_cast<const uint2 *>(lut + lut_addr(ev[0], laneoff, j));
+                const uint2 e1 = *reinterpret_cast<const uint2 *>(lut + lut_addr(ev[1], laneoff, j));
+                const half8_t ae = pair_half8(e0, e1);
+                const uint2 f0 = *reinterpret_cast<const uint2 *>(lut + lut_addr(od[0], laneoff, j));
+                const uint2 f1 = *reinterpret_cast<const uint2 *>(lut + lut_addr(od[1], laneoff, j));
+                const half8_t ao = pair_half8(f0, f1);
+#pragma unroll
+                for (int c = 0; c < NCB; ++c) {
+                    oacc[c][2 * j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ae, pb[c][u], oacc[c][2 * j], 0, 0, 0);
+                    oacc[c][2 * j + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ao, pb[c][u], oacc[c][2 * j + 1], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    // every key tile, in order, with the decode kernel's unconditional ring
+    constexpr int stride = kDecTile;
+    PreTileRaw ring[PF];
+#pragma unroll
+    for (int p = 0; p < PF - 1; ++p) pre_load<QJL>(ring[p], P, OFS, s_begin + p * stride);
+    int tt0 = s_begin;
+    for (; tt0 + (PF - 1) * stride < s_end; tt0 += PF * stride) {
+#pragma unroll
+        for (int p = 0; p < PF; ++p) {
+            __builtin_amdgcn_sched_barrier(0);
+            pre_load<QJL>(ring[(p + PF - 1) % PF], P, OFS, tt0 + (p + PF - 1) * stride);
+            __builtin_amdgcn_sched_barrier(0);
+            tile_step(ring[p], tt0 + p * stride);
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < PF - 1; ++p)
+        if (tt0 + p * stride < s_end) tile_step(ring[p], tt0 + p * stride);
+
+    // ── rows out (or split partials) ──────────────────────────────────────
+    const int64_t unit = (b * a.Hkv + hk) * a.n_rchunks + rc;
+#pragma unroll
+    for (int c = 0; c < NCB; ++c) {
+        const int rho = row0 + 16 * c + n;
+        if (!rowok[c]) continue;
+        const float l = lacc[c][0];
+        if (a.splits == 1) {
+            const int t = rho / a.G, hq = hk * a.G + (rho - t * a.G);
+            float *o = a.out + ((b * a.Hq + hq) * a.T + t) * D;
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) o[8 * (4 * g + i) + k] = oacc[c][k][i] / l;
+        } else {
+            const int rr = wave * RW + 16 * c + n;
+            float *wp = a.ws + ((unit * a.splits + split) * a.rows + rr) * (D + 2);
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) wp[8 * (4 * g + i) + k] = oacc[c][k][i];
+            if (g == 0) { wp[D] = m_run[c]; wp[D + 1] = l; }
+        }
+    }
+}
+
 // ── launch planning ─────────────────────────────────────────────────────
 
 struct Plan {
     bool dec128;       // D == 128: decode kernel with 8 query rows per block
+    bool prefill;      // D == 128 with many rows per kv head: prefill kernel
     int rows, n_rchunks, splits, nw, ncopy;
     int64_t split_len;
     size_t lds, ws_bytes;
@@ -1015,15 +1420,25 @@ static int device_cus() {
 
 static int64_t clamp64(int64_t v, int64_t lo, int64_t hi) { return v < lo ? lo : (v > hi ? hi : v); }
 
-static Plan make_plan(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int D) {
+static Plan make_plan(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int D, bool q32) {
     Plan p;
     const int G = Hq / Hkv;
     const int cus = device_cus();
-    p.dec128 = (D == 128);
-    p.rows = p.dec128 ? kDecRows : kRows;
+    p.prefill = (D == 128) && T * G > kPrefillMinRows;
+    p.dec128 = (D == 128) && !p.prefill;
+    p.rows = p.prefill ? kPreWaves * 16 * (q32 ? 1 : kPreNcb) : (p.dec128 ? kDecRows : kRows);
     p.n_rchunks = (int)((T * G + p.rows - 1) / p.rows);
     const int64_t units = B * (int64_t)Hkv * p.n_rchunks;
-    if (p.dec128) {
+    if (p.prefill) {
+        const int64_t tiles = (S + kDecTile - 1) / kDecTile;
+        int64_t splits = clamp64((cus + units - 1) / (units > 0 ? units : 1), 1, (tiles / 16) > 1 ? tiles / 16 : 1);
+        const int64_t tps = (tiles + splits - 1) / splits;
+        p.splits = (int)splits;
+        p.split_len = tps * kDecTile;
+        p.nw = kPreWaves;
+        p.ncopy = 32;
+        p.lds = kPreLdsBytes;
+    } else if (p.dec128) {
         const int64_t tiles = (S + kDecTile - 1) / kDecTile;
         int64_t splits = clamp64((cus + units - 1) / (units > 0 ? units : 1), 1, (tiles / 16) > 1 ? tiles / 16 : 1);
         const int64_t tps = (tiles + splits - 1) / splits;
@@ -1053,7 +1468,10 @@ using namespace omni;
 
 extern "C" size_t omni_attn_workspace_size(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int head_dim) {
     if (B <= 0 || Hq <= 0 || Hkv <= 0 || T <= 0 || S <= 0 || Hq % Hkv || !head_dim_ok(head_dim)) return 0;
-    return make_plan(B, Hq, Hkv, T, S, head_dim).ws_bytes;
+    // the prefill plan differs for f32 queries: size for either
+    const size_t a = make_plan(B, Hq, Hkv, T, S, head_dim, false).ws_bytes;
+    const size_t b = make_plan(B, Hq, Hkv, T, S, head_dim, true).ws_bytes;
+    return a > b ? a : b;
 }
 
 extern "C" int omni_attn(const void *q, int q_dtype, const uint8_t *k_nib, const uint8_t *k_qjl,
@@ -1073,7 +1491,7 @@ extern "C" int omni_attn(const void *q, int q_dtype, const uint8_t *k_nib, const
     OMNI_CHECK_ARG(isfinite(scale), "omni_attn: scale must be finite");
     OMNI_CHECK_ARG(S < (int64_t(1) << 25), "omni_attn: S must be < 2^25 tokens per sequence");
     OMNI_CHECK_ARG(T * (Hq / Hkv) < (int64_t(1) << 31), "omni_attn: T * (n_heads / n_kv_heads) must be < 2^31");
-    Plan p = make_plan(B, Hq, Hkv, T, S, head_dim);
+    Plan p = make_plan(B, Hq, Hkv, T, S, head_dim, q_dtype == OMNI_F32);
     OMNI_CHECK_ARG(Hkv <= 65535 && B * p.n_rchunks <= 2147483647LL && p.splits <= 2147483647,
                    "omni_attn: grid too large");
     if (p.ws_bytes > 0 && (workspace == nullptr || workspace_bytes < p.ws_bytes)) {
@@ -1094,7 +1512,16 @@ extern "C" int omni_attn(const void *q, int q_dtype, const uint8_t *k_nib, const
     a.wht_scale = inv_sqrt_dim_f32(head_dim);
     dim3 grid((unsigned)p.splits, (unsigned)Hkv, (unsigned)(B * p.n_rchunks));
     dim3 block(64 * p.nw);
-    if (p.dec128) {
+    if (p.prefill) {
+        const bool qlo = q_dtype == OMNI_F32;
+        if (with_qjl) {
+            if (qlo) hipLaunchKernelGGL((attn_prefill128_kernel<true, 1, 2, true>), grid, block, 0, as_stream(stream), a);
+            else hipLaunchKernelGGL((attn_prefill128_kernel<true, kPreNcb, 2, false>), grid, block, 0, as_stream(stream), a);
+        } else {
+            if (qlo) hipLaunchKernelGGL((attn_prefill128_kernel<false, 1, 2, true>), grid, block, 0, as_stream(stream), a);
+            else hipLaunchKernelGGL((attn_prefill128_kernel<false, kPreNcb, 2, false>), grid, block, 0, as_stream(stream), a);
+        }
+    } else if (p.dec128) {
         if (with_qjl)
             hipLaunchKernelGGL((attn_decode128_kernel<true, kDecPrefetch>), grid, block, 0, as_stream(stream), a);
         else

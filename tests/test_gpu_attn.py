@@ -232,3 +232,57 @@ def test_prepared_run_replays_in_hip_graph(device):
         assert torch.equal(att.out, eager), f"replay {i} differs from the eager result"
         att.run(other, x, ids)                        # eager work between replays
         torch.cuda.synchronize()
+
+
+# ── chunked prefill (T * G > 32 rows per kv head) ───────────────────────
+
+def _causal_mask(T, S, off):
+    mask = torch.zeros(1, 1, T, S)
+    for t in range(T):
+        mask[..., t, off + t + 1:] = float("-inf")
+    return mask
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,T,S,causal,dtype", [
+    (2, 32, 8, 64, 600, True, torch.bfloat16),       # C5 shape, scaled down
+    (1, 8, 2, 40, 333, False, torch.bfloat16),
+    (2, 16, 4, 37, 1000, True, torch.float16),        # ragged rows (148 per kv head)
+    (1, 32, 8, 20, 256, True, torch.float32),         # f32 q: hi + remainder operands
+    (1, 8, 1, 16, 2048, True, torch.bfloat16),        # one kv head: split-K + combine
+])
+@pytest.mark.parametrize("with_qjl", [True, False])
+def test_prefill_matches_oracle(device, B, Hq, Hkv, T, S, causal, dtype, with_qjl):
+    uid = 11
+    print(f"[prefill] B={B} Hq={Hq} Hkv={Hkv} T={T} S={S} causal={causal} {dtype} qjl={with_qjl}", flush=True)
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=2000 + S, user_id=uid)
+    q = _data.query((B, Hq, T, 128), seed=S + 3 * T, dtype=dtype)
+    off = S - T if causal else None
+    got = _run(device, q, kn, kq, kr, vn, cb, uid, with_qjl, causal_offset=off)
+    mask = _causal_mask(T, S, off) if causal else None
+    want = restate.fused_attn_python(q.float(), kn, kq, kr, vn, cb, uid, 1 / math.sqrt(128), with_qjl, mask=mask)
+    _assert_close(got, want, f"prefill B{B} Hq{Hq} Hkv{Hkv} T{T} S{S} {dtype} qjl{int(with_qjl)}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_prefill_rotate_q_in_kernel(device, dtype):
+    B, Hq, Hkv, T, S, uid = 2, 16, 4, 24, 500, 6
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=21, user_id=uid)
+    q = _data.query((B, Hq, T, 128), seed=22, dtype=dtype)
+    s = _data.sign_flip()
+    got = _run(device, q, kn, kq, kr, vn, cb, uid, rotate_q=True, sign_flip=s.to(device), causal_offset=S - T)
+    want = restate.fused_attn_python(restate.rotate(q, s).float(), kn, kq, kr, vn, cb, uid, 1 / math.sqrt(128), True,
+                                     mask=_causal_mask(T, S, S - T))
+    _assert_close(got, want, f"prefill rotate_q {dtype}")
+
+
+def test_prefill_large_and_tiny_query_rows(device):
+    """Per-row power-of-two scaling keeps bf16 rows far outside fp16 range exact."""
+    B, Hq, Hkv, T, S, uid = 1, 8, 2, 16, 300, 2
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=23, user_id=uid)
+    q = _data.query((B, Hq, T, 128), seed=24, dtype=torch.float32)
+    q[0, 0] *= 3e5           # beyond fp16 max
+    q[0, 1] *= 1e-7          # fp16 subnormal range
+    q = q.to(torch.bfloat16)
+    got = _run(device, q, kn, kq, kr, vn, cb, uid, scale=1e-6)
+    want = restate.fused_attn_python(q.float(), kn, kq, kr, vn, cb, uid, 1e-6, True)
+    _assert_close(got, want, "prefill extreme rows")
