@@ -53,12 +53,13 @@ struct AttnArgs {
     int with_qjl, rotate_q;
     int rows;                  // query rows per block (16: generic kernel, 8: D=128 decode kernel)
     float qscale;              // scale * log2(e)
-    float alpha_c;             // fp32 sqrt(2/pi)/D (qscale is already folded into G q)
+    float alpha_c;             // fp32 sqrt(2/pi)/D (the row scale multiplies the whole score)
     float wht_scale;
 };
 
 __device__ __forceinline__ int64_t imin64(int64_t x, int64_t y) { return x < y ? x : y; }
 __device__ __forceinline__ int imin(int x, int y) { return x < y ? x : y; }
+__device__ __forceinline__ int imax(int x, int y) { return x > y ? x : y; }
 
 __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
     return (uint32_t)f32_to_f16_rne(a) | ((uint32_t)f32_to_f16_rne(b) << 16);
@@ -93,7 +94,7 @@ struct Lds {
     static constexpr int QD = D / 2;
     __host__ __device__ static size_t lut_bytes(int ncopy) { return (size_t)256 * ncopy * 8 + 16 * 8; }
     __host__ __device__ static size_t comb_bytes(int nw) { (void)nw; return (size_t)(2 * kMaxWaves * kRows + kRows * D) * 4; }
-    __host__ __device__ static size_t fixed_bytes() { return (size_t)kRows * (D + QD) * 4; }
+    __host__ __device__ static size_t fixed_bytes() { return (size_t)kRows * (D + QD + 1) * 4; }
     static size_t total(int ncopy, int nw) {
         size_t a = lut_bytes(ncopy), c = comb_bytes(nw);
         return (a > c ? a : c) + fixed_bytes();
@@ -117,6 +118,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void attn_kernel(AttnArgs a) {
                                                                                  : Lds<D>::comb_bytes(nw);
     float *qs = reinterpret_cast<float *>(smem + var_bytes);
     float *gq = qs + kRows * D;
+    float *rsc = gq + kRows * QD;       // per row: scale * log2(e) / 2^k
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -173,6 +175,19 @@ __global__ __launch_bounds__(64 * kMaxWaves) void attn_kernel(AttnArgs a) {
         for (int d = 0; d < D; ++d) row[d] = round_to_dtype(row[d] * a.wht_scale, a.q_dtype);
     }
     __syncthreads();
+    if (tid < kRows) {
+        // row max |q| -> 2^k with max * 2^k in [2^14, 2^15): the scaled row
+        // and G q stay in fp16 range for any finite q
+        float *row = qs + tid * D;
+        float m = 0.0f;
+        for (int d = 0; d < D; ++d) m = fmaxf(m, fabsf(row[d]));
+        int ex = 0;
+        if (m > 0.0f && m < INFINITY) frexpf(m, &ex);
+        const float sr = ldexpf(1.0f, 15 - imax(ex, -100));
+        for (int d = 0; d < D; ++d) row[d] *= sr;
+        rsc[tid] = a.qscale / sr;
+    }
+    __syncthreads();
     if (a.with_qjl) {
         const uint32_t *gh = a.g_bits + (int64_t)hk * QD * (D / 32);
         for (int s = tid; s < kRows * QD; s += blockDim.x) {
@@ -200,23 +215,31 @@ __global__ __launch_bounds__(64 * kMaxWaves) void attn_kernel(AttnArgs a) {
         float v[4], lo[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            v[j] = row[j] * a.qscale;
+            v[j] = row[j];
             lo[j] = v[j] - f16_to_f32(f32_to_f16_rne(v[j]));
         }
         qb[s] = as_half4(pack_h2(v[0], v[1]), pack_h2(v[2], v[3]));
         qbl[s] = as_half4(pack_h2(lo[0], lo[1]), pack_h2(lo[2], lo[3]));
     }
-    half4_t gb[QSTEPS];
+    // sqrt(2/pi)/D G (2^k q) as fp16 hi + fp16 remainder (|.| <= 2^15 sqrt(2/pi))
+    half4_t gb[QSTEPS], gbl[QSTEPS];
 #pragma unroll
     for (int s = 0; s < QSTEPS; ++s) {
         if (a.with_qjl) {
             const float *row = gq + r * QD + g * (QD / 4) + 4 * s;
-            gb[s] = as_half4(pack_h2(row[0] * a.qscale, row[1] * a.qscale),
-                             pack_h2(row[2] * a.qscale, row[3] * a.qscale));
+            float gh[4], gl[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                gh[j] = row[j] * a.alpha_c;
+                gl[j] = gh[j] - f16_to_f32(f32_to_f16_rne(gh[j]));
+            }
+            gb[s] = as_half4(pack_h2(gh[0], gh[1]), pack_h2(gh[2], gh[3]));
+            gbl[s] = as_half4(pack_h2(gl[0], gl[1]), pack_h2(gl[2], gl[3]));
         } else {
-            gb[s] = as_half4(0u, 0u);
+            gb[s] = gbl[s] = as_half4(0u, 0u);
         }
     }
+    const float row_scale = rsc[r];
 
     // Causal limit for this lane's row.
     const int64_t rho = (int64_t)rc * kRows + r;
@@ -263,7 +286,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void attn_kernel(AttnArgs a) {
         }
 
         float4_t cacc = float4_t{0.f, 0.f, 0.f, 0.f};
-        float4_t alpha4 = float4_t{0.f, 0.f, 0.f, 0.f};
+        float4_t nrm4 = float4_t{0.f, 0.f, 0.f, 0.f};
         if (a.with_qjl) {
             uint32_t sb;
             if constexpr (D == 128) {
@@ -275,11 +298,12 @@ __global__ __launch_bounds__(64 * kMaxWaves) void attn_kernel(AttnArgs a) {
             for (int s = 0; s < QSTEPS; ++s) {
                 const uint2 e = qlut[(sb >> (4 * s)) & 0xfu];
                 cacc = __builtin_amdgcn_mfma_f32_16x16x16f16(as_half4(e.x, e.y), gb[s], cacc, 0, 0, 0);
+                cacc = __builtin_amdgcn_mfma_f32_16x16x16f16(as_half4(e.x, e.y), gbl[s], cacc, 0, 0, 0);
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int64_t tn = imin64(t0 + 4 * g + i, s_end - 1);
-                alpha4[i] = a.k_norms[kv_base + tn] * a.alpha_c;
+                nrm4[i] = a.k_norms[kv_base + tn];
             }
         }
 
@@ -289,7 +313,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void attn_kernel(AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int64_t tn = t0 + 4 * g + i;
-            float v = __builtin_fmaf(alpha4[i], cacc[i], sacc[i]);
+            float v = __builtin_fmaf(nrm4[i], cacc[i], sacc[i]) * row_scale;
             if (tn >= s_end || tn > key_limit) v = -INFINITY;
             sc[i] = v;
             mt = fmaxf(mt, v);
@@ -433,9 +457,13 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
 //            lo slots: columns 0-7 = Q_hi (both slots), columns 8-15 = Q_lo
 //            (hi slots only).  S_main(row n) = acc[n] + acc[n+8]
 //            = K_hi.Q_hi + K_lo.Q_hi + K_hi.Q_lo.
-//   QJL pass A = B+- (16 tok x 64), B = scale log2e G_h q in columns 0-7.
-//   score = S_main + alpha_t * qjl
-// One DPP row shift moves columns 8-15 onto 0-7.  PV contracts the 32
+//   QJL pass A = B+- (16 tok x 64), B = scale log2e sqrt(2/pi)/D G_h q:
+//            fp16 in columns 0-7, its fp16 remainder in 8-15, into a second
+//            accumulator; t = acc + norm * qacc (norms fp32, quad-broadcast
+//            by DPP), score = t[n] + t[n+8].
+// One DPP row shift moves columns 8-15 onto 0-7.
+// Twelve waves per block (three per SIMD, <= 168 VGPRs) each keep a 2-deep
+// ring of tiles in flight; waves 0-7 also own one query row in the prologue.  PV contracts the 32
 // tokens of the tile: O^T (128 x 16) += V^T_hi . P^T + V^T_lo . P^T, plus a
 // ones row that accumulates the softmax denominator from the same fp16 P.
 //
@@ -448,10 +476,11 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
 //                              B images for the scores, q hi/lo A images
 //                              for G q
 //               [86K, +64)     codebook as (fp16 hi, fp16 remainder) pairs
+//               [+64, +32)     per-row score scales
 constexpr int kDecRows = 8;
-constexpr int kDecWaves = 8;
+constexpr int kDecWaves = 12;
 constexpr int kDecTile = 32;
-constexpr int kDecPrefetch = 3;      // tiles in flight per wave (ring depth)
+constexpr int kDecPrefetch = 2;      // tiles in flight per wave (ring depth)
 constexpr int kLutOff = 0;
 constexpr int kLutBytes = 256 * 256;
 constexpr int kSlutOff = kLutBytes;
@@ -461,12 +490,14 @@ constexpr int kDecQsOff = kSlutOff + kSlutBytes;
 constexpr int kDecBkOff = kDecQsOff + kDecRows * (128 + 64) * 4;   // [row][quad][hi, lo] 16 B
 constexpr int kDecGaOff = kDecBkOff + kDecRows * 32 * 2 * 16;        // [row][8-dim group][hi, lo] 16 B
 constexpr int kDecCbOff = kDecGaOff + kDecRows * 16 * 2 * 16;       // 16 x (fp16 hi | remainder << 16)
-constexpr int kDecLdsBytes = kDecCbOff + 16 * 4;
+constexpr int kDecCscOff = kDecCbOff + 16 * 4;                     // per row: scale * log2(e) / 2^k
+constexpr int kDecLdsBytes = kDecCscOff + kDecRows * 4;
 // epilogue reuse of [0, 68K): per-wave O slabs (rows padded to 132 floats),
 // then per-wave running max and denominator
 constexpr int kObStride = 128 + 4;
 constexpr int kDecSlabBytes = kDecWaves * kDecRows * kObStride * 4;
 static_assert(kDecSlabBytes + 2 * kDecWaves * kDecRows * 4 <= kDecQsOff, "epilogue slabs overlap the query rows");
+static_assert(kDecWaves >= kDecRows, "one query row per wave in the prologue");
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 
@@ -479,6 +510,16 @@ __device__ __forceinline__ half8_t pair_half8(uint2 x, uint2 y) {
     return as_half8(x.x, x.y, y.x, y.y);
 }
 
+// Value of lane 4 * (lane / 4) + I (a broadcast within each quad).
+template <int I>
+__device__ __forceinline__ float dpp_quad_bcast_i(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), I * 0x55, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float dpp_quad_bcast(float v, int i) {
+    return i == 0 ? dpp_quad_bcast_i<0>(v) : i == 1 ? dpp_quad_bcast_i<1>(v) : i == 2 ? dpp_quad_bcast_i<2>(v)
+                                                                                      : dpp_quad_bcast_i<3>(v);
+}
+
 __device__ __forceinline__ float dpp_row_shl8(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x108, 0xf, 0xf, false));
 }
@@ -487,13 +528,6 @@ __device__ __forceinline__ float dpp_row_shl8(float v) {
 __device__ __forceinline__ uint32_t lut_addr(uint32_t w, uint32_t laneoff, int k) {
     return __builtin_amdgcn_perm(w, laneoff, 0x0C0C0000u | ((uint32_t)(4 + k) << 8));
 }
-
-struct DecTileRaw {
-    uint4 k[2];        // K nibbles: token t0 + 16u + (lane % 16), bytes 16g .. 16g + 15
-    uint2 sg[2];       // sign rows of the same tokens
-    float nr[2][4];    // norms of output tokens t0 + 16u + 4g + i
-    uint32_t v[8];     // V dword (lane % 16) of tokens t0 + 16(i/4) + 4g + i%4
-};
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
@@ -511,8 +545,16 @@ struct DecOffsets {
     uint32_t k, sg, nr, v;
 };
 
+// One 32-token tile as loaded, before any decoding.
+struct TileRaw {
+    uint4 k[2];        // K nibbles: token t0 + 16u + (lane % 16), bytes 16g .. 16g + 15
+    uint2 sg[2];       // sign rows of the same tokens
+    float nr[2];       // one norm per lane and half u; which token is set by the offsets
+    uint32_t v[8];     // V dword (lane % 16) of tokens t0 + 16(i/4) + 4g + i%4
+};
+
 template <bool QJL>
-__device__ __forceinline__ void dec_load(DecTileRaw &R, const DecBufs &P, const DecOffsets &O, int t0) {
+__device__ __forceinline__ void tile_load(TileRaw &R, const DecBufs &P, const DecOffsets &O, int t0) {
     // The tile offset goes into the per-lane offset, which the buffer range
     // check covers: tiles past the split end read as 0 and touch no memory.
     const uint32_t t = (uint32_t)t0;
@@ -524,9 +566,7 @@ __device__ __forceinline__ void dec_load(DecTileRaw &R, const DecBufs &P, const 
         if (QJL) {
             const u32x2_t sv = __builtin_amdgcn_raw_buffer_load_b64(P.kq, vsg + 128u * u, 0, 0);
             R.sg[u] = make_uint2(sv.x, sv.y);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                R.nr[u][i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(P.kr, vnr + 4u * (16 * u + i), 0, 0));
+            R.nr[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(P.kr, vnr + 64u * u, 0, 0));
         }
     }
 #pragma unroll
@@ -636,7 +676,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     DecOffsets OFS;
     OFS.k = (uint32_t)n * 64u + 16u * g;
     OFS.sg = (uint32_t)n * 8u;
-    OFS.nr = 16u * g;
+    OFS.nr = 16u * g + 4u * (n & 3);      // norm of token 4g + n % 4 (of each 16-token half)
     OFS.v = 256u * g + 4u * n;
 
     // ── prologue loads: branch-free buffer loads (an absent input gets a
@@ -675,9 +715,9 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     //    the split end they read 0), so the compiler counts outstanding
     //    loads exactly and waits only for the tile it consumes. ────────
     const int stride = nw * kDecTile;
-    DecTileRaw ring[PF];
+    TileRaw ring[PF];
 #pragma unroll
-    for (int p = 0; p < PF - 1; ++p) dec_load<QJL>(ring[p], P, OFS, s_begin + wave * kDecTile + p * stride);
+    for (int p = 0; p < PF - 1; ++p) tile_load<QJL>(ring[p], P, OFS, s_begin + wave * kDecTile + p * stride);
 
     // ── codebook as (fp16 hi, fp16 remainder) pairs (every lane stores
     //    entry lane % 16: same values, no branch) ──────────────────────
@@ -715,16 +755,30 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
             lo = round_to_dtype(lo * a.wht_scale, a.q_dtype);
             hi = round_to_dtype(hi * a.wht_scale, a.q_dtype);
         }
-        qs[wave * D + lane] = row_ok ? lo : 0.0f;
-        qs[wave * D + 64 + lane] = row_ok ? hi : 0.0f;
+        // row max |q| -> 2^k with max * 2^k in [2^14, 2^15): the scaled row
+        // and G q (|.| <= 128 * 2^15 * sqrt(2/pi) / 128) stay in fp16 range
+        // for any finite q; scores take scale * log2(e) * 2^-k
+        float m = row_ok ? fmaxf(fabsf(lo), fabsf(hi)) : 0.0f;
+#pragma unroll
+        for (int sh = 32; sh >= 1; sh >>= 1) m = fmaxf(m, __shfl_xor(m, sh));
+        int ex = 0;
+        if (m > 0.0f && m < INFINITY) frexpf(m, &ex);
+        const float sr = ldexpf(1.0f, 15 - imax(ex, -100));     // 2^k stays finite for tiny rows
+        if (wave < kDecRows) {
+            qs[wave * D + lane] = row_ok ? lo * sr : 0.0f;
+            qs[wave * D + 64 + lane] = row_ok ? hi * sr : 0.0f;
+            if (lane == 0) reinterpret_cast<float *>(smem + kDecCscOff)[wave] = a.qscale / sr;
+        }
     }
     // MFMA operand images of this row (read back by the same wave):
-    //   lanes 0-31, quad j = dims 4j..4j+3 of scale q: B slots
+    //   lanes 0-31, quad j = dims 4j..4j+3 of 2^k q: B slots
     //     hi [h0 h1 h0 h1 h2 h3 h2 h3], lo [l0 l1 0 0 l2 l3 0 0]
-    //   lanes 32-47, group j = dims 8j..8j+7 of q: A slots hi / lo
-    if (lane < 32) {
+    //   lanes 32-47, group j = dims 8j..8j+7 of 2^k q: A slots hi / lo
+    if (wave >= kDecRows) {
+        // no query row of its own
+    } else if (lane < 32) {
         const float4 v = *reinterpret_cast<const float4 *>(qs + wave * D + 4 * lane);
-        const float h[4] = {v.x * a.qscale, v.y * a.qscale, v.z * a.qscale, v.w * a.qscale};
+        const float h[4] = {v.x, v.y, v.z, v.w};
         float l[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) l[j] = h[j] - f16_to_f32(f32_to_f16_rne(h[j]));
@@ -751,7 +805,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
 
     // ── byte LUT: entry e at e * 256, 32 copies of (hi pair, lo pair);
     //    thread t writes 16-byte chunk t % 16 of entries (t >> 4) + 32 i ──
-    {
+    if (tid < 512) {
         const uint32_t *cbh = reinterpret_cast<const uint32_t *>(smem + kDecCbOff);
         const uint32_t w0 = cbh[(tid >> 4) & 15];           // low nibble, same for all i
         uint32_t w1[8];
@@ -810,16 +864,23 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
         const uint4 v = *reinterpret_cast<const uint4 *>(smem + kDecBkOff + ((rn * 32 + 8 * g + s) * 2 + (lo_col ? 1 : 0)) * 16);
         bk[s] = as_half8(v.x, v.y, v.z, v.w);
     }
-    // QJL B operand carries scale * log2(e) * sqrt(2/pi) / D, so a score
-    // needs only norm * (signs . B)
-    const float gscale = a.qscale * a.alpha_c;
+    // QJL B operand carries sqrt(2/pi) / D on G (2^k q) (fp16 in columns
+    // 0-7, its fp16 remainder in 8-15), so a score needs only
+    // norm * (signs . B) on top of the K pass, then the row's scale
+    const float gscale = a.alpha_c;
+    const float csc = reinterpret_cast<const float *>(smem + kDecCscOff)[rn];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
         uint32_t w[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const float *row = gq + rn * QD + 32 * s + 8 * g + 2 * j;
-            w[j] = (!lo_col && QJL) ? pack_h2(row[0] * gscale, row[1] * gscale) : 0u;
+            float g0 = row[0] * gscale, g1 = row[1] * gscale;
+            if (lo_col) {
+                g0 -= (float)(_Float16)g0;
+                g1 -= (float)(_Float16)g1;
+            }
+            w[j] = QJL ? pack_h2(g0, g1) : 0u;
         }
         bgq[s] = as_half8(w[0], w[1], w[2], w[3]);
     }
@@ -844,7 +905,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     float m_run = -INFINITY;
 
     // One 32-token tile: scores, online softmax, PV.
-    auto tile_step = [&](DecTileRaw &R, const int tt) {
+    auto tile_step = [&](TileRaw &R, const int tt) {
         const bool full = tt + kDecTile <= full_end;
 
         // scores: lane (n, g) holds tokens tt + 16u + 4g + i
@@ -870,11 +931,13 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                // columns 8-15 compute finite junk that never reaches
-                // columns 0-7 (MFMA columns are independent) nor the output
-                float v = acc[i] + dpp_row_shl8(acc[i]);
-                if (QJL) v = __builtin_fmaf(R.nr[u][i], qacc[i], v);
-                sc[4 * u + i] = v;
+                // token 4g + i's norm sits in lane 4 * (n / 4) + i of this row:
+                // a quad broadcast.  Columns 8-15 compute finite junk that
+                // never reaches columns 0-7 (MFMA columns are independent)
+                // nor the output.
+                float v = acc[i];
+                if (QJL) v = __builtin_fmaf(dpp_quad_bcast(R.nr[u], i), qacc[i], v);
+                sc[4 * u + i] = (v + dpp_row_shl8(v)) * csc;
             }
         }
         if (!full) {
@@ -939,7 +1002,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
 #pragma unroll
         for (int p = 0; p < PF; ++p) {
             __builtin_amdgcn_sched_barrier(0);
-            dec_load<QJL>(ring[(p + PF - 1) % PF], P, OFS, tt0 + (p + PF - 1) * stride);
+            tile_load<QJL>(ring[(p + PF - 1) % PF], P, OFS, tt0 + (p + PF - 1) * stride);
             __builtin_amdgcn_sched_barrier(0);
             tile_step(ring[p], tt0 + p * stride);
         }
@@ -1013,34 +1076,6 @@ constexpr int kPreStageOff = kPreCbOff + 64;                     // per wave: q 
 constexpr int kPreQsrOff = kPreStageOff + kPreWaves * 32 * 128 * 2;   // per wave: 32 x f32 score scales
 constexpr int kPreLdsBytes = kPreQsrOff + kPreWaves * 32 * 4;
 
-// Prefill tile: as DecTileRaw, but the norms are those of the A-operand rows
-// (token t0 + 16 u + (lane % 16)): the QJL sign rows are scaled by them.
-struct PreTileRaw {
-    uint4 k[2];
-    uint2 sg[2];
-    float nr[2];
-    uint32_t v[8];
-};
-
-template <bool QJL>
-__device__ __forceinline__ void pre_load(PreTileRaw &R, const DecBufs &P, const DecOffsets &O, int t0) {
-    const uint32_t t = (uint32_t)t0;
-    const uint32_t vk = O.k + t * 64u, vsg = O.sg + t * 8u, vnr = O.nr + t * 4u, vv = O.v + t * 64u;
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const u32x4_t kv4 = __builtin_amdgcn_raw_buffer_load_b128(P.kn, vk + 1024u * u, 0, 0);
-        R.k[u] = make_uint4(kv4.x, kv4.y, kv4.z, kv4.w);
-        if (QJL) {
-            const u32x2_t sv = __builtin_amdgcn_raw_buffer_load_b64(P.kq, vsg + 128u * u, 0, 0);
-            R.sg[u] = make_uint2(sv.x, sv.y);
-            R.nr[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(P.kr, vnr + 64u * u, 0, 0));
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-        R.v[i] = __builtin_amdgcn_raw_buffer_load_b32(P.vn, vv + 64u * (16 * (i / 4) + (i % 4)), 0, 0);
-}
-
 template <bool QJL, int NCB, int PF, bool QLO>
 __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArgs a) {
     constexpr int D = 128, QD = 64, RW = 16 * NCB;      // rows per wave
@@ -1102,7 +1137,7 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
             for (int sh = 32; sh >= 1; sh >>= 1) m = fmaxf(m, __shfl_xor(m, sh));
             int ex = 0;
             if (m > 0.0f && m < INFINITY) { frexpf(m, &ex); }
-            const float sr = ldexpf(1.0f, 15 - ex);       // m * sr in [2^14, 2^15)
+            const float sr = ldexpf(1.0f, 15 - imax(ex, -100));   // m * sr in [2^14, 2^15) unless m < 2^-101
             const uint16_t l16 = f32_to_f16_rne(lo * sr), h16 = f32_to_f16_rne(hi * sr);
             reinterpret_cast<uint16_t *>(stage)[rr * D + lane] = l16;
             reinterpret_cast<uint16_t *>(stage)[rr * D + 64 + lane] = h16;
@@ -1134,7 +1169,7 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
     }
 
     // ── per-lane B operands: q (exact fp16) for the scores ───────────────
-    half8_t bk[NCB][8], bgq[NCB][2], bkl[QLO ? NCB : 1][8];
+    half8_t bk[NCB][8], bgq[NCB][2], bgl[NCB][2], bkl[QLO ? NCB : 1][8];
     float qsr[NCB];
 #pragma unroll
     for (int c = 0; c < NCB; ++c) {
@@ -1178,6 +1213,13 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
                                                                      (16 * c + n) * D + 32 * s + 8 * g);
                     gacc[c][ob] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(qv.x, qv.y, qv.z, qv.w), bg,
                                                                         gacc[c][ob], 0, 0, 0);
+                    if constexpr (QLO) {
+                        // the f32 row's fp16 remainder plane
+                        const uint4 lv = *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(stage) +
+                                                                         16 * D + (16 * c + n) * D + 32 * s + 8 * g);
+                        gacc[c][ob] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(lv.x, lv.y, lv.z, lv.w), bg,
+                                                                            gacc[c][ob], 0, 0, 0);
+                    }
                 }
             }
         }
@@ -1193,17 +1235,22 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
             for (int i = 0; i < 4; ++i) gqs[(16 * c + 4 * g + i) * QD + 16 * ob + n] = gacc[c][ob][i];
 #pragma unroll
     for (int c = 0; c < NCB; ++c) {
-        // B carries sqrt(2/pi) / D * 2^4 on the staged (2^k-scaled) G q; the
-        // A rows are signs * norm * 2^-4, so the QJL term lands in the score
-        // accumulator beside K . q and both take the row's scale * 2^-k
-        const float gsc = a.alpha_c * 16.0f;
+        // B carries sqrt(2/pi) / D on the staged (2^k-scaled) G q (fp16 hi in
+        // bgq, fp16 remainder in bgl); norm * (signs . B) joins K . q in the
+        // score accumulator and both take the row's scale * 2^-k
+        const float gsc = a.alpha_c;
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
             const float *row = gqs + (16 * c + n) * QD + 32 * s + 8 * g;
-            uint32_t w[4];
+            uint32_t w[4], wl[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) w[j] = QJL ? pack_h2(row[2 * j] * gsc, row[2 * j + 1] * gsc) : 0u;
+            for (int j = 0; j < 4; ++j) {
+                const float g0 = row[2 * j] * gsc, g1 = row[2 * j + 1] * gsc;
+                w[j] = QJL ? pack_h2(g0, g1) : 0u;
+                wl[j] = QJL ? pack_h2(g0 - (float)(_Float16)g0, g1 - (float)(_Float16)g1) : 0u;
+            }
             bgq[c][s] = as_half8(w[0], w[1], w[2], w[3]);
+            bgl[c][s] = as_half8(wl[0], wl[1], wl[2], wl[3]);
         }
     }
     __syncthreads();   // byte LUT complete
@@ -1238,7 +1285,7 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
     DecOffsets OFS;
     OFS.k = (uint32_t)n * 64u + 16u * g;
     OFS.sg = (uint32_t)n * 8u;
-    OFS.nr = 4u * n;
+    OFS.nr = 16u * g + 4u * (n & 3);      // norm of token 4g + n % 4 (of each 16-token half)
     OFS.v = 256u * g + 4u * n;
     const uint32_t laneoff = (uint32_t)(lane & 31) * 8u;
     const half8_t ones = as_half8(0x3C003C00u, 0u, 0x3C003C00u, 0u);
@@ -1254,7 +1301,7 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
         m_run[c] = -INFINITY;
     }
 
-    auto tile_step = [&](PreTileRaw &R, const int tt) {
+    auto tile_step = [&](TileRaw &R, const int tt) {
         const bool full = tt + kDecTile <= full_end;
         float4_t acc[NCB][2];
 #pragma unroll
@@ -1263,6 +1310,9 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
             for (int u = 0; u < 2; ++u) acc[c][u] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
+            float4_t qacc[NCB];
+#pragma unroll
+            for (int c = 0; c < NCB; ++c) qacc[c] = float4_t{0.f, 0.f, 0.f, 0.f};
             const uint32_t kw[4] = {R.k[u].x, R.k[u].y, R.k[u].z, R.k[u].w};
 #pragma unroll
             for (int s = 0; s < 8; ++s) {
@@ -1276,15 +1326,24 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
                 }
             }
             if (QJL) {
-                const _Float16 nh = (_Float16)(R.nr[u] * 0.0625f);
+                // signs . (G q as fp16 hi + fp16 remainder), then + norm * that
+                // (norm of token 4g + i: a quad broadcast, fp32)
 #pragma unroll
                 for (int s = 0; s < 2; ++s) {
                     const uint32_t byte = __builtin_amdgcn_ubfe(s ? R.sg[u].y : R.sg[u].x, 8u * g, 8u);
                     const uint4 sv = *reinterpret_cast<const uint4 *>(smem + ((byte << 4) | (uint32_t)kSlutOff));
-                    const half8_t as_ = as_half8(sv.x, sv.y, sv.z, sv.w) * nh;
+                    const half8_t s8 = as_half8(sv.x, sv.y, sv.z, sv.w);
 #pragma unroll
-                    for (int c = 0; c < NCB; ++c)
-                        acc[c][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_, bgq[c][s], acc[c][u], 0, 0, 0);
+                    for (int c = 0; c < NCB; ++c) {
+                        qacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(s8, bgq[c][s], qacc[c], 0, 0, 0);
+                        qacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(s8, bgl[c][s], qacc[c], 0, 0, 0);
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float nri = dpp_quad_bcast(R.nr[u], i);
+#pragma unroll
+                    for (int c = 0; c < NCB; ++c) acc[c][u][i] = __builtin_fmaf(nri, qacc[c][i], acc[c][u][i]);
                 }
             }
         }
@@ -1353,15 +1412,15 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
 
     // every key tile, in order, with the decode kernel's unconditional ring
     constexpr int stride = kDecTile;
-    PreTileRaw ring[PF];
+    TileRaw ring[PF];
 #pragma unroll
-    for (int p = 0; p < PF - 1; ++p) pre_load<QJL>(ring[p], P, OFS, s_begin + p * stride);
+    for (int p = 0; p < PF - 1; ++p) tile_load<QJL>(ring[p], P, OFS, s_begin + p * stride);
     int tt0 = s_begin;
     for (; tt0 + (PF - 1) * stride < s_end; tt0 += PF * stride) {
 #pragma unroll
         for (int p = 0; p < PF; ++p) {
             __builtin_amdgcn_sched_barrier(0);
-            pre_load<QJL>(ring[(p + PF - 1) % PF], P, OFS, tt0 + (p + PF - 1) * stride);
+            tile_load<QJL>(ring[(p + PF - 1) % PF], P, OFS, tt0 + (p + PF - 1) * stride);
             __builtin_amdgcn_sched_barrier(0);
             tile_step(ring[p], tt0 + p * stride);
         }
@@ -1444,7 +1503,7 @@ static Plan make_plan(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int D, b
         const int64_t tps = (tiles + splits - 1) / splits;
         p.splits = (int)splits;
         p.split_len = tps * kDecTile;
-        p.nw = kDecWaves;          // one query row per wave in the prologue
+        p.nw = kDecWaves;
         p.ncopy = 32;
         p.lds = kDecLdsBytes;
     } else {

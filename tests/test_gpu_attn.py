@@ -160,6 +160,14 @@ def test_attn_head_dim_32(device):
     got = _run(device, q, kn, kq, kr, vn, cb, uid)
     want = restate.fused_attn_python(q.float(), kn, kq, kr, vn, cb, uid, 1 / math.sqrt(32), True)
     _assert_close(got, want, "d32")
+    # sharp softmax and rows outside fp16 range
+    q2 = q * 200.0
+    q2[0, 0] *= 3e5
+    q2[1, 1] *= 1e-9
+    got = _run(device, q2, kn, kq, kr, vn, cb, uid)
+    want = restate.fused_attn_python(q2.float(), kn, kq, kr, vn, cb, uid, 1 / math.sqrt(32), True)
+    assert torch.isfinite(got).all()
+    _assert_close(got, want, "d32 extreme rows")
 
 
 def test_attn_shared_codebook(device):
@@ -273,6 +281,38 @@ def test_prefill_rotate_q_in_kernel(device, dtype):
     want = restate.fused_attn_python(restate.rotate(q, s).float(), kn, kq, kr, vn, cb, uid, 1 / math.sqrt(128), True,
                                      mask=_causal_mask(T, S, S - T))
     _assert_close(got, want, f"prefill rotate_q {dtype}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_attn_large_and_tiny_query_rows(device, dtype):
+    """Decode rows far outside fp16 range (and near f32's smallest normals)
+    keep their accuracy: each row is scaled by a power of two in-kernel."""
+    B, Hq, Hkv, T, S, uid = 2, 8, 2, 1, 300, 2
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=25, user_id=uid)
+    q = _data.query((B, Hq, T, 128), seed=26, dtype=torch.float32)
+    q[0, 0] *= 3e5           # beyond fp16 max
+    q[0, 1] *= 1e-7          # fp16 subnormal range
+    q[1, 2] *= 1e30
+    q[1, 3] *= 1e-36         # f32 near its smallest normal
+    q = q.to(dtype)
+    for scale in (1e-6, 1 / math.sqrt(128)):
+        got = _run(device, q, kn, kq, kr, vn, cb, uid, scale=scale)
+        want = restate.fused_attn_python(q.float(), kn, kq, kr, vn, cb, uid, scale, True)
+        assert torch.isfinite(got).all()
+        _assert_close(got, want, f"decode extreme rows {dtype} scale {scale:.3g}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_prefill_extreme_q_no_overflow(device, dtype):
+    """Sharp softmax (q x 200) amplifies score rounding; the prefill tile path
+    must stay within the bar."""
+    B, Hq, Hkv, T, S, uid = 1, 4, 2, 32, 200, 0
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=12, user_id=uid)
+    q = (torch.randn(B, Hq, T, 128, generator=_data.gen(13)) * 200.0).to(dtype)
+    got = _run(device, q, kn, kq, kr, vn, cb, uid)
+    assert torch.isfinite(got).all()
+    want = restate.fused_attn_python(q.float(), kn, kq, kr, vn, cb, uid, 1 / math.sqrt(128), True)
+    _assert_close(got, want, f"prefill q x200 {dtype}")
 
 
 def test_prefill_large_and_tiny_query_rows(device):
