@@ -513,7 +513,9 @@ __device__ __forceinline__ half8_t pair_half8(uint2 x, uint2 y) {
 // Value of lane 4 * (lane / 4) + I (a broadcast within each quad).
 template <int I>
 __device__ __forceinline__ float dpp_quad_bcast_i(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), I * 0x55, 0xf, 0xf, false));
+    // every source lane exists (no old value needed), so the move can fold
+    // into the consuming VOP2 instruction as its DPP operand
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), I * 0x55, 0xf, 0xf, true));
 }
 __device__ __forceinline__ float dpp_quad_bcast(float v, int i) {
     return i == 0 ? dpp_quad_bcast_i<0>(v) : i == 1 ? dpp_quad_bcast_i<1>(v) : i == 2 ? dpp_quad_bcast_i<2>(v)
@@ -950,7 +952,8 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
                 }
         }
 
-        // online softmax (exp2 domain), lazy rescale
+        // online softmax (exp2 domain), lazy rescale.  Logits are rounded
+        // before the max is taken, so every exponent below is <= 8 exactly.
         float mt = fmaxf(fmaxf(fmaxf(fmaxf(sc[0], sc[1]), sc[2]), fmaxf(fmaxf(sc[3], sc[4]), sc[5])), fmaxf(sc[6], sc[7]));
         mt = max_over_groups(mt);
         const bool need = mt > m_run + 8.0f;

@@ -302,6 +302,21 @@ def test_attn_large_and_tiny_query_rows(device, dtype):
         _assert_close(got, want, f"decode extreme rows {dtype} scale {scale:.3g}")
 
 
+@pytest.mark.parametrize("T", [1, 3, 40])          # decode kernel, D=128 decode with 12 rows, prefill tiles
+@pytest.mark.parametrize("scale", [-0.3, 0.0])
+def test_attn_negative_and_zero_scale(device, T, scale):
+    """The score scale's sign is folded into the query rows; a zero scale is a
+    uniform softmax over the visible keys (causal masks still apply)."""
+    B, Hq, Hkv, S, uid = 1, 8, 2, 100, 4
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=27, user_id=uid)
+    q = _data.query((B, Hq, T, 128), seed=28, dtype=torch.bfloat16)
+    off = S - T
+    got = _run(device, q, kn, kq, kr, vn, cb, uid, scale=scale, causal_offset=off)
+    want = restate.fused_attn_python(q.float(), kn, kq, kr, vn, cb, uid, scale, True, mask=_causal_mask(T, S, off))
+    assert torch.isfinite(got).all()
+    _assert_close(got, want, f"scale {scale} T{T}")
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_prefill_extreme_q_no_overflow(device, dtype):
     """Sharp softmax (q x 200) amplifies score rounding; the prefill tile path
