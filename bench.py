@@ -42,7 +42,7 @@ BYTES_PER_TOKEN_HEAD = 64 + 8 + 4 + 64     # K nibbles + K signs + K norm (f32) 
 # (FETCH_SIZE reads half the copied bytes -> x2.0; WRITE_SIZE reads them
 # exactly -> x1.0).  Recorded in profiles/attn_decode128_c3.md; re-measure
 # after any change to the decode kernel.
-C3_TRAFFIC = {"fetch_kib": 143686.5, "fetch_scale": 2.0, "write_kib": 512.0, "write_scale": 1.0}
+C3_TRAFFIC = {"fetch_kib": 143632.9, "fetch_scale": 2.0, "write_kib": 512.0, "write_scale": 1.0}
 
 
 def log(msg: str) -> None:
@@ -125,25 +125,43 @@ def wall_graph(fn, steps, warmup):
 
 def cpu_baseline_c3(kn, kq, kr, vn, cb, q, sign, uid, budget_s):
     """The reference's CPU path (rotate_queries + _fused_attn_python, restated
-    in oracle/) on whole sequences of the C3 batch until `budget_s` elapses."""
+    in oracle/) over the whole C3 batch, sequence by sequence (bounded host
+    memory): one untimed warm-up sequence, then full passes over the batch
+    with every host core until `budget_s` elapses (at least one pass); the
+    median pass is reported.  A single-thread rate is taken on the first
+    sequences for about a fifth of the budget.  Returns (seconds per pass,
+    passes, threads, single-thread seconds per sequence, sequences timed)."""
     import torch
     from oracle import restate
-    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    threads = len(os.sched_getaffinity(0))
+    prev = torch.get_num_threads()
     cbc, sc = cb.cpu(), sign.cpu()
-    B, Hkv, S, _ = kn.shape
-    done, t_total = 0, 0.0
-    for b in range(B):
+    B = kn.shape[0]
+    host = [t.cpu() for t in (kn, kq, kr, vn)]
+    qh = q.cpu()
+
+    def one(b):
         sl = slice(b, b + 1)
-        args = [t[sl].cpu() for t in (kn, kq, kr, vn)]
-        qb = q[sl].cpu()
+        qr = restate.rotate(qh[sl], sc)
+        restate.fused_attn_python(qr, *[t[sl] for t in host], cbc, uid, 1 / math.sqrt(128), True)
+
+    torch.set_num_threads(threads)
+    one(0)
+    passes, t_begin = [], time.perf_counter()
+    while not passes or time.perf_counter() - t_begin < budget_s:
         t0 = time.perf_counter()
-        qr = restate.rotate(qb, sc)
-        restate.fused_attn_python(qr, *args, cbc, uid, 1 / math.sqrt(128), True)
-        t_total += time.perf_counter() - t0
-        done += 1
-        if t_total >= budget_s:
-            break
-    return done, t_total
+        for b in range(B):
+            one(b)
+        passes.append(time.perf_counter() - t0)
+    torch.set_num_threads(1)
+    n1, t1 = 0, 0.0
+    while n1 < B and (n1 == 0 or t1 < budget_s / 5):
+        t0 = time.perf_counter()
+        one(n1)
+        t1 += time.perf_counter() - t0
+        n1 += 1
+    torch.set_num_threads(prev)
+    return statistics.median(passes), len(passes), threads, t1 / n1, n1
 
 
 def main() -> int:
@@ -182,6 +200,10 @@ def main() -> int:
     cbuf2 = torch.empty_like(cbuf)
     cbuf2.copy_(cbuf)
     torch.cuda.synchronize()
+    # STREAM-style probe: the same device copy, timed (read + write bytes)
+    copy_t = statistics.median(per_call_events(lambda: cbuf2.copy_(cbuf), 10, 2, stream))
+    copy_gbs = 2 * COPY_BYTES / copy_t / 1e9
+    log(f"[bench] device copy probe: {copy_gbs:.0f} GB/s (256 MiB read + 256 MiB written)")
     del cbuf, cbuf2
 
     uid, D = 42, 128
@@ -228,6 +250,8 @@ def main() -> int:
                                "INT4 Lloyd-Max + 1-bit QJL K, INT4 V, bf16 query, rotate_q in-kernel",
                    "bytes_per_step": bytes_step, "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
                    "launch": "K back-to-back eager calls", "graph_us_per_step": round(t_graph * 1e6, 2)},
+        "hbm_copy_probe": {"GB_s": round(copy_gbs, 1), "bytes": 2 * COPY_BYTES,
+                           "note": "torch device-to-device copy of 256 MiB, median of 10 HIP-event timings"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": c3_traffic,
                      "kernel": "omni::attn_decode128_kernel (+ attn_combine_kernel<128> when split-K)",
@@ -295,19 +319,36 @@ def main() -> int:
         log(f"[bench] C5: {t5 * 1e6:.0f} us -> {tf5:.1f} TFLOP/s ({tf5 / 2500:.1%} of fp16 dense MFMA peak)")
         del kn5, kq5, kr5, vn5, att5
 
+        # C5 at head_dim 32 (the generalized codec: 16 B nibbles, 2 B signs)
+        D32 = 32
+        log("[bench] C5 (head_dim 32): prefill 8 x 512 queries over 8 x 16384 cached tokens (causal)")
+        kn6, kq6, kr6, vn6 = make_cache(B5, Hkv, S5, D32, dev, 57, uid, cb, None)
+        q6 = torch.randn(B5, Hq, T5, D32, generator=torch.Generator(device=dev).manual_seed(58), device=dev).to(torch.bfloat16)
+        att6 = PackedKVAttention(kn6, kq6, kr6, vn6, cb, n_heads=Hq, q_tokens=T5, user_id=uid, causal_offset=off5)
+        t6 = wall_eager(lambda: att6.run(q6), max(3, args.steps // 10), 1)
+        fl6 = 2 * 2 * B5 * Hq * keys * D32 + 2 * B5 * Hq * keys * (D32 // 2)
+        tf6 = fl6 / t6 / 1e12
+        result["prefill_c5_d32"] = {"us_per_call": round(t6 * 1e6, 1), "TFLOP_s": round(tf6, 2), "flops_per_call": fl6,
+                                    "frac_of_fp16_dense_peak": round(tf6 / 2500.0, 4),
+                                    "note": "head_dim 32 variant of C5 (no reference implementation at D=32)"}
+        log(f"[bench] C5 (head_dim 32): {t6 * 1e6:.0f} us -> {tf6:.1f} TFLOP/s")
+        del kn6, kq6, kr6, vn6, att6
+
     # ── CPU baseline (reference CPU path restated in oracle/) ────────────
     if not args.no_cpu:
-        log(f"[bench] CPU baseline: oracle on C3 sequences, ~{args.cpu_budget_s:.0f} s budget")
-        n_seq, t_cpu = cpu_baseline_c3(kn, kq, kr, vn, cb, q, sign, uid, args.cpu_budget_s)
+        log(f"[bench] CPU baseline: oracle on the C3 batch, ~{args.cpu_budget_s:.0f} s budget")
+        t_pass, n_pass, cores, t_seq1, n_seq1 = cpu_baseline_c3(kn, kq, kr, vn, cb, q, sign, uid, args.cpu_budget_s)
         b_seq = Hkv * S * BYTES_PER_TOKEN_HEAD + Hq * D * 2 + Hq * D * 4
-        cores = len(os.sched_getaffinity(0))
-        result["cpu_baseline"] = {"value": round(b_seq * n_seq / t_cpu / 1e9, 4), "unit": "GB/s",
+        result["cpu_baseline"] = {"value": round(bytes_step / t_pass / 1e9, 4), "unit": "GB/s",
                                   "cores": cores, "kind": "port",
-                                  "sample": f"{n_seq} of 32 C3 sequences (8 kv heads x 8192 tokens each): "
-                                            f"rotate_queries + dequantize_heads + reference_attn, fp32 torch, "
-                                            f"{t_cpu:.2f} s",
+                                  "sample": f"whole C3 batch (32 sequences x 8 kv heads x 8192 tokens), median of "
+                                            f"{n_pass} passes of {t_pass:.2f} s after one warm-up sequence: "
+                                            f"rotate_queries + dequantize_heads + reference_attn, fp32 torch",
+                                  "single_thread": {"value": round(b_seq / t_seq1 / 1e9, 4), "unit": "GB/s",
+                                                    "sample": f"{n_seq1} sequences, {t_seq1:.2f} s each"},
                                   "cpu": platform.processor() or platform.machine()}
-        log(f"[bench] CPU: {n_seq} seq in {t_cpu:.2f} s")
+        log(f"[bench] CPU: {t_pass:.2f} s per C3 batch ({n_pass} passes, {cores} threads); "
+            f"1 thread {t_seq1:.2f} s per sequence")
 
     print(json.dumps(result), flush=True)
     return 0

@@ -140,6 +140,9 @@ int omni_lora_apply(const void *q, int q_dtype, const void *x, const void *A, co
  * rotated space); 0 reproduces omni_attn, which takes q as given.
  * Output f32 (B, Hq, T, D).  `workspace` must hold
  * omni_attn_workspace_size(...) bytes (may be 0 -> NULL allowed).
+ * Domain: codebook centroids within fp16 range (|c| <= 65504; they are held
+ * as fp16 hi + fp16 remainder pairs), S < 2^25; query rows of any finite
+ * magnitude (each row is scaled by a power of two in-kernel).
  * Replaces omni_attn / OmniAttention.forward / _fused_attn_triton /
  * _fused_attn_python (omnistack_rs/kernels/fused_attention.py:320-396,
  * :435-466, :471-565).

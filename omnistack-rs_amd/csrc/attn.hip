@@ -477,6 +477,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
 //                              for G q
 //               [86K, +64)     codebook as (fp16 hi, fp16 remainder) pairs
 //               [+64, +32)     per-row score scales
+//               [+32, +16)     tile counter (dynamic tile claims)
 constexpr int kDecRows = 8;
 constexpr int kDecWaves = 12;
 constexpr int kDecTile = 32;
@@ -491,7 +492,8 @@ constexpr int kDecBkOff = kDecQsOff + kDecRows * (128 + 64) * 4;   // [row][quad
 constexpr int kDecGaOff = kDecBkOff + kDecRows * 32 * 2 * 16;        // [row][8-dim group][hi, lo] 16 B
 constexpr int kDecCbOff = kDecGaOff + kDecRows * 16 * 2 * 16;       // 16 x (fp16 hi | remainder << 16)
 constexpr int kDecCscOff = kDecCbOff + 16 * 4;                     // per row: scale * log2(e) / 2^k
-constexpr int kDecLdsBytes = kDecCscOff + kDecRows * 4;
+constexpr int kDecCntOff = kDecCscOff + kDecRows * 4;                // next unclaimed tile of the block
+constexpr int kDecLdsBytes = kDecCntOff + 16;
 // epilogue reuse of [0, 68K): per-wave O slabs (rows padded to 132 floats),
 // then per-wave running max and denominator
 constexpr int kObStride = 128 + 4;
@@ -647,6 +649,13 @@ __device__ __forceinline__ void wht128_lanes(float &lo, float &hi, int lane) {
     hi = a - b;
 }
 
+// Next tile index of the block (wave-uniform): lane 0 bumps the LDS counter.
+__device__ __forceinline__ int claim_tile(int *cnt, int lane) {
+    int v = 0;
+    if (lane == 0) v = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    return __builtin_amdgcn_readfirstlane(v);
+}
+
 template <bool QJL, int PF>
 __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs a) {
     constexpr int D = 128, QD = 64;
@@ -713,13 +722,12 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
         (void *)(a.g_bits + (QJL ? (int64_t)hk * QD * 4 : 0)), (short)0, (QJL && wave < QD / 16) ? QD * 16 : 0, kBufWord3);
     const u32x4_t gw = __builtin_amdgcn_raw_buffer_load_b128(GB, (uint32_t)(16 * wave + n) * 16u, 0, 0);
 
-    // ── first cache tiles in flight.  Prefetches are unconditional (past
-    //    the split end they read 0), so the compiler counts outstanding
-    //    loads exactly and waits only for the tile it consumes. ────────
-    const int stride = nw * kDecTile;
+    // ── first cache tile in flight (tile `wave` of the split).  Loads are
+    //    unconditional (past the split end they read 0), so the compiler
+    //    counts outstanding loads exactly and waits only for the tile it
+    //    consumes. ──────────────────────────────────────────────────────
     TileRaw ring[PF];
-#pragma unroll
-    for (int p = 0; p < PF - 1; ++p) tile_load<QJL>(ring[p], P, OFS, s_begin + wave * kDecTile + p * stride);
+    tile_load<QJL>(ring[0], P, OFS, s_begin + wave * kDecTile);
 
     // ── codebook as (fp16 hi, fp16 remainder) pairs (every lane stores
     //    entry lane % 16: same values, no branch) ──────────────────────
@@ -728,6 +736,8 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
         *reinterpret_cast<uint32_t *>(smem + kDecCbOff + 4 * (lane & 15)) =
             (uint32_t)h | ((uint32_t)f32_to_f16_rne(cb_mine - f16_to_f32(h)) << 16);
     }
+    // tiles 0 .. nw - 1 are taken statically (one per wave, already in flight)
+    if (tid == 0) *reinterpret_cast<int *>(smem + kDecCntOff) = nw;
     // ── sign byte -> eight +-1.0 halves (threads 0..255) ──────────────
     if (tid < 256) {
         const int e = tid;
@@ -997,23 +1007,34 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
         }
     };
 
-    // Full groups of PF tiles: each step first prefetches the tile PF - 1
-    // steps ahead (unconditionally), so the loop body never branches around
-    // a load and the compiler's wait counts keep PF - 1 tiles in flight.
-    int tt0 = s_begin + wave * kDecTile;
-    for (; tt0 + (PF - 1) * stride < s_end; tt0 += PF * stride) {
-#pragma unroll
-        for (int p = 0; p < PF; ++p) {
-            __builtin_amdgcn_sched_barrier(0);
-            tile_load<QJL>(ring[(p + PF - 1) % PF], P, OFS, tt0 + (p + PF - 1) * stride);
-            __builtin_amdgcn_sched_barrier(0);
-            tile_step(ring[p], tt0 + p * stride);
-        }
+    // Tiles are claimed dynamically from the block's LDS counter: the waves
+    // sharing a SIMD do not progress at the same rate (the issue arbiter
+    // favours the oldest), and static round-robin tiles would leave the
+    // youngest waves running alone at the end.  Each step claims the tile
+    // after next (its result is needed one step later, so the atomic's
+    // latency hides behind the LUT traffic), prefetches the next tile
+    // (unconditionally: past the split end it reads 0 and touches no
+    // memory) and consumes the current one.
+    static_assert(PF == 2, "the dynamic tile loop alternates two ring slots");
+    int *tile_cnt = reinterpret_cast<int *>(smem + kDecCntOff);
+    int t_cur = s_begin + wave * kDecTile;
+    int c_nxt = claim_tile(tile_cnt, lane);
+    for (;;) {
+        if (t_cur >= s_end) break;
+        const int t_nxt = s_begin + c_nxt * kDecTile;
+        c_nxt = claim_tile(tile_cnt, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        tile_load<QJL>(ring[1], P, OFS, t_nxt);
+        __builtin_amdgcn_sched_barrier(0);
+        tile_step(ring[0], t_cur);
+        if (t_nxt >= s_end) break;
+        t_cur = s_begin + c_nxt * kDecTile;
+        c_nxt = claim_tile(tile_cnt, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        tile_load<QJL>(ring[0], P, OFS, t_cur);
+        __builtin_amdgcn_sched_barrier(0);
+        tile_step(ring[1], t_nxt);
     }
-    // the last (up to PF - 1) tiles are already in ring[0 ..]
-#pragma unroll
-    for (int p = 0; p < PF - 1; ++p)
-        if (tt0 + p * stride < s_end) tile_step(ring[p], tt0 + p * stride);
 
     // ── combine waves (deterministic order) ──────────────────────────
     __syncthreads();   // LUTs are dead from here on

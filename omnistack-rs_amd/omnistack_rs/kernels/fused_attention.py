@@ -202,6 +202,8 @@ class PackedKVAttention:
         dev = _lib.require_device(k_nibbles, v_nibbles)
         from .quantize import _prep_codebooks
         self.cb, self.per_head = _prep_codebooks(codebooks, Hkv, dev)
+        if not bool((self.cb.abs() <= 65504.0).all()):
+            raise ValueError("codebook centroids must lie within fp16 range (|c| <= 65504)")
         self.kn, self.vn = k_nibbles.contiguous(), v_nibbles.contiguous()
         self.kq = k_qjl.contiguous() if with_qjl else None
         self.kr = k_norms.to(torch.float32).contiguous() if with_qjl else None

@@ -185,6 +185,9 @@ def test_attn_rejects_bad_shapes(device):
         _run(device, torch.randn(1, 3, 1, 128), kn, kq, kr, vn, cb, 0)
     with pytest.raises(ValueError):
         _run(device, torch.randn(1, 4, 1, 128), kn, kq, kr, vn[:, :, :8], cb, 0)
+    from omnistack_rs.kernels.fused_attention import PackedKVAttention
+    with pytest.raises(ValueError, match="fp16 range"):
+        PackedKVAttention(*(t.to(device) for t in (kn, kq, kr, vn)), (cb * 1e5).to(device), n_heads=4, user_id=0)
 
 
 def _prepared(device, B=4, Hq=32, Hkv=8, S=300, uid=9, L=16, rank=8, hidden=128):
