@@ -475,8 +475,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
 //               [74K, 86K)     query rows as MFMA operands: (scale q) hi/lo
 //                              B images for the scores, q hi/lo A images
 //                              for G q
-//               [86K, +64)     codebook as (fp16 hi, fp16 remainder) pairs
-//               [+64, +32)     per-row score scales
+//               [86K, +32)     per-row score scales
 //               [+32, +16)     tile counter (dynamic tile claims)
 constexpr int kDecRows = 8;
 constexpr int kDecWaves = 12;
@@ -490,8 +489,7 @@ static_assert((kSlutOff & (kSlutOff - 1)) == 0 && kSlutOff >= kSlutBytes, "sign 
 constexpr int kDecQsOff = kSlutOff + kSlutBytes;
 constexpr int kDecBkOff = kDecQsOff + kDecRows * (128 + 64) * 4;   // [row][quad][hi, lo] 16 B
 constexpr int kDecGaOff = kDecBkOff + kDecRows * 32 * 2 * 16;        // [row][8-dim group][hi, lo] 16 B
-constexpr int kDecCbOff = kDecGaOff + kDecRows * 16 * 2 * 16;       // 16 x (fp16 hi | remainder << 16)
-constexpr int kDecCscOff = kDecCbOff + 16 * 4;                     // per row: scale * log2(e) / 2^k
+constexpr int kDecCscOff = kDecGaOff + kDecRows * 16 * 2 * 16;      // per row: scale * log2(e) / 2^k
 constexpr int kDecCntOff = kDecCscOff + kDecRows * 4;                // next unclaimed tile of the block
 constexpr int kDecLdsBytes = kDecCntOff + 16;
 // epilogue reuse of [0, 68K): per-wave O slabs (rows padded to 132 floats),
@@ -729,13 +727,9 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     TileRaw ring[PF];
     tile_load<QJL>(ring[0], P, OFS, s_begin + wave * kDecTile);
 
-    // ── codebook as (fp16 hi, fp16 remainder) pairs (every lane stores
-    //    entry lane % 16: same values, no branch) ──────────────────────
-    {
-        const uint16_t h = f32_to_f16_rne(cb_mine);
-        *reinterpret_cast<uint32_t *>(smem + kDecCbOff + 4 * (lane & 15)) =
-            (uint32_t)h | ((uint32_t)f32_to_f16_rne(cb_mine - f16_to_f32(h)) << 16);
-    }
+    // ── centroid lane % 16 as an (fp16 hi, fp16 remainder) pair ────────
+    const uint16_t cb_h16 = f32_to_f16_rne(cb_mine);
+    const uint32_t cb_pair = (uint32_t)cb_h16 | ((uint32_t)f32_to_f16_rne(cb_mine - f16_to_f32(cb_h16)) << 16);
     // tiles 0 .. nw - 1 are taken statically (one per wave, already in flight)
     if (tid == 0) *reinterpret_cast<int *>(smem + kDecCntOff) = nw;
     // ── sign byte -> eight +-1.0 halves (threads 0..255) ──────────────
@@ -747,90 +741,88 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
             w[k] = (((e >> (2 * k)) & 1) ? 0x3C00u : 0xBC00u) | ((((e >> (2 * k + 1)) & 1) ? 0x3C00u : 0xBC00u) << 16);
         *reinterpret_cast<uint4 *>(smem + kSlutOff + e * 16) = make_uint4(w[0], w[1], w[2], w[3]);
     }
-    // ── this wave's query row: (sign flip,) WHT, round to the q dtype ──
-    {
-        float lo, hi;
-        if (q32) {
-            lo = __uint_as_float(q32_lo);
-            hi = __uint_as_float(q32_hi);
-        } else if (a.q_dtype == OMNI_BF16) {
-            lo = __uint_as_float(q16_lo << 16);
-            hi = __uint_as_float(q16_hi << 16);
-        } else {
-            lo = f16_to_f32((uint16_t)q16_lo);
-            hi = f16_to_f32((uint16_t)q16_hi);
-        }
-        lo = (sf_lo & 0x80u) ? -lo : lo;
-        hi = (sf_hi & 0x80u) ? -hi : hi;
-        if (a.rotate_q) {
-            wht128_lanes(lo, hi, lane);
-            lo = round_to_dtype(lo * a.wht_scale, a.q_dtype);
-            hi = round_to_dtype(hi * a.wht_scale, a.q_dtype);
-        }
-        // row max |q| -> 2^k with max * 2^k in [2^14, 2^15): the scaled row
-        // and G q (|.| <= 128 * 2^15 * sqrt(2/pi) / 128) stay in fp16 range
-        // for any finite q; scores take scale * log2(e) * 2^-k
-        float m = row_ok ? fmaxf(fabsf(lo), fabsf(hi)) : 0.0f;
+    if (wave >= kDecRows) {
+        // ── byte LUT, built by the waves without a query row while the
+        //    others rotate theirs: entry e at e * 256, 32 copies of (hi
+        //    pair, lo pair); thread t writes 16-byte chunk t % 16 of the
+        //    entries with low nibble t / 16 (high nibble i) ──────────────
+        static_assert(kDecWaves - kDecRows == 4, "four LUT-building waves (256 threads)");
+        const int t = tid - 64 * kDecRows;
+        const uint32_t w0 = __shfl(cb_pair, (t >> 4) & 15);      // low nibble's centroid
 #pragma unroll
-        for (int sh = 32; sh >= 1; sh >>= 1) m = fmaxf(m, __shfl_xor(m, sh));
-        int ex = 0;
-        if (m > 0.0f && m < INFINITY) frexpf(m, &ex);
-        const float sr = ldexpf(1.0f, 15 - imax(ex, -100));     // 2^k stays finite for tiny rows
-        if (wave < kDecRows) {
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t w1 = __builtin_amdgcn_readlane(cb_pair, i);   // high nibble's centroid
+            const int e = (t >> 4) + 16 * i;
+            const uint32_t hp = __builtin_amdgcn_perm(w1, w0, 0x05040100u);   // (hi c0, hi c1)
+            const uint32_t lp = __builtin_amdgcn_perm(w1, w0, 0x07060302u);   // (lo c0, lo c1)
+            *reinterpret_cast<uint4 *>(smem + kLutOff + e * 256 + (t & 15) * 16) = make_uint4(hp, lp, hp, lp);
+        }
+    } else {
+        // ── this wave's query row: (sign flip,) WHT, round to the q dtype ──
+        {
+            float lo, hi;
+            if (q32) {
+                lo = __uint_as_float(q32_lo);
+                hi = __uint_as_float(q32_hi);
+            } else if (a.q_dtype == OMNI_BF16) {
+                lo = __uint_as_float(q16_lo << 16);
+                hi = __uint_as_float(q16_hi << 16);
+            } else {
+                lo = f16_to_f32((uint16_t)q16_lo);
+                hi = f16_to_f32((uint16_t)q16_hi);
+            }
+            lo = (sf_lo & 0x80u) ? -lo : lo;
+            hi = (sf_hi & 0x80u) ? -hi : hi;
+            if (a.rotate_q) {
+                wht128_lanes(lo, hi, lane);
+                lo = round_to_dtype(lo * a.wht_scale, a.q_dtype);
+                hi = round_to_dtype(hi * a.wht_scale, a.q_dtype);
+            }
+            // row max |q| -> 2^k with max * 2^k in [2^14, 2^15): the scaled row
+            // and G q (|.| <= 128 * 2^15 * sqrt(2/pi) / 128) stay in fp16 range
+            // for any finite q; scores take scale * log2(e) * 2^-k
+            float m = row_ok ? fmaxf(fabsf(lo), fabsf(hi)) : 0.0f;
+#pragma unroll
+            for (int sh = 32; sh >= 1; sh >>= 1) m = fmaxf(m, __shfl_xor(m, sh));
+            int ex = 0;
+            if (m > 0.0f && m < INFINITY) frexpf(m, &ex);
+            const float sr = ldexpf(1.0f, 15 - imax(ex, -100));     // 2^k stays finite for tiny rows
             qs[wave * D + lane] = row_ok ? lo * sr : 0.0f;
             qs[wave * D + 64 + lane] = row_ok ? hi * sr : 0.0f;
             if (lane == 0) reinterpret_cast<float *>(smem + kDecCscOff)[wave] = a.qscale / sr;
         }
-    }
-    // MFMA operand images of this row (read back by the same wave):
-    //   lanes 0-31, quad j = dims 4j..4j+3 of 2^k q: B slots
-    //     hi [h0 h1 h0 h1 h2 h3 h2 h3], lo [l0 l1 0 0 l2 l3 0 0]
-    //   lanes 32-47, group j = dims 8j..8j+7 of 2^k q: A slots hi / lo
-    if (wave >= kDecRows) {
-        // no query row of its own
-    } else if (lane < 32) {
-        const float4 v = *reinterpret_cast<const float4 *>(qs + wave * D + 4 * lane);
-        const float h[4] = {v.x, v.y, v.z, v.w};
-        float l[4];
+        // MFMA operand images of this row (read back by the same wave):
+        //   lanes 0-31, quad j = dims 4j..4j+3 of 2^k q: B slots
+        //     hi [h0 h1 h0 h1 h2 h3 h2 h3], lo [l0 l1 0 0 l2 l3 0 0]
+        //   lanes 32-47, group j = dims 8j..8j+7 of 2^k q: A slots hi / lo
+        if (lane < 32) {
+            const float4 v = *reinterpret_cast<const float4 *>(qs + wave * D + 4 * lane);
+            const float h[4] = {v.x, v.y, v.z, v.w};
+            float l[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) l[j] = h[j] - f16_to_f32(f32_to_f16_rne(h[j]));
-        uint4 *dst = reinterpret_cast<uint4 *>(smem + kDecBkOff + (wave * 32 + lane) * 32);
-        dst[0] = make_uint4(pack_h2(h[0], h[1]), pack_h2(h[0], h[1]), pack_h2(h[2], h[3]), pack_h2(h[2], h[3]));
-        dst[1] = make_uint4(pack_h2(l[0], l[1]), 0u, pack_h2(l[2], l[3]), 0u);
-    } else if (QJL && lane < 48) {
-        const int j = lane - 32;
-        const float4 v0 = *reinterpret_cast<const float4 *>(qs + wave * D + 8 * j);
-        const float4 v1 = *reinterpret_cast<const float4 *>(qs + wave * D + 8 * j + 4);
-        const float x[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-        uint32_t hw[4], lw[4];
+            for (int j = 0; j < 4; ++j) l[j] = h[j] - f16_to_f32(f32_to_f16_rne(h[j]));
+            uint4 *dst = reinterpret_cast<uint4 *>(smem + kDecBkOff + (wave * 32 + lane) * 32);
+            dst[0] = make_uint4(pack_h2(h[0], h[1]), pack_h2(h[0], h[1]), pack_h2(h[2], h[3]), pack_h2(h[2], h[3]));
+            dst[1] = make_uint4(pack_h2(l[0], l[1]), 0u, pack_h2(l[2], l[3]), 0u);
+        } else if (QJL && lane < 48) {
+            const int j = lane - 32;
+            const float4 v0 = *reinterpret_cast<const float4 *>(qs + wave * D + 8 * j);
+            const float4 v1 = *reinterpret_cast<const float4 *>(qs + wave * D + 8 * j + 4);
+            const float x[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            uint32_t hw[4], lw[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            hw[k] = pack_h2(x[2 * k], x[2 * k + 1]);
-            lw[k] = pack_h2(x[2 * k] - f16_to_f32(f32_to_f16_rne(x[2 * k])),
-                            x[2 * k + 1] - f16_to_f32(f32_to_f16_rne(x[2 * k + 1])));
+            for (int k = 0; k < 4; ++k) {
+                hw[k] = pack_h2(x[2 * k], x[2 * k + 1]);
+                lw[k] = pack_h2(x[2 * k] - f16_to_f32(f32_to_f16_rne(x[2 * k])),
+                                x[2 * k + 1] - f16_to_f32(f32_to_f16_rne(x[2 * k + 1])));
+            }
+            uint4 *dst = reinterpret_cast<uint4 *>(smem + kDecGaOff + (wave * 16 + j) * 32);
+            dst[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+            dst[1] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
         }
-        uint4 *dst = reinterpret_cast<uint4 *>(smem + kDecGaOff + (wave * 16 + j) * 32);
-        dst[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-        dst[1] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
     }
     __syncthreads();
 
-    // ── byte LUT: entry e at e * 256, 32 copies of (hi pair, lo pair);
-    //    thread t writes 16-byte chunk t % 16 of entries (t >> 4) + 32 i ──
-    if (tid < 512) {
-        const uint32_t *cbh = reinterpret_cast<const uint32_t *>(smem + kDecCbOff);
-        const uint32_t w0 = cbh[(tid >> 4) & 15];           // low nibble, same for all i
-        uint32_t w1[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) w1[i] = cbh[(tid >> 8) + 2 * i];   // high nibble (e >> 4)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int e = (tid >> 4) + 32 * i;
-            const uint32_t hp = __builtin_amdgcn_perm(w1[i], w0, 0x05040100u);   // (hi c0, hi c1)
-            const uint32_t lp = __builtin_amdgcn_perm(w1[i], w0, 0x07060302u);   // (lo c0, lo c1)
-            *reinterpret_cast<uint4 *>(smem + kLutOff + e * 256 + (tid & 15) * 16) = make_uint4(hp, lp, hp, lp);
-        }
-    }
 
     if (QJL && wave < QD / 16) {
         // GQ (rows x 64) = Q (rows x 128) . G_h^T on MFMA, one 16-column block
