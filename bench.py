@@ -171,8 +171,13 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-budget-s", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--no-extras", action="store_true", help="C3 (and the CPU baseline) only")
+    ap.add_argument("--only", default="",
+                    help="comma-separated sections to run (c3, c2, c4, c5, c5d32), for profiling one "
+                         "configuration; the JSON line then carries only those sections")
     args = ap.parse_args()
+    sections = set(args.only.split(",")) if args.only else (
+        {"c3"} if args.no_extras else {"c3", "c2", "c4", "c5", "c5d32"})
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -211,55 +216,53 @@ def main() -> int:
     cb1 = calibrate_codebook(torch.randn(1 << 16, generator=torch.Generator().manual_seed(11)), max_iters=100)
 
     # ── C3: decode at 8K context ─────────────────────────────────────────
-    B, Hq, Hkv, S = 32, 32, 8, 8192
+    Hq, Hkv = 32, 8
     cb = cb1.reshape(1, 16).repeat(Hkv, 1).to(dev)
-    log("[bench] C3: encoding 32 x 8 x 8192 K/V")
-    kn, kq, kr, vn = make_cache(B, Hkv, S, D, dev, 42, uid, cb, sign)
-    q = torch.randn(B, Hq, 1, D, generator=torch.Generator(device=dev).manual_seed(43), device=dev).to(torch.bfloat16)
-    att = PackedKVAttention(kn, kq, kr, vn, cb, n_heads=Hq, user_id=uid, rotate_q=True, sign_flip=sign)
-    bytes_step = B * Hkv * S * BYTES_PER_TOKEN_HEAD + q.numel() * 2 + B * Hq * D * 4 + Hkv * 16 * 4 + Hkv * 64 * 16
-    log(f"[bench] C3: timing {args.steps} steps (warmup {args.warmup}); split-K workspace {att.ws_bytes} B")
-    # One call is long enough that back-to-back eager launches keep the GPU
-    # busy; `value` uses them (a graph of the same steps is reported too).
-    step = lambda: att.run(q)
-    t_step = wall_eager(step, args.steps, args.warmup)
-    t_graph = wall_graph(step, args.steps, args.warmup)
-    per = per_call_events(step, args.steps, 2, stream)
-    value = bytes_step / t_step / 1e9
-    ev_mean = statistics.fmean(per)
-    achieved = bytes_step / ev_mean / 1e9
-    log(f"[bench] C3: {t_step * 1e6:.1f} us/step (eager), {t_graph * 1e6:.1f} us/step (graph), "
-        f"{ev_mean * 1e6:.1f} us/call (events) -> {value:.0f} GB/s ({value / HBM_PEAK_GBS:.1%} of peak)")
-
-    c3_traffic = round(1024 * (C3_TRAFFIC["fetch_kib"] * C3_TRAFFIC["fetch_scale"]
-                                + C3_TRAFFIC["write_kib"] * C3_TRAFFIC["write_scale"]))
     result = {
         "metric": "compressed-KV decode attn HBM GB/s (% peak) @8K ctx; users/sec @B=64,L=50",
-        "value": round(value, 1),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(t_step * 1e3, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f16",
-        "data": "synthetic",
-        "config": {"workload": "C3 decode: 32 seq x 8192 cached tokens, 32 q / 8 kv heads, head_dim 128, "
-                               "INT4 Lloyd-Max + 1-bit QJL K, INT4 V, bf16 query, rotate_q in-kernel",
-                   "bytes_per_step": bytes_step, "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
-                   "launch": "K back-to-back eager calls", "graph_us_per_step": round(t_graph * 1e6, 2)},
+        "value": None, "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16", "data": "synthetic",
         "hbm_copy_probe": {"GB_s": round(copy_gbs, 1), "bytes": 2 * COPY_BYTES,
                            "note": "torch device-to-device copy of 256 MiB, median of 10 HIP-event timings"},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": c3_traffic,
-                     "kernel": "omni::attn_decode128_kernel (+ attn_combine_kernel<128> when split-K)",
-                     "avg_call_us_events": round(ev_mean * 1e6, 2)},
     }
+    if "c3" in sections:
+        B, S = 32, 8192
+        log("[bench] C3: encoding 32 x 8 x 8192 K/V")
+        kn, kq, kr, vn = make_cache(B, Hkv, S, D, dev, 42, uid, cb, sign)
+        q = torch.randn(B, Hq, 1, D, generator=torch.Generator(device=dev).manual_seed(43), device=dev).to(torch.bfloat16)
+        att = PackedKVAttention(kn, kq, kr, vn, cb, n_heads=Hq, user_id=uid, rotate_q=True, sign_flip=sign)
+        bytes_step = B * Hkv * S * BYTES_PER_TOKEN_HEAD + q.numel() * 2 + B * Hq * D * 4 + Hkv * 16 * 4 + Hkv * 64 * 16
+        log(f"[bench] C3: timing {args.steps} steps (warmup {args.warmup}); split-K workspace {att.ws_bytes} B")
+        # One call is long enough that back-to-back eager launches keep the GPU
+        # busy; `value` uses them (a graph of the same steps is reported too).
+        step = lambda: att.run(q)
+        t_step = wall_eager(step, args.steps, args.warmup)
+        t_graph = wall_graph(step, args.steps, args.warmup)
+        per = per_call_events(step, args.steps, 2, stream)
+        value = bytes_step / t_step / 1e9
+        ev_mean = statistics.fmean(per)
+        achieved = bytes_step / ev_mean / 1e9
+        log(f"[bench] C3: {t_step * 1e6:.1f} us/step (eager), {t_graph * 1e6:.1f} us/step (graph), "
+            f"{ev_mean * 1e6:.1f} us/call (events) -> {value:.0f} GB/s ({value / HBM_PEAK_GBS:.1%} of peak)")
 
-    # ── extras: C2 serving and C4 encode ─────────────────────────────────
-    if not args.no_extras:
+        c3_traffic = round(1024 * (C3_TRAFFIC["fetch_kib"] * C3_TRAFFIC["fetch_scale"]
+                                    + C3_TRAFFIC["write_kib"] * C3_TRAFFIC["write_scale"]))
+        result.update({
+            "value": round(value, 1),
+            "ms_per_step": round(t_step * 1e3, 5),
+            "config": {"workload": "C3 decode: 32 seq x 8192 cached tokens, 32 q / 8 kv heads, head_dim 128, "
+                                   "INT4 Lloyd-Max + 1-bit QJL K, INT4 V, bf16 query, rotate_q in-kernel",
+                       "bytes_per_step": bytes_step, "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+                       "launch": "K back-to-back eager calls", "graph_us_per_step": round(t_graph * 1e6, 2)},
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": c3_traffic,
+                         "kernel": "omni::attn_decode128_kernel (+ attn_combine_kernel<128> when split-K)",
+                         "avg_call_us_events": round(ev_mean * 1e6, 2)},
+        })
+
+    # ── extras: C2 serving, C4 encode, C5 prefill ────────────────────────
+    if "c2" in sections:
         B2, S2, L2, R2, HID = 64, 50, 256, 8, 128
         log("[bench] C2: serving B=64 S=50 with 256 x rank-8 LoRA")
         kn2, kq2, kr2, vn2 = make_cache(B2, Hkv, S2, D, dev, 52, uid, cb, sign)
@@ -285,6 +288,7 @@ def main() -> int:
         log(f"[bench] C2: p50 {p50 * 1e6:.1f} us p99 {p99 * 1e6:.1f} us (events), "
             f"{t2 * 1e6:.1f} us/step graph -> {B2 / t2:.0f} users/s")
 
+    if "c4" in sections:
         B4, T4 = 16, 4096
         log("[bench] C4: encode 16 x 4096 x 8 K and V")
         g4 = torch.Generator(device=dev).manual_seed(46)
@@ -299,16 +303,17 @@ def main() -> int:
         log(f"[bench] C4: {t4 * 1e6:.0f} us -> {bytes4 / t4 / 1e9:.0f} GB/s")
         del k4, v4
 
-        # C5: chunked prefill, a 512-token bf16 query chunk at the end of a
-        # 16384-token cache (query t sees keys 0 .. 15872 + t)
-        B5, T5, S5 = 8, 512, 16384
-        off5 = S5 - T5
+    # C5: chunked prefill, a 512-token bf16 query chunk at the end of a
+    # 16384-token cache (query t sees keys 0 .. 15872 + t)
+    B5, T5, S5 = 8, 512, 16384
+    off5 = S5 - T5
+    keys = T5 * off5 + T5 * (T5 + 1) // 2            # visible (query, key) pairs per (b, q head)
+    if "c5" in sections:
         log("[bench] C5: prefill 8 x 512 queries over 8 x 16384 cached tokens (causal)")
         kn5, kq5, kr5, vn5 = make_cache(B5, Hkv, S5, D, dev, 55, uid, cb, sign)
         q5 = torch.randn(B5, Hq, T5, D, generator=torch.Generator(device=dev).manual_seed(56), device=dev).to(torch.bfloat16)
         att5 = PackedKVAttention(kn5, kq5, kr5, vn5, cb, n_heads=Hq, q_tokens=T5, user_id=uid, causal_offset=off5)
         t5 = wall_eager(lambda: att5.run(q5), max(3, args.steps // 10), 1)
-        keys = T5 * off5 + T5 * (T5 + 1) // 2            # visible (query, key) pairs per (b, q head)
         fl_qkpv = 2 * 2 * B5 * Hq * keys * D             # Q.K and P.V
         fl_qjl = 2 * B5 * Hq * keys * (D // 2)           # signs . (G q) score correction
         tf5 = (fl_qkpv + fl_qjl) / t5 / 1e12
@@ -319,6 +324,7 @@ def main() -> int:
         log(f"[bench] C5: {t5 * 1e6:.0f} us -> {tf5:.1f} TFLOP/s ({tf5 / 2500:.1%} of fp16 dense MFMA peak)")
         del kn5, kq5, kr5, vn5, att5
 
+    if "c5d32" in sections:
         # C5 at head_dim 32 (the generalized codec: 16 B nibbles, 2 B signs)
         D32 = 32
         log("[bench] C5 (head_dim 32): prefill 8 x 512 queries over 8 x 16384 cached tokens (causal)")
@@ -335,7 +341,7 @@ def main() -> int:
         del kn6, kq6, kr6, vn6, att6
 
     # ── CPU baseline (reference CPU path restated in oracle/) ────────────
-    if not args.no_cpu:
+    if not args.no_cpu and "c3" in sections:
         log(f"[bench] CPU baseline: oracle on the C3 batch, ~{args.cpu_budget_s:.0f} s budget")
         t_pass, n_pass, cores, t_seq1, n_seq1 = cpu_baseline_c3(kn, kq, kr, vn, cb, q, sign, uid, args.cpu_budget_s)
         b_seq = Hkv * S * BYTES_PER_TOKEN_HEAD + Hq * D * 2 + Hq * D * 4

@@ -1028,7 +1028,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
         tile_step(ring[1], t_nxt);
     }
 
-    // ── combine waves (deterministic order) ──────────────────────────
+    // ── combine waves (in wave order) ───────────────────────────────
     __syncthreads();   // LUTs are dead from here on
     float *ob = reinterpret_cast<float *>(smem);                     // [nw][kDecRows][kObStride]
     float *wm = reinterpret_cast<float *>(smem + kDecSlabBytes);     // [nw][kDecRows] running max

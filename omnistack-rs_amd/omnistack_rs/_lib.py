@@ -137,6 +137,18 @@ def g_bits(seeds: tuple, head_dim: int, device: torch.device) -> torch.Tensor:
     return t
 
 
+def sign_flip_i8(sign_flip: torch.Tensor, head_dim: int, device: torch.device) -> torch.Tensor:
+    """The +-1 sign-flip vector as contiguous int8 on `device` (the kernels
+    flip where the value is negative).  An int8 vector already there is used
+    as is: no conversion kernels on the per-call path."""
+    if sign_flip.numel() != head_dim:
+        raise ValueError(f"sign_flip must have {head_dim} entries, got {sign_flip.numel()}")
+    sf = sign_flip.reshape(-1)
+    if sf.dtype != torch.int8:
+        sf = torch.where(sf < 0, -1, 1).to(torch.int8)
+    return sf.to(device).contiguous()
+
+
 def head_seeds(user_id: int, n_heads: int) -> tuple:
     """(user_id % 1024) ^ h for each kv head (quantize.py:293-295, :583)."""
     return tuple((user_id % 1024) ^ h for h in range(n_heads))

@@ -111,9 +111,7 @@ def _attn(q, k_nibbles, k_qjl, k_norms, v_nibbles, codebooks, user_id, scale, wi
     gb = _lib.g_bits(_lib.head_seeds(user_id, Hkv), D, dev) if with_qjl else None
     sf = None
     if rotate_q and sign_flip is not None:
-        if sign_flip.numel() != D:
-            raise ValueError(f"sign_flip must have {D} entries, got {sign_flip.numel()}")
-        sf = torch.where(sign_flip.reshape(-1) < 0, -1, 1).to(torch.int8).to(dev).contiguous()
+        sf = _lib.sign_flip_i8(sign_flip, D, dev)
     out = torch.empty(B, Hq, T, D, dtype=torch.float32, device=dev)
     L = _lib.lib()
     ws_bytes = L.omni_attn_workspace_size(B, Hq, Hkv, T, S, D)
@@ -210,9 +208,7 @@ class PackedKVAttention:
         self.gb = _lib.g_bits(_lib.head_seeds(user_id, Hkv), D, dev) if with_qjl else None
         self.sf = None
         if rotate_q and sign_flip is not None:
-            if sign_flip.numel() != D:
-                raise ValueError(f"sign_flip must have {D} entries, got {sign_flip.numel()}")
-            self.sf = torch.where(sign_flip.reshape(-1) < 0, -1, 1).to(torch.int8).to(dev).contiguous()
+            self.sf = _lib.sign_flip_i8(sign_flip, D, dev)
         self.shape = (B, n_heads, q_tokens, D)
         self.q_dtype = q_dtype
         self.device = dev

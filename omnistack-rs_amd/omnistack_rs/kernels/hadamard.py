@@ -43,9 +43,7 @@ def rotate(x: torch.Tensor, sign_flip: Optional[torch.Tensor] = None) -> torch.T
     out = torch.empty_like(xc)
     sf = None
     if sign_flip is not None:
-        if sign_flip.numel() != D:
-            raise ValueError(f"sign_flip must have {D} entries, got {sign_flip.numel()}")
-        sf = torch.where(sign_flip.reshape(-1) < 0, -1, 1).to(torch.int8).contiguous()
+        sf = _lib.sign_flip_i8(sign_flip, D, dev)
     rows = xc.numel() // D
     _lib.check(_lib.lib().omni_wht_rotate(
         _lib.ptr(xc), _lib.dtype_code(xc.dtype), rows, D, _lib.ptr(sf), _lib.ptr(out),

@@ -102,9 +102,7 @@ def _encode(x: torch.Tensor, codebooks: torch.Tensor, user_id: int, rotate: bool
     nrm = torch.empty(B, H, T, dtype=torch.float32, device=dev)
     sf = None
     if sign_flip is not None:
-        if sign_flip.numel() != D:
-            raise ValueError(f"sign_flip must have {D} entries, got {sign_flip.numel()}")
-        sf = torch.where(sign_flip.reshape(-1) < 0, -1, 1).to(torch.int8).to(dev).contiguous()
+        sf = _lib.sign_flip_i8(sign_flip, D, dev)
     L = _lib.lib()
     code = _lib.dtype_code(xc.dtype)
     ws_n = L.omni_encode_workspace_size(B, H, T, D, code, per_head)

@@ -52,4 +52,9 @@ PINS = {
                               "1e-5; V=const -> const; single unmasked key -> v0",
     "restate.apply_lora_to_q": "merged-weight closed form q + x (B A)^T alpha "
                                "in fp64; sentinel -1 exactly unchanged",
+    "exact.projection_signs_exact": "tests/test_oracle_pins.py::"
+                                    "test_exact_projection_signs_survive_cancellation: "
+                                    "rows whose fp64 sum loses the small terms after "
+                                    "+-1e30 cancellation keep the sign of the exact "
+                                    "rational sum (and it equals fp64 where that is exact)",
 }
