@@ -51,6 +51,7 @@ struct AttnArgs {
     int64_t causal_offset;     // < 0: no mask
     int q_dtype, per_head, Hq, Hkv, G, n_rchunks, splits, ncopy;
     int with_qjl, rotate_q;
+    uint64_t g_magic, rch_magic;   // floor(2^32 / d) + 1 for d = G, n_rchunks
     int rows;                  // query rows per block (16: generic kernel, 8: D=128 decode kernel)
     float qscale;              // scale * log2(e)
     float alpha_c;             // fp32 sqrt(2/pi)/D (the row scale multiplies the whole score)
@@ -58,6 +59,14 @@ struct AttnArgs {
 };
 
 __device__ __forceinline__ int64_t imin64(int64_t x, int64_t y) { return x < y ? x : y; }
+
+// floor(x / d) for 0 <= x, d < 2^16 as (x * (floor(2^32 / d) + 1)) >> 32:
+// the excess x * e / 2^32 (0 < e <= 1) stays below 1/d, so the floor is
+// exact.  Branch- and division-free, so the kernel-argument loads are not
+// split around a division sequence.
+__device__ __forceinline__ int div_small(int x, uint64_t magic) {
+    return (int)(((uint64_t)(uint32_t)x * magic) >> 32);
+}
 __device__ __forceinline__ int imin(int x, int y) { return x < y ? x : y; }
 __device__ __forceinline__ int imax(int x, int y) { return x > y ? x : y; }
 
@@ -665,9 +674,11 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int split = blockIdx.x, hk = blockIdx.y;
-    const int64_t bz = blockIdx.z;
-    const int64_t b = bz / a.n_rchunks;
-    const int rc = (int)(bz % a.n_rchunks);
+    // (batch, row chunk) from blockIdx.z (< 2^16)
+    const int bz = blockIdx.z;
+    const int b32 = div_small(bz, a.rch_magic);
+    const int rc = bz - b32 * a.n_rchunks;
+    const int64_t b = b32;
     const int nrows_total = (int)(a.T * a.G);
     const int n = lane & 15, g = lane >> 4;
 
@@ -695,7 +706,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     const int rho = rc * kDecRows + wave;
     const bool row_ok = rho < nrows_total;
     const int rho_c = row_ok ? rho : nrows_total - 1;
-    const int t_q = rho_c / a.G;
+    const int t_q = div_small(rho_c, a.g_magic);
     const int hq_q = hk * a.G + (rho_c - t_q * a.G);
     const bool q32 = a.q_dtype == OMNI_F32;
     const int esz = q32 ? 4 : 2;
@@ -889,13 +900,13 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
         bgq[s] = as_half8(w[0], w[1], w[2], w[3]);
     }
     const int rho_n = rc * kDecRows + rn;
-    const int64_t key_limit64 = (a.causal_offset >= 0 && rho_n < nrows_total) ? a.causal_offset + rho_n / a.G
+    const int64_t key_limit64 = (a.causal_offset >= 0 && rho_n < nrows_total) ? a.causal_offset + div_small(rho_n, a.g_magic)
                                                                              : INT64_MAX;
 
     // ── main loop ─────────────────────────────────────────────────────
     const int key_limit = (int)imin64(key_limit64, (int64_t)0x7fffffff);
     // tiles ending at or below min(s_end, first masked key of any row) need no masks
-    const int64_t min_limit64 = (a.causal_offset >= 0) ? a.causal_offset + (rc * kDecRows) / a.G : INT64_MAX;
+    const int64_t min_limit64 = (a.causal_offset >= 0) ? a.causal_offset + div_small(rc * kDecRows, a.g_magic) : INT64_MAX;
     const int full_end = (int)imin64((int64_t)s_end, min_limit64 + 1);
     const uint32_t laneoff = (uint32_t)(lane & 31) * 8u;
     // ones on the hi slots of each (hi, lo) pair: sums every token's P once
@@ -1060,7 +1071,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
             osum = __builtin_fmaf(f, ob[(w * kDecRows + rr) * kObStride + d], osum);
         }
         if (a.splits == 1) {
-            const int t = rr_rho / a.G;
+            const int t = div_small(rr_rho, a.g_magic);
             const int hq = hk * a.G + (rr_rho - t * a.G);
             a.out[((b * a.Hq + hq) * a.T + t) * D + d] = osum / lsum;
         } else {
@@ -1567,8 +1578,8 @@ extern "C" int omni_attn(const void *q, int q_dtype, const uint8_t *k_nib, const
     OMNI_CHECK_ARG(S < (int64_t(1) << 25), "omni_attn: S must be < 2^25 tokens per sequence");
     OMNI_CHECK_ARG(T * (Hq / Hkv) < (int64_t(1) << 31), "omni_attn: T * (n_heads / n_kv_heads) must be < 2^31");
     Plan p = make_plan(B, Hq, Hkv, T, S, head_dim, q_dtype == OMNI_F32);
-    OMNI_CHECK_ARG(Hkv <= 65535 && B * p.n_rchunks <= 2147483647LL && p.splits <= 2147483647,
-                   "omni_attn: grid too large");
+    OMNI_CHECK_ARG(Hkv <= 65535 && B * p.n_rchunks <= 65535 && p.splits <= 2147483647,
+                   "omni_attn: grid too large (batch x row chunks must be <= 65535)");
     if (p.ws_bytes > 0 && (workspace == nullptr || workspace_bytes < p.ws_bytes)) {
         set_error("omni_attn: workspace of %zu bytes required, %zu given", p.ws_bytes, workspace_bytes);
         return OMNI_EWORKSPACE;
@@ -1581,6 +1592,8 @@ extern "C" int omni_attn(const void *q, int q_dtype, const uint8_t *k_nib, const
     a.q_dtype = q_dtype; a.per_head = per_head_codebook; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv;
     a.n_rchunks = p.n_rchunks; a.splits = p.splits; a.ncopy = p.ncopy; a.rows = p.rows;
     a.with_qjl = with_qjl; a.rotate_q = rotate_q;
+    a.g_magic = ((uint64_t)1 << 32) / (uint64_t)a.G + 1;
+    a.rch_magic = ((uint64_t)1 << 32) / (uint64_t)p.n_rchunks + 1;
     const double log2e = 1.4426950408889634;
     a.qscale = (float)((double)scale * log2e);
     a.alpha_c = (float)(sqrt(2.0 / M_PI) / (double)head_dim);
