@@ -493,7 +493,7 @@ constexpr int kDecPrefetch = 2;      // tiles in flight per wave (ring depth)
 constexpr int kLutOff = 0;
 constexpr int kLutBytes = 256 * 256;
 constexpr int kSlutOff = kLutBytes;
-constexpr int kSlutBytes = 256 * 16;
+constexpr int kSlutBytes = 16 * 256;
 static_assert((kSlutOff & (kSlutOff - 1)) == 0 && kSlutOff >= kSlutBytes, "sign LUT address is formed with an OR");
 constexpr int kDecQsOff = kSlutOff + kSlutBytes;
 constexpr int kDecBkOff = kDecQsOff + kDecRows * (128 + 64) * 4;   // [row][quad][hi, lo] 16 B
@@ -538,6 +538,28 @@ __device__ __forceinline__ float dpp_row_shl8(float v) {
 // LDS byte offset of the LUT entry for byte k of w: (byte << 8) | copy offset.
 __device__ __forceinline__ uint32_t lut_addr(uint32_t w, uint32_t laneoff, int k) {
     return __builtin_amdgcn_perm(w, laneoff, 0x0C0C0000u | ((uint32_t)(4 + k) << 8));
+}
+
+// Sign table: nibble v -> four fp16 halves (+1.0 where bit i of v is set,
+// -1.0 elsewhere), 32 bank-private copies at a 256-byte stride like the byte
+// LUT, so random nibbles read without bank conflicts.  `slane` is
+// kSlutOff | (lane % 32) * 8.
+__device__ __forceinline__ void sign_table_store(unsigned char *smem, int t) {
+    // thread t < 512 writes copy t % 32 of nibble t / 32
+    const uint32_t v = (uint32_t)t >> 5;
+    uint32_t w[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+        w[k] = (((v >> (2 * k)) & 1) ? 0x3C00u : 0xBC00u) | ((((v >> (2 * k + 1)) & 1) ? 0x3C00u : 0xBC00u) << 16);
+    *reinterpret_cast<uint2 *>(smem + kSlutOff + v * 256u + ((uint32_t)t & 31u) * 8u) = make_uint2(w[0], w[1]);
+}
+
+// Eight +-1.0 halves for bits pos .. pos + 7 of w (bit pos first).
+__device__ __forceinline__ half8_t sign_halves(const unsigned char *smem, uint32_t w, uint32_t pos, uint32_t slane) {
+    const uint32_t n0 = __builtin_amdgcn_ubfe(w, pos, 4u), n1 = __builtin_amdgcn_ubfe(w, pos + 4u, 4u);
+    const uint2 e0 = *reinterpret_cast<const uint2 *>(smem + ((n0 << 8) | slane));
+    const uint2 e1 = *reinterpret_cast<const uint2 *>(smem + ((n1 << 8) | slane));
+    return as_half8(e0.x, e0.y, e1.x, e1.y);
 }
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
@@ -743,15 +765,8 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     const uint32_t cb_pair = (uint32_t)cb_h16 | ((uint32_t)f32_to_f16_rne(cb_mine - f16_to_f32(cb_h16)) << 16);
     // tiles 0 .. nw - 1 are taken statically (one per wave, already in flight)
     if (tid == 0) *reinterpret_cast<int *>(smem + kDecCntOff) = nw;
-    // ── sign byte -> eight +-1.0 halves (threads 0..255) ──────────────
-    if (tid < 256) {
-        const int e = tid;
-        uint32_t w[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-            w[k] = (((e >> (2 * k)) & 1) ? 0x3C00u : 0xBC00u) | ((((e >> (2 * k + 1)) & 1) ? 0x3C00u : 0xBC00u) << 16);
-        *reinterpret_cast<uint4 *>(smem + kSlutOff + e * 16) = make_uint4(w[0], w[1], w[2], w[3]);
-    }
+    // ── sign table (threads 0..511) ───────────────────────────────────
+    if (tid < 512) sign_table_store(smem, tid);
     if (wave >= kDecRows) {
         // ── byte LUT, built by the waves without a query row while the
         //    others rotate theirs: entry e at e * 256, 32 copies of (hi
@@ -855,11 +870,10 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
         float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
         const int o = 16 * cb + n;
         const uint32_t gws[4] = {gw.x, gw.y, gw.z, gw.w};
+        const uint32_t slane = (uint32_t)kSlutOff | ((uint32_t)(lane & 31) * 8u);
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            const uint32_t byte = (gws[s] >> (8 * g)) & 0xffu;
-            const uint4 gv = *reinterpret_cast<const uint4 *>(smem + kSlutOff + byte * 16u);
-            const half8_t bg = as_half8(gv.x, gv.y, gv.z, gv.w);
+            const half8_t bg = sign_halves(smem, gws[s], 8u * g, slane);
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[s], bg, acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[s], bg, acc, 0, 0, 0);
         }
@@ -909,6 +923,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     const int64_t min_limit64 = (a.causal_offset >= 0) ? a.causal_offset + div_small(rc * kDecRows, a.g_magic) : INT64_MAX;
     const int full_end = (int)imin64((int64_t)s_end, min_limit64 + 1);
     const uint32_t laneoff = (uint32_t)(lane & 31) * 8u;
+    const uint32_t slane = (uint32_t)kSlutOff | laneoff;
     // ones on the hi slots of each (hi, lo) pair: sums every token's P once
     const half8_t ones = as_half8(0x3C003C00u, 0u, 0x3C003C00u, 0u);
     const unsigned char *lut = smem + kLutOff;
@@ -937,12 +952,9 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
             }
             if (QJL) {
 #pragma unroll
-                for (int s = 0; s < 2; ++s) {
-                    // LDS address kSlutOff | byte << 4 (kSlutOff is a power of two above 4K)
-                    const uint32_t byte = __builtin_amdgcn_ubfe(s ? R.sg[u].y : R.sg[u].x, 8u * g, 8u);
-                    const uint4 sv = *reinterpret_cast<const uint4 *>(smem + ((byte << 4) | (uint32_t)kSlutOff));
-                    qacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(sv.x, sv.y, sv.z, sv.w), bgq[s], qacc, 0, 0, 0);
-                }
+                for (int s = 0; s < 2; ++s)
+                    qacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(sign_halves(smem, s ? R.sg[u].y : R.sg[u].x, 8u * g, slane),
+                                                                  bgq[s], qacc, 0, 0, 0);
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -1129,14 +1141,7 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
         *reinterpret_cast<uint32_t *>(smem + kPreCbOff + 4 * (lane & 15)) =
             (uint32_t)h | ((uint32_t)f32_to_f16_rne(c - f16_to_f32(h)) << 16);
     }
-    if (tid < 256) {
-        const int e = tid;
-        uint32_t w[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-            w[k] = (((e >> (2 * k)) & 1) ? 0x3C00u : 0xBC00u) | ((((e >> (2 * k + 1)) & 1) ? 0x3C00u : 0xBC00u) << 16);
-        *reinterpret_cast<uint4 *>(smem + kSlutOff + e * 16) = make_uint4(w[0], w[1], w[2], w[3]);
-    }
+    sign_table_store(smem, tid);      // 512 threads
 
     // ── this wave's query rows: (sign flip,) WHT, round; per-row power-of-2
     //    scale into fp16 range; staged as fp16 ───────────────────────────
@@ -1231,9 +1236,7 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
             const uint32_t gws[4] = {gw.x, gw.y, gw.z, gw.w};
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                const uint32_t byte = (gws[s] >> (8 * g)) & 0xffu;
-                const uint4 gv = *reinterpret_cast<const uint4 *>(smem + kSlutOff + byte * 16u);
-                const half8_t bg = as_half8(gv.x, gv.y, gv.z, gv.w);
+                const half8_t bg = sign_halves(smem, gws[s], 8u * g, (uint32_t)kSlutOff | ((uint32_t)(lane & 31) * 8u));
 #pragma unroll
                 for (int c = 0; c < NCB; ++c) {
                     const uint4 qv = *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(stage) +
@@ -1315,6 +1318,7 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
     OFS.nr = 16u * g + 4u * (n & 3);      // norm of token 4g + n % 4 (of each 16-token half)
     OFS.v = 256u * g + 4u * n;
     const uint32_t laneoff = (uint32_t)(lane & 31) * 8u;
+    const uint32_t slane = (uint32_t)kSlutOff | laneoff;
     const half8_t ones = as_half8(0x3C003C00u, 0u, 0x3C003C00u, 0u);
     const unsigned char *lut = smem + kLutOff;
 
@@ -1357,9 +1361,7 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
                 // (norm of token 4g + i: a quad broadcast, fp32)
 #pragma unroll
                 for (int s = 0; s < 2; ++s) {
-                    const uint32_t byte = __builtin_amdgcn_ubfe(s ? R.sg[u].y : R.sg[u].x, 8u * g, 8u);
-                    const uint4 sv = *reinterpret_cast<const uint4 *>(smem + ((byte << 4) | (uint32_t)kSlutOff));
-                    const half8_t s8 = as_half8(sv.x, sv.y, sv.z, sv.w);
+                    const half8_t s8 = sign_halves(smem, s ? R.sg[u].y : R.sg[u].x, 8u * g, slane);
 #pragma unroll
                     for (int c = 0; c < NCB; ++c) {
                         qacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(s8, bgq[c][s], qacc[c], 0, 0, 0);
