@@ -167,8 +167,11 @@ def cpu_baseline_c3(kn, kq, kr, vn, cb, q, sign, uid, budget_s):
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=200)
+    # The GPU's clocks ramp up over the first tens of milliseconds of
+    # sustained work (C3 calls run ~80 us when cold, ~55-58 us once warm);
+    # 1000 warm-up calls (~60 ms) let them settle before the timed calls.
+    ap.add_argument("--warmup", type=int, default=1000)
     ap.add_argument("--cpu-budget-s", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="C3 (and the CPU baseline) only")
@@ -236,6 +239,7 @@ def main() -> int:
         log(f"[bench] C3: timing {args.steps} steps (warmup {args.warmup}); split-K workspace {att.ws_bytes} B")
         # One call is long enough that back-to-back eager launches keep the GPU
         # busy; `value` uses them (a graph of the same steps is reported too).
+        # The warm-up calls run back to back right before the timed ones.
         step = lambda: att.run(q)
         t_step = wall_eager(step, args.steps, args.warmup)
         t_graph = wall_graph(step, args.steps, args.warmup)
