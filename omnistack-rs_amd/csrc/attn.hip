@@ -52,6 +52,8 @@ struct AttnArgs {
     int q_dtype, per_head, Hq, Hkv, G, n_rchunks, splits, ncopy;
     int with_qjl, rotate_q;
     uint64_t g_magic, rch_magic;   // floor(2^32 / d) + 1 for d = G, n_rchunks
+    int64_t B;
+    int spb;                   // D=128 decode: sequences per block (1, or 2 when T * G <= 4)
     int rows;                  // query rows per block (16: generic kernel, 8: D=128 decode kernel)
     float qscale;              // scale * log2(e)
     float alpha_c;             // fp32 sqrt(2/pi)/D (the row scale multiplies the whole score)
@@ -685,8 +687,9 @@ __device__ __forceinline__ int claim_tile(int *cnt, int lane) {
     return __builtin_amdgcn_readfirstlane(v);
 }
 
-template <bool QJL, int PF>
+template <bool QJL, int PF, int SPB>
 __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs a) {
+    static_assert(SPB == 1 || SPB == 2, "one or two sequences per block");
     constexpr int D = 128, QD = 64;
     constexpr int nw = kDecWaves;
     __shared__ __attribute__((aligned(16))) unsigned char smem[kDecLdsBytes];
@@ -696,25 +699,42 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int split = blockIdx.x, hk = blockIdx.y;
-    // (batch, row chunk) from blockIdx.z (< 2^16)
+    // (batch, row chunk) from blockIdx.z (< 2^16); with two sequences per
+    // block (spb = 2, one row chunk), sequences 2 bz and 2 bz + 1
     const int bz = blockIdx.z;
-    const int b32 = div_small(bz, a.rch_magic);
-    const int rc = bz - b32 * a.n_rchunks;
+    const int bzq = div_small(bz, a.rch_magic);
+    const int rc = bz - bzq * a.n_rchunks;
+    const int b32 = bzq * SPB;
     const int64_t b = b32;
     const int nrows_total = (int)(a.T * a.G);
+    const int nseq = (SPB > 1 && b32 + 1 < a.B) ? 2 : 1;
     const int n = lane & 15, g = lane >> 4;
+    // row slot r -> (sequence index, flat (t, head) row of that sequence, valid)
+    auto row_seq = [&](int r) { return (SPB > 1 && r >= nrows_total) ? 1 : 0; };
+    auto row_rho = [&](int r) { return SPB > 1 ? r - row_seq(r) * nrows_total : rc * kDecRows + r; };
+    auto row_valid = [&](int r) {
+        return SPB > 1 ? (r < 2 * nrows_total && row_seq(r) < nseq) : (rc * kDecRows + r < nrows_total);
+    };
 
     // ── cache stream descriptors ──────────────────────────────────────
     const int s_begin = split * (int)a.split_len;
     const int s_end = (int)imin64(a.S, (int64_t)s_begin + a.split_len);
-    const int64_t kv_base = (b * a.Hkv + hk) * a.S;
-    DecBufs P;
-    P.kn = __builtin_amdgcn_make_buffer_rsrc((void *)(a.k_nib + kv_base * 64), (short)0, s_end * 64, kBufWord3);
-    P.vn = __builtin_amdgcn_make_buffer_rsrc((void *)(a.v_nib + kv_base * 64), (short)0, s_end * 64, kBufWord3);
-    P.kq = __builtin_amdgcn_make_buffer_rsrc((void *)(QJL ? a.k_qjl + kv_base * 8 : a.k_nib), (short)0,
-                                             QJL ? s_end * 8 : 0, kBufWord3);
-    P.kr = __builtin_amdgcn_make_buffer_rsrc((void *)(QJL ? a.k_norms + kv_base : (const float *)a.k_nib), (short)0,
-                                             QJL ? s_end * 4 : 0, kBufWord3);
+    auto stream_bufs = [&](int64_t bb) {
+        const int64_t kv_base = (bb * a.Hkv + hk) * a.S;
+        DecBufs Q;
+        Q.kn = __builtin_amdgcn_make_buffer_rsrc((void *)(a.k_nib + kv_base * 64), (short)0, s_end * 64, kBufWord3);
+        Q.vn = __builtin_amdgcn_make_buffer_rsrc((void *)(a.v_nib + kv_base * 64), (short)0, s_end * 64, kBufWord3);
+        Q.kq = __builtin_amdgcn_make_buffer_rsrc((void *)(QJL ? a.k_qjl + kv_base * 8 : a.k_nib), (short)0,
+                                                 QJL ? s_end * 8 : 0, kBufWord3);
+        Q.kr = __builtin_amdgcn_make_buffer_rsrc((void *)(QJL ? a.k_norms + kv_base : (const float *)a.k_nib),
+                                                 (short)0, QJL ? s_end * 4 : 0, kBufWord3);
+        return Q;
+    };
+    const DecBufs P = stream_bufs(b);
+    const DecBufs P1 = stream_bufs(nseq > 1 ? b + 1 : b);
+    // tiles of the split per sequence; claim index i -> sequence i / tps
+    const int tps = (s_end - s_begin + kDecTile - 1) / kDecTile;
+    const int ntiles = tps * nseq;
     DecOffsets OFS;
     OFS.k = (uint32_t)n * 64u + 16u * g;
     OFS.sg = (uint32_t)n * 8u;
@@ -724,16 +744,16 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     // ── prologue loads: branch-free buffer loads (an absent input gets a
     //    zero-size descriptor and reads 0), issued before the cache
     //    prefetch so that waiting for them does not wait for the cache ──
-    // this wave's query row: flat (t, g) = rc * 8 + wave
-    const int rho = rc * kDecRows + wave;
-    const bool row_ok = rho < nrows_total;
-    const int rho_c = row_ok ? rho : nrows_total - 1;
+    // this wave's query row
+    const bool row_ok = row_valid(wave);
+    const int rho_c = row_ok ? row_rho(wave) : 0;
+    const int64_t b_q = row_ok ? b + row_seq(wave) : b;
     const int t_q = div_small(rho_c, a.g_magic);
     const int hq_q = hk * a.G + (rho_c - t_q * a.G);
     const bool q32 = a.q_dtype == OMNI_F32;
     const int esz = q32 ? 4 : 2;
     const __amdgpu_buffer_rsrc_t QR = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(reinterpret_cast<const char *>(a.q) + ((b * a.Hq + hq_q) * a.T + t_q) * (int64_t)(D * esz)),
+        (void *)(reinterpret_cast<const char *>(a.q) + ((b_q * a.Hq + hq_q) * a.T + t_q) * (int64_t)(D * esz)),
         (short)0, D * esz, kBufWord3);
     const uint32_t q32_lo = __builtin_amdgcn_raw_buffer_load_b32(QR, 4u * lane, 0, 0);
     const uint32_t q32_hi = __builtin_amdgcn_raw_buffer_load_b32(QR, 4u * (64 + lane), 0, 0);
@@ -758,7 +778,10 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     //    counts outstanding loads exactly and waits only for the tile it
     //    consumes. ──────────────────────────────────────────────────────
     TileRaw ring[PF];
-    tile_load<QJL>(ring[0], P, OFS, s_begin + wave * kDecTile);
+    // claim index i -> (sequence, token offset); i >= ntiles is past the end
+    auto tile_seq = [&](int i) { return (nseq > 1 && i >= tps) ? 1 : 0; };
+    auto tile_tok = [&](int i) { return s_begin + (i - tile_seq(i) * tps) * kDecTile; };
+    tile_load<QJL>(ring[0], wave >= tps ? P1 : P, OFS, tile_tok(wave));
 
     // ── centroid lane % 16 as an (fp16 hi, fp16 remainder) pair ────────
     const uint16_t cb_h16 = f32_to_f16_rne(cb_mine);
@@ -913,15 +936,17 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
         }
         bgq[s] = as_half8(w[0], w[1], w[2], w[3]);
     }
-    const int rho_n = rc * kDecRows + rn;
-    const int64_t key_limit64 = (a.causal_offset >= 0 && rho_n < nrows_total) ? a.causal_offset + div_small(rho_n, a.g_magic)
-                                                                             : INT64_MAX;
+    const int rho_n = row_rho(rn);
+    const int seq_n = row_seq(rn);             // this column's sequence
+    const int64_t key_limit64 = (a.causal_offset >= 0 && row_valid(rn)) ? a.causal_offset + div_small(rho_n, a.g_magic)
+                                                                       : INT64_MAX;
 
     // ── main loop ─────────────────────────────────────────────────────
     const int key_limit = (int)imin64(key_limit64, (int64_t)0x7fffffff);
     // tiles ending at or below min(s_end, first masked key of any row) need no masks
     const int64_t min_limit64 = (a.causal_offset >= 0) ? a.causal_offset + div_small(rc * kDecRows, a.g_magic) : INT64_MAX;
-    const int full_end = (int)imin64((int64_t)s_end, min_limit64 + 1);
+    // two sequences per block: every tile masks the other sequence's columns
+    const int full_end = nseq > 1 ? s_begin : (int)imin64((int64_t)s_end, min_limit64 + 1);
     const uint32_t laneoff = (uint32_t)(lane & 31) * 8u;
     const uint32_t slane = (uint32_t)kSlutOff | laneoff;
     // ones on the hi slots of each (hi, lo) pair: sums every token's P once
@@ -935,7 +960,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     float m_run = -INFINITY;
 
     // One 32-token tile: scores, online softmax, PV.
-    auto tile_step = [&](TileRaw &R, const int tt) {
+    auto tile_step = [&](TileRaw &R, const int tt, const int tseq) {
         const bool full = tt + kDecTile <= full_end;
 
         // scores: lane (n, g) holds tokens tt + 16u + 4g + i
@@ -973,7 +998,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int tn = tt + 16 * u + 4 * g + i;
-                    if (tn >= s_end || tn > key_limit) sc[4 * u + i] = -INFINITY;
+                    if (tn >= s_end || tn > key_limit || seq_n != tseq) sc[4 * u + i] = -INFINITY;
                 }
         }
 
@@ -1032,23 +1057,23 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     // memory) and consumes the current one.
     static_assert(PF == 2, "the dynamic tile loop alternates two ring slots");
     int *tile_cnt = reinterpret_cast<int *>(smem + kDecCntOff);
-    int t_cur = s_begin + wave * kDecTile;
+    int i_cur = wave;
     int c_nxt = claim_tile(tile_cnt, lane);
     for (;;) {
-        if (t_cur >= s_end) break;
-        const int t_nxt = s_begin + c_nxt * kDecTile;
+        if (i_cur >= ntiles) break;
+        const int i_nxt = c_nxt;
         c_nxt = claim_tile(tile_cnt, lane);
         __builtin_amdgcn_sched_barrier(0);
-        tile_load<QJL>(ring[1], P, OFS, t_nxt);
+        tile_load<QJL>(ring[1], tile_seq(i_nxt) ? P1 : P, OFS, tile_tok(i_nxt));
         __builtin_amdgcn_sched_barrier(0);
-        tile_step(ring[0], t_cur);
-        if (t_nxt >= s_end) break;
-        t_cur = s_begin + c_nxt * kDecTile;
+        tile_step(ring[0], tile_tok(i_cur), tile_seq(i_cur));
+        if (i_nxt >= ntiles) break;
+        i_cur = c_nxt;
         c_nxt = claim_tile(tile_cnt, lane);
         __builtin_amdgcn_sched_barrier(0);
-        tile_load<QJL>(ring[0], P, OFS, t_cur);
+        tile_load<QJL>(ring[0], tile_seq(i_cur) ? P1 : P, OFS, tile_tok(i_cur));
         __builtin_amdgcn_sched_barrier(0);
-        tile_step(ring[1], t_nxt);
+        tile_step(ring[1], tile_tok(i_nxt), tile_seq(i_nxt));
     }
 
     // ── combine waves (in wave order) ───────────────────────────────
@@ -1071,8 +1096,9 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     const int64_t unit = (b * a.Hkv + hk) * a.n_rchunks + rc;
     for (int s = tid; s < kDecRows * D; s += blockDim.x) {
         const int rr = s / D, d = s % D;
-        const int rr_rho = rc * kDecRows + rr;
-        if (rr_rho >= nrows_total) continue;
+        if (!row_valid(rr)) continue;
+        const int rr_rho = row_rho(rr);
+        const int64_t rr_b = b + row_seq(rr);
         float rmx = -INFINITY;
         for (int w = 0; w < nw; ++w) rmx = fmaxf(rmx, wm[w * kDecRows + rr]);
         const float rmu = (rmx == -INFINITY) ? 0.0f : rmx;
@@ -1085,7 +1111,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
         if (a.splits == 1) {
             const int t = div_small(rr_rho, a.g_magic);
             const int hq = hk * a.G + (rr_rho - t * a.G);
-            a.out[((b * a.Hq + hq) * a.T + t) * D + d] = osum / lsum;
+            a.out[((rr_b * a.Hq + hq) * a.T + t) * D + d] = osum / lsum;
         } else {
             float *wp = a.ws + ((unit * a.splits + split) * kDecRows + rr) * (D + 2);
             wp[d] = osum;
@@ -1490,6 +1516,7 @@ struct Plan {
     bool dec128;       // D == 128: decode kernel with 8 query rows per block
     bool prefill;      // D == 128 with many rows per kv head: prefill kernel
     int rows, n_rchunks, splits, nw, ncopy;
+    int spb;           // decode kernel: sequences sharing a block's 8 row slots
     int64_t split_len;
     size_t lds, ws_bytes;
 };
@@ -1516,7 +1543,12 @@ static Plan make_plan(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int D, b
     p.dec128 = (D == 128) && !p.prefill;
     p.rows = p.prefill ? kPreWaves * 16 * (q32 ? 1 : kPreNcb) : (p.dec128 ? kDecRows : kRows);
     p.n_rchunks = (int)((T * G + p.rows - 1) / p.rows);
-    const int64_t units = B * (int64_t)Hkv * p.n_rchunks;
+    // Short decode steps of many sequences (more (sequence, kv head) pairs
+    // than CUs, at most 4 query rows each): two sequences share a block's 8
+    // row slots, halving the blocks (and the per-block prologues) without
+    // idling any slot.
+    p.spb = (p.dec128 && T * G <= kDecRows / 2 && B >= 2 && B * (int64_t)Hkv > cus) ? 2 : 1;
+    const int64_t units = ((B + p.spb - 1) / p.spb) * (int64_t)Hkv * p.n_rchunks;
     if (p.prefill) {
         const int64_t tiles = (S + kDecTile - 1) / kDecTile;
         int64_t splits = clamp64((cus + units - 1) / (units > 0 ? units : 1), 1, (tiles / 16) > 1 ? tiles / 16 : 1);
@@ -1529,6 +1561,7 @@ static Plan make_plan(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int D, b
     } else if (p.dec128) {
         const int64_t tiles = (S + kDecTile - 1) / kDecTile;
         int64_t splits = clamp64((cus + units - 1) / (units > 0 ? units : 1), 1, (tiles / 16) > 1 ? tiles / 16 : 1);
+        if (p.spb > 1) splits = 1;
         const int64_t tps = (tiles + splits - 1) / splits;
         p.splits = (int)splits;
         p.split_len = tps * kDecTile;
@@ -1580,7 +1613,7 @@ extern "C" int omni_attn(const void *q, int q_dtype, const uint8_t *k_nib, const
     OMNI_CHECK_ARG(S < (int64_t(1) << 25), "omni_attn: S must be < 2^25 tokens per sequence");
     OMNI_CHECK_ARG(T * (Hq / Hkv) < (int64_t(1) << 31), "omni_attn: T * (n_heads / n_kv_heads) must be < 2^31");
     Plan p = make_plan(B, Hq, Hkv, T, S, head_dim, q_dtype == OMNI_F32);
-    OMNI_CHECK_ARG(Hkv <= 65535 && B * p.n_rchunks <= 65535 && p.splits <= 2147483647,
+    OMNI_CHECK_ARG(Hkv <= 65535 && ((B + p.spb - 1) / p.spb) * p.n_rchunks <= 65535 && p.splits <= 2147483647,
                    "omni_attn: grid too large (batch x row chunks must be <= 65535)");
     if (p.ws_bytes > 0 && (workspace == nullptr || workspace_bytes < p.ws_bytes)) {
         set_error("omni_attn: workspace of %zu bytes required, %zu given", p.ws_bytes, workspace_bytes);
@@ -1600,7 +1633,9 @@ extern "C" int omni_attn(const void *q, int q_dtype, const uint8_t *k_nib, const
     a.qscale = (float)((double)scale * log2e);
     a.alpha_c = (float)(sqrt(2.0 / M_PI) / (double)head_dim);
     a.wht_scale = inv_sqrt_dim_f32(head_dim);
-    dim3 grid((unsigned)p.splits, (unsigned)Hkv, (unsigned)(B * p.n_rchunks));
+    a.B = B;
+    a.spb = p.spb;
+    dim3 grid((unsigned)p.splits, (unsigned)Hkv, (unsigned)(((B + p.spb - 1) / p.spb) * p.n_rchunks));
     dim3 block(64 * p.nw);
     if (p.prefill) {
         const bool qlo = q_dtype == OMNI_F32;
@@ -1612,10 +1647,14 @@ extern "C" int omni_attn(const void *q, int q_dtype, const uint8_t *k_nib, const
             else hipLaunchKernelGGL((attn_prefill128_kernel<false, kPreNcb, 2, false>), grid, block, 0, as_stream(stream), a);
         }
     } else if (p.dec128) {
-        if (with_qjl)
-            hipLaunchKernelGGL((attn_decode128_kernel<true, kDecPrefetch>), grid, block, 0, as_stream(stream), a);
+        if (with_qjl && p.spb > 1)
+            hipLaunchKernelGGL((attn_decode128_kernel<true, kDecPrefetch, 2>), grid, block, 0, as_stream(stream), a);
+        else if (with_qjl)
+            hipLaunchKernelGGL((attn_decode128_kernel<true, kDecPrefetch, 1>), grid, block, 0, as_stream(stream), a);
+        else if (p.spb > 1)
+            hipLaunchKernelGGL((attn_decode128_kernel<false, kDecPrefetch, 2>), grid, block, 0, as_stream(stream), a);
         else
-            hipLaunchKernelGGL((attn_decode128_kernel<false, kDecPrefetch>), grid, block, 0, as_stream(stream), a);
+            hipLaunchKernelGGL((attn_decode128_kernel<false, kDecPrefetch, 1>), grid, block, 0, as_stream(stream), a);
     } else {
         hipLaunchKernelGGL(attn_kernel<32>, grid, block, p.lds, as_stream(stream), a);
     }

@@ -305,6 +305,24 @@ def test_attn_large_and_tiny_query_rows(device, dtype):
         _assert_close(got, want, f"decode extreme rows {dtype} scale {scale:.3g}")
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,T,S,causal", [
+    (65, 32, 8, 1, 50, False),      # C2 shape with an odd batch: two sequences per block, last block one
+    (40, 16, 8, 2, 70, True),       # T * G = 4 rows per sequence, causal chunk at the end
+    (33, 8, 8, 4, 33, True),        # G = 1, four query tokens per sequence
+])
+def test_attn_two_sequences_per_block(device, B, Hq, Hkv, T, S, causal):
+    """More (sequence, kv head) pairs than CUs with <= 4 rows each: the decode
+    kernel packs two sequences into one block's row slots."""
+    uid = 3
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=29 + B, user_id=uid)
+    q = _data.query((B, Hq, T, 128), seed=30 + B)
+    off = S - T if causal else None
+    got = _run(device, q, kn, kq, kr, vn, cb, uid, causal_offset=off)
+    mask = _causal_mask(T, S, off) if causal else None
+    want = restate.fused_attn_python(q.float(), kn, kq, kr, vn, cb, uid, 1 / math.sqrt(128), True, mask=mask)
+    _assert_close(got, want, f"packed B{B} Hq{Hq} Hkv{Hkv} T{T} S{S}")
+
+
 @pytest.mark.parametrize("T", [1, 3, 40])          # decode kernel, D=128 decode with 12 rows, prefill tiles
 @pytest.mark.parametrize("scale", [-0.3, 0.0])
 def test_attn_negative_and_zero_scale(device, T, scale):
