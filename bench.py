@@ -287,7 +287,8 @@ def main() -> int:
         result["serving_c2"] = {"p50_us": round(p50 * 1e6, 2), "p99_us": round(p99 * 1e6, 2),
                                 "users_per_s": round(B2 / t2, 1),
                                 "us_per_step_graph": round(t2 * 1e6, 2),
-                                "note": "one step = LoRA gather-apply + rotate_q + decode attention for 64 users; "
+                                "note": "one step = per-user LoRA update of q, rotate_q and decode attention for 64 users "
+                                        "(one launch: the update runs in the decode kernel's prologue); "
                                         "p50/p99 from HIP events per eager call, users/s from a HIP graph of steps"}
         log(f"[bench] C2: p50 {p50 * 1e6:.1f} us p99 {p99 * 1e6:.1f} us (events), "
             f"{t2 * 1e6:.1f} us/step graph -> {B2 / t2:.0f} users/s")

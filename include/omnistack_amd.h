@@ -158,6 +158,35 @@ int omni_attn(const void *q, int q_dtype,
               int rotate_q, const int8_t *sign_flip,
               float *out, void *workspace, size_t workspace_bytes, void *stream);
 
+/*
+ * omni_attn with the per-user LoRA update of q applied first:
+ *   q_eff[b] = dtype(q[b] + ((x[b] A[idx[b]]^T) B[idx[b]]^T) * lora_alpha)
+ * (idx < 0: q unchanged; idx >= n_loras: NaN rows), then attention on q_eff
+ * exactly as omni_attn.  LoRA shapes and dtypes as omni_lora_apply.  At
+ * head_dim 128 with <= 32 query rows per kv head and a 16-bit adapter of
+ * rank <= 16 and hidden <= 256 the update runs inside the attention
+ * kernel's prologue (one launch); otherwise the gather-apply kernel writes
+ * q_eff into the workspace tail first.  q_eff is rounded
+ * exactly as omni_lora_apply rounds it.  `workspace` must hold
+ * omni_attn_lora_workspace_size(...) bytes.
+ * Replaces omni_attn(..., x, lora_a, lora_b, lora_indices, lora_alpha)
+ * (omnistack_rs/kernels/fused_attention.py:537-565) and the Triton kernel's
+ * LoRA block (:166-191).
+ */
+size_t omni_attn_lora_workspace_size(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int head_dim,
+                                     int q_dtype);
+
+int omni_attn_lora(const void *q, int q_dtype,
+                   const void *x, const void *lora_a, const void *lora_b, int w_dtype,
+                   const int32_t *lora_idx, int hidden, int rank, int n_loras, float lora_alpha,
+                   const uint8_t *k_nib, const uint8_t *k_qjl, const float *k_norms,
+                   const uint8_t *v_nib, const float *codebooks, int per_head_codebook,
+                   const uint32_t *g_bits,
+                   int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int head_dim,
+                   float scale, int with_qjl, int64_t causal_offset,
+                   int rotate_q, const int8_t *sign_flip,
+                   float *out, void *workspace, size_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -54,6 +54,11 @@ struct AttnArgs {
     uint64_t g_magic, rch_magic;   // floor(2^32 / d) + 1 for d = G, n_rchunks
     int64_t B;
     int spb;                   // D=128 decode: sequences per block (1, or 2 when T * G <= 4)
+    // per-user LoRA on q, fused into the D=128 decode prologue (lora_w_dtype < 0: none)
+    const void *lora_x, *lora_a, *lora_b;
+    const int32_t *lora_idx;
+    int lora_w_dtype, lora_hidden, lora_rank, lora_n;
+    float lora_alpha;
     int rows;                  // query rows per block (16: generic kernel, 8: D=128 decode kernel)
     float qscale;              // scale * log2(e)
     float alpha_c;             // fp32 sqrt(2/pi)/D (the row scale multiplies the whole score)
@@ -680,6 +685,96 @@ __device__ __forceinline__ void wht128_lanes(float &lo, float &hi, int lane) {
     hi = a - b;
 }
 
+// q_eff = round(q + ((x A_id^T) B_id^T) alpha) for one query row (b, t, hq)
+// held as (lo = dim lane, hi = dim 64 + lane), in exactly the operation order
+// of lora_kernel (per-lane fma over hidden = lane, lane + 64, ...; xor-tree
+// wave sum; sequential fma over the rank), so the fused and the separate
+// paths round q_eff identically.  id < 0: unchanged; id >= n: NaN.
+// The fused path takes 16-bit adapters with rank <= 16 and hidden <= 256
+// (the host sends others to the gather-apply kernel); every load is a
+// branch-free 16-bit buffer load whose range ends at the row it serves.
+__device__ __forceinline__ float lora_wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+    return v;
+}
+constexpr int kLoraFusedMaxRank = 16;
+constexpr int kLoraFusedMaxHidden = 256;
+
+__device__ __forceinline__ float lora_w16(uint32_t w, bool bf) {
+    return bf ? __uint_as_float(w << 16) : f16_to_f32((uint16_t)w);
+}
+
+// x row of (b, t) as raw 16-bit values: element 64 kh + lane in xw[kh]
+// (0 past `hidden`: the descriptor's range ends there).
+__device__ __forceinline__ void lora_x_load(uint32_t (&xw)[4], const AttnArgs &a, int64_t b, int64_t t, int lane) {
+    const __amdgpu_buffer_rsrc_t XR = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(reinterpret_cast<const uint16_t *>(a.lora_x) + (b * a.T + t) * a.lora_hidden), (short)0,
+        2 * a.lora_hidden, kBufWord3);
+#pragma unroll
+    for (int kh = 0; kh < 4; ++kh) xw[kh] = __builtin_amdgcn_raw_buffer_load_b16(XR, 2u * (64 * kh + lane), 0, 0);
+}
+
+__device__ __forceinline__ void lora_row(float &lo, float &hi, const AttnArgs &a, int32_t id_raw,
+                                         const uint32_t (&xw)[4], int hq, int lane) {
+    const int32_t id = __builtin_amdgcn_readfirstlane(id_raw);
+    const bool active = id >= 0 && id < a.lora_n, bad = id >= a.lora_n;
+    const int64_t sid = active ? id : 0;
+    const bool bf = a.lora_w_dtype == OMNI_BF16;
+    const int hidden = a.lora_hidden, rank = a.lora_rank;
+    // A[sid] (rank x hidden) and this head's 128 rows of B[sid] (128 x rank)
+    const __amdgpu_buffer_rsrc_t AR = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(reinterpret_cast<const uint16_t *>(a.lora_a) + sid * rank * (int64_t)hidden), (short)0,
+        2 * rank * hidden, kBufWord3);
+    const __amdgpu_buffer_rsrc_t BR = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(reinterpret_cast<const uint16_t *>(a.lora_b) + (sid * a.Hq + hq) * 128 * (int64_t)rank), (short)0,
+        2 * 128 * rank, kBufWord3);
+    float xv[4];
+#pragma unroll
+    for (int kh = 0; kh < 4; ++kh) xv[kh] = lora_w16(xw[kh], bf);
+    float acc_lo = 0.0f, acc_hi = 0.0f;
+    for (int j0 = 0; j0 < rank; j0 += 8) {
+        // all loads of eight rank components first (one latency); rows past
+        // the rank read 0 (A) or are not used (B)
+        uint32_t aw[8][4], bl[8], bh[8];
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+            const uint32_t j = j0 + jj;
+#pragma unroll
+            for (int kh = 0; kh < 4; ++kh)
+                aw[jj][kh] = __builtin_amdgcn_raw_buffer_load_b16(AR, 2u * (j * hidden + 64 * kh + lane), 0, 0);
+            bl[jj] = __builtin_amdgcn_raw_buffer_load_b16(BR, 2u * (lane * rank + j), 0, 0);
+            bh[jj] = __builtin_amdgcn_raw_buffer_load_b16(BR, 2u * ((64 + lane) * rank + j), 0, 0);
+        }
+        float dr[8];
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+            float part = 0.0f;
+#pragma unroll
+            for (int kh = 0; kh < 4; ++kh) {
+                // a select, not a branch: the load must not sink into one
+                const float f = __builtin_fmaf(xv[kh], lora_w16(aw[jj][kh], bf), part);
+                part = 64 * kh + lane < hidden ? f : part;
+            }
+            dr[jj] = lora_wave_sum(part);
+        }
+        // B values live in registers here: keeps the compiler from sinking
+        // their loads into the (uniform) rank test below
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) asm volatile("" : "+v"(bl[jj]), "+v"(bh[jj]));
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+            const bool jv = j0 + jj < rank;
+            acc_lo = jv ? __builtin_fmaf(dr[jj], lora_w16(bl[jj], bf), acc_lo) : acc_lo;
+            acc_hi = jv ? __builtin_fmaf(dr[jj], lora_w16(bh[jj], bf), acc_hi) : acc_hi;
+        }
+    }
+    const float ulo = round_to_dtype(__fadd_rn(lo, __fmul_rn(acc_lo, a.lora_alpha)), a.q_dtype);
+    const float uhi = round_to_dtype(__fadd_rn(hi, __fmul_rn(acc_hi, a.lora_alpha)), a.q_dtype);
+    lo = active ? ulo : (bad ? __builtin_nanf("") : lo);
+    hi = active ? uhi : (bad ? __builtin_nanf("") : hi);
+}
+
 // Next tile index of the block (wave-uniform): lane 0 bumps the LDS counter.
 __device__ __forceinline__ int claim_tile(int *cnt, int lane) {
     int v = 0;
@@ -687,7 +782,7 @@ __device__ __forceinline__ int claim_tile(int *cnt, int lane) {
     return __builtin_amdgcn_readfirstlane(v);
 }
 
-template <bool QJL, int PF, int SPB>
+template <bool QJL, int PF, int SPB, bool LORA>
 __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs a) {
     static_assert(SPB == 1 || SPB == 2, "one or two sequences per block");
     constexpr int D = 128, QD = 64;
@@ -759,6 +854,14 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     const uint32_t q32_hi = __builtin_amdgcn_raw_buffer_load_b32(QR, 4u * (64 + lane), 0, 0);
     const uint32_t q16_lo = __builtin_amdgcn_raw_buffer_load_b16(QR, 2u * lane, 0, 0);
     const uint32_t q16_hi = __builtin_amdgcn_raw_buffer_load_b16(QR, 2u * (64 + lane), 0, 0);
+    int32_t lora_id = -1;
+    uint32_t lora_xw[4] = {0u, 0u, 0u, 0u};
+    if constexpr (LORA) {
+        if (row_ok && wave < kDecRows) {
+            lora_id = a.lora_idx[b_q];
+            lora_x_load(lora_xw, a, b_q, t_q, lane);
+        }
+    }
     const bool use_flip = a.rotate_q && a.sign_flip;
     const __amdgpu_buffer_rsrc_t SF = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(use_flip ? (const void *)a.sign_flip : (const void *)a.codebooks), (short)0, use_flip ? D : 0, kBufWord3);
@@ -819,6 +922,9 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
             } else {
                 lo = f16_to_f32((uint16_t)q16_lo);
                 hi = f16_to_f32((uint16_t)q16_hi);
+            }
+            if constexpr (LORA) {
+                if (row_ok) lora_row(lo, hi, a, lora_id, lora_xw, hq_q, lane);
             }
             lo = (sf_lo & 0x80u) ? -lo : lo;
             hi = (sf_hi & 0x80u) ? -hi : hi;
@@ -1595,12 +1701,31 @@ extern "C" size_t omni_attn_workspace_size(int64_t B, int Hq, int Hkv, int64_t T
     return a > b ? a : b;
 }
 
-extern "C" int omni_attn(const void *q, int q_dtype, const uint8_t *k_nib, const uint8_t *k_qjl,
-                         const float *k_norms, const uint8_t *v_nib, const float *codebooks,
-                         int per_head_codebook, const uint32_t *g_bits, int64_t B, int Hq, int Hkv,
-                         int64_t T, int64_t S, int head_dim, float scale, int with_qjl,
-                         int64_t causal_offset, int rotate_q, const int8_t *sign_flip, float *out,
-                         void *workspace, size_t workspace_bytes, void *stream) {
+// Per-user LoRA on q (omni_attn_lora).
+struct LoraSpec {
+    const void *x, *A, *Bw;
+    int w_dtype;
+    const int32_t *idx;
+    int hidden, rank, n_loras;
+    float alpha;
+};
+
+static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+template <bool QJL, int SPB>
+static void launch_decode128(bool lora, dim3 grid, dim3 block, hipStream_t s, const AttnArgs &a) {
+    if (lora)
+        hipLaunchKernelGGL((attn_decode128_kernel<QJL, kDecPrefetch, SPB, true>), grid, block, 0, s, a);
+    else
+        hipLaunchKernelGGL((attn_decode128_kernel<QJL, kDecPrefetch, SPB, false>), grid, block, 0, s, a);
+}
+
+static int attn_run(const void *q, int q_dtype, const uint8_t *k_nib, const uint8_t *k_qjl,
+                    const float *k_norms, const uint8_t *v_nib, const float *codebooks,
+                    int per_head_codebook, const uint32_t *g_bits, int64_t B, int Hq, int Hkv,
+                    int64_t T, int64_t S, int head_dim, float scale, int with_qjl,
+                    int64_t causal_offset, int rotate_q, const int8_t *sign_flip, float *out,
+                    void *workspace, size_t workspace_bytes, void *stream, const LoraSpec *lora) {
     OMNI_CHECK_ARG(dtype_ok(q_dtype), "omni_attn: bad q dtype %d", q_dtype);
     OMNI_CHECK_ARG(head_dim_ok(head_dim), "omni_attn: head_dim must be 128 or 32, got %d", head_dim);
     OMNI_CHECK_ARG(B >= 0 && Hq > 0 && Hkv > 0 && T >= 0 && S >= 0, "omni_attn: bad shape");
@@ -1615,11 +1740,32 @@ extern "C" int omni_attn(const void *q, int q_dtype, const uint8_t *k_nib, const
     Plan p = make_plan(B, Hq, Hkv, T, S, head_dim, q_dtype == OMNI_F32);
     OMNI_CHECK_ARG(Hkv <= 65535 && ((B + p.spb - 1) / p.spb) * p.n_rchunks <= 65535 && p.splits <= 2147483647,
                    "omni_attn: grid too large (batch x row chunks must be <= 65535)");
-    if (p.ws_bytes > 0 && (workspace == nullptr || workspace_bytes < p.ws_bytes)) {
-        set_error("omni_attn: workspace of %zu bytes required, %zu given", p.ws_bytes, workspace_bytes);
+    // LoRA: fused into the D=128 decode prologue; other kernels read q_eff
+    // written by the gather-apply kernel into the workspace tail
+    const bool lora_fused = lora != nullptr && p.dec128 && lora->w_dtype != OMNI_F32 &&
+                            lora->rank <= kLoraFusedMaxRank && lora->hidden <= kLoraFusedMaxHidden;
+    const size_t q_bytes = (size_t)B * Hq * T * head_dim * (q_dtype == OMNI_F32 ? 4 : 2);
+    const size_t ws_need = (lora != nullptr && !lora_fused) ? align256(p.ws_bytes) + q_bytes : p.ws_bytes;
+    if (ws_need > 0 && (workspace == nullptr || workspace_bytes < ws_need)) {
+        set_error("omni_attn: workspace of %zu bytes required, %zu given", ws_need, workspace_bytes);
         return OMNI_EWORKSPACE;
     }
+    if (lora != nullptr && !lora_fused) {
+        void *q_eff = reinterpret_cast<char *>(workspace) + align256(p.ws_bytes);
+        const int rc = omni_lora_apply(q, q_dtype, lora->x, lora->A, lora->Bw, lora->w_dtype, lora->idx, B, Hq, T,
+                                       head_dim, lora->hidden, lora->rank, lora->n_loras, lora->alpha, q_eff, stream);
+        if (rc != OMNI_OK) return rc;
+        q = q_eff;
+    }
     AttnArgs a;
+    a.lora_x = a.lora_a = a.lora_b = nullptr;
+    a.lora_idx = nullptr;
+    a.lora_w_dtype = -1; a.lora_hidden = a.lora_rank = a.lora_n = 0; a.lora_alpha = 0.0f;
+    if (lora_fused) {
+        a.lora_x = lora->x; a.lora_a = lora->A; a.lora_b = lora->Bw; a.lora_idx = lora->idx;
+        a.lora_w_dtype = lora->w_dtype; a.lora_hidden = lora->hidden; a.lora_rank = lora->rank;
+        a.lora_n = lora->n_loras; a.lora_alpha = lora->alpha;
+    }
     a.q = q; a.k_nib = k_nib; a.k_qjl = k_qjl; a.k_norms = k_norms; a.v_nib = v_nib;
     a.codebooks = codebooks; a.g_bits = g_bits; a.sign_flip = sign_flip; a.out = out;
     a.ws = reinterpret_cast<float *>(workspace);
@@ -1647,14 +1793,11 @@ extern "C" int omni_attn(const void *q, int q_dtype, const uint8_t *k_nib, const
             else hipLaunchKernelGGL((attn_prefill128_kernel<false, kPreNcb, 2, false>), grid, block, 0, as_stream(stream), a);
         }
     } else if (p.dec128) {
-        if (with_qjl && p.spb > 1)
-            hipLaunchKernelGGL((attn_decode128_kernel<true, kDecPrefetch, 2>), grid, block, 0, as_stream(stream), a);
-        else if (with_qjl)
-            hipLaunchKernelGGL((attn_decode128_kernel<true, kDecPrefetch, 1>), grid, block, 0, as_stream(stream), a);
-        else if (p.spb > 1)
-            hipLaunchKernelGGL((attn_decode128_kernel<false, kDecPrefetch, 2>), grid, block, 0, as_stream(stream), a);
-        else
-            hipLaunchKernelGGL((attn_decode128_kernel<false, kDecPrefetch, 1>), grid, block, 0, as_stream(stream), a);
+        hipStream_t st = as_stream(stream);
+        if (with_qjl && p.spb > 1) launch_decode128<true, 2>(lora_fused, grid, block, st, a);
+        else if (with_qjl) launch_decode128<true, 1>(lora_fused, grid, block, st, a);
+        else if (p.spb > 1) launch_decode128<false, 2>(lora_fused, grid, block, st, a);
+        else launch_decode128<false, 1>(lora_fused, grid, block, st, a);
     } else {
         hipLaunchKernelGGL(attn_kernel<32>, grid, block, p.lds, as_stream(stream), a);
     }
@@ -1668,4 +1811,45 @@ extern "C" int omni_attn(const void *q, int q_dtype, const uint8_t *k_nib, const
         OMNI_CHECK_LAUNCH("omni_attn combine");
     }
     return OMNI_OK;
+}
+
+extern "C" int omni_attn(const void *q, int q_dtype, const uint8_t *k_nib, const uint8_t *k_qjl,
+                         const float *k_norms, const uint8_t *v_nib, const float *codebooks,
+                         int per_head_codebook, const uint32_t *g_bits, int64_t B, int Hq, int Hkv,
+                         int64_t T, int64_t S, int head_dim, float scale, int with_qjl,
+                         int64_t causal_offset, int rotate_q, const int8_t *sign_flip, float *out,
+                         void *workspace, size_t workspace_bytes, void *stream) {
+    return attn_run(q, q_dtype, k_nib, k_qjl, k_norms, v_nib, codebooks, per_head_codebook, g_bits, B, Hq, Hkv, T,
+                    S, head_dim, scale, with_qjl, causal_offset, rotate_q, sign_flip, out, workspace,
+                    workspace_bytes, stream, nullptr);
+}
+
+extern "C" size_t omni_attn_lora_workspace_size(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int head_dim,
+                                                int q_dtype) {
+    if (B <= 0 || Hq <= 0 || Hkv <= 0 || T <= 0 || S <= 0 || Hq % Hkv || !head_dim_ok(head_dim) || !dtype_ok(q_dtype))
+        return 0;
+    const Plan p = make_plan(B, Hq, Hkv, T, S, head_dim, q_dtype == OMNI_F32);
+    // room for the gather-apply fallback's q_eff: the adapter's rank and
+    // hidden size, which decide between it and the fused path, are not
+    // arguments here
+    return align256(p.ws_bytes) + (size_t)B * Hq * T * head_dim * (q_dtype == OMNI_F32 ? 4 : 2);
+}
+
+extern "C" int omni_attn_lora(const void *q, int q_dtype, const void *x, const void *lora_a, const void *lora_b,
+                              int w_dtype, const int32_t *lora_idx, int hidden, int rank, int n_loras,
+                              float lora_alpha, const uint8_t *k_nib, const uint8_t *k_qjl, const float *k_norms,
+                              const uint8_t *v_nib, const float *codebooks, int per_head_codebook,
+                              const uint32_t *g_bits, int64_t B, int Hq, int Hkv, int64_t T, int64_t S,
+                              int head_dim, float scale, int with_qjl, int64_t causal_offset, int rotate_q,
+                              const int8_t *sign_flip, float *out, void *workspace, size_t workspace_bytes,
+                              void *stream) {
+    OMNI_CHECK_ARG(dtype_ok(w_dtype), "omni_attn_lora: bad LoRA dtype %d", w_dtype);
+    OMNI_CHECK_ARG(hidden > 0 && rank >= 1 && rank <= 64 && n_loras >= 1,
+                   "omni_attn_lora: need hidden > 0, 1 <= rank <= 64, n_loras >= 1");
+    if (B > 0 && T > 0) OMNI_CHECK_ARG(x && lora_a && lora_b && lora_idx, "omni_attn_lora: NULL LoRA pointer");
+    OMNI_CHECK_ARG((int64_t)Hq * head_dim <= (int64_t)1 << 30, "omni_attn_lora: n_heads * head_dim too large");
+    const LoraSpec spec{x, lora_a, lora_b, w_dtype, lora_idx, hidden, rank, n_loras, lora_alpha};
+    return attn_run(q, q_dtype, k_nib, k_qjl, k_norms, v_nib, codebooks, per_head_codebook, g_bits, B, Hq, Hkv, T,
+                    S, head_dim, scale, with_qjl, causal_offset, rotate_q, sign_flip, out, workspace,
+                    workspace_bytes, stream, &spec);
 }

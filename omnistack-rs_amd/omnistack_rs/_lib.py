@@ -39,6 +39,11 @@ SIGNATURES = {
     "omni_attn": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _vp, _vp, _c_int, _vp,
                            _c_i64, _c_int, _c_int, _c_i64, _c_i64, _c_int,
                            _c_f32, _c_int, _c_i64, _c_int, _vp, _vp, _vp, _c_sz, _vp]),
+    "omni_attn_lora_workspace_size": (_c_sz, [_c_i64, _c_int, _c_int, _c_i64, _c_i64, _c_int, _c_int]),
+    "omni_attn_lora": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_f32,
+                                _vp, _vp, _vp, _vp, _vp, _c_int, _vp,
+                                _c_i64, _c_int, _c_int, _c_i64, _c_i64, _c_int,
+                                _c_f32, _c_int, _c_i64, _c_int, _vp, _vp, _vp, _c_sz, _vp]),
 }
 
 

@@ -53,10 +53,9 @@ def make_g_matrix(n_kv_heads: int, seed: int, device="cpu") -> tuple[torch.Tenso
     return g_lo.to(device), g_hi.to(device)
 
 
-def _apply_lora_to_q(q: torch.Tensor, x: torch.Tensor, lora_a: torch.Tensor, lora_b: torch.Tensor,
-                     lora_indices: torch.Tensor, lora_alpha: float, *, validate: bool = True) -> torch.Tensor:
-    """q_eff[b] = q[b] + ((x[b] A[id]^T) B[id]^T) * alpha for id >= 0, else q[b];
-    returned in q's dtype (fused_attention.py:401-430)."""
+def _prep_lora(q: torch.Tensor, x, lora_a, lora_b, lora_indices, lora_alpha, validate: bool):
+    """Validated, contiguous LoRA operands for the C ABI:
+    (x, A, B, weight dtype code, int32 ids, hidden, rank, n_loras, alpha)."""
     if q.dim() != 4:
         raise ValueError(f"q must be (B, n_heads, T, head_dim), got {tuple(q.shape)}")
     B, Hq, T, D = q.shape
@@ -75,18 +74,30 @@ def _apply_lora_to_q(q: torch.Tensor, x: torch.Tensor, lora_a: torch.Tensor, lor
     if wdt not in _lib.DTYPE_CODE:
         wdt = torch.float32
     xc, ac, bc = (t.to(wdt).contiguous() for t in (x, lora_a, lora_b))
+    return xc, ac, bc, _lib.dtype_code(wdt), idx, hidden, rank, n_loras, float(lora_alpha)
+
+
+def _apply_lora_to_q(q: torch.Tensor, x: torch.Tensor, lora_a: torch.Tensor, lora_b: torch.Tensor,
+                     lora_indices: torch.Tensor, lora_alpha: float, *, validate: bool = True) -> torch.Tensor:
+    """q_eff[b] = q[b] + ((x[b] A[id]^T) B[id]^T) * alpha for id >= 0, else q[b];
+    returned in q's dtype (fused_attention.py:401-430)."""
+    xc, ac, bc, wcode, idx, hidden, rank, n_loras, alpha = _prep_lora(q, x, lora_a, lora_b, lora_indices,
+                                                                      lora_alpha, validate)
+    B, Hq, T, D = q.shape
     qc = q if q.dtype in _lib.DTYPE_CODE else q.float()
     qc = qc.contiguous()
     out = torch.empty_like(qc)
     _lib.check(_lib.lib().omni_lora_apply(
         _lib.ptr(qc), _lib.dtype_code(qc.dtype), _lib.ptr(xc), _lib.ptr(ac), _lib.ptr(bc),
-        _lib.dtype_code(wdt), _lib.ptr(idx), B, Hq, T, D, hidden, rank, n_loras, float(lora_alpha),
-        _lib.ptr(out), _lib.stream_of(dev)))
+        wcode, _lib.ptr(idx), B, Hq, T, D, hidden, rank, n_loras, alpha,
+        _lib.ptr(out), _lib.stream_of(qc.device)))
     return out if out.dtype == q.dtype else out.to(q.dtype)
 
 
 def _attn(q, k_nibbles, k_qjl, k_norms, v_nibbles, codebooks, user_id, scale, with_qjl,
-          causal_offset=None, rotate_q=False, sign_flip=None) -> torch.Tensor:
+          causal_offset=None, rotate_q=False, sign_flip=None, lora=None) -> torch.Tensor:
+    """`lora`: _prep_lora's tuple; the update of q then runs inside the
+    attention call (omni_attn_lora)."""
     if q.dim() != 4 or k_nibbles.dim() != 4:
         raise ValueError("q must be (B, n_heads, T, D) and k_nibbles (B, n_kv_heads, S, D/2)")
     B, Hq, T, D = q.shape
@@ -114,13 +125,20 @@ def _attn(q, k_nibbles, k_qjl, k_norms, v_nibbles, codebooks, user_id, scale, wi
         sf = _lib.sign_flip_i8(sign_flip, D, dev)
     out = torch.empty(B, Hq, T, D, dtype=torch.float32, device=dev)
     L = _lib.lib()
-    ws_bytes = L.omni_attn_workspace_size(B, Hq, Hkv, T, S, D)
+    qcode = _lib.dtype_code(qc.dtype)
+    tail = (_lib.ptr(kn), _lib.ptr(kq), _lib.ptr(kr), _lib.ptr(vn), _lib.ptr(cb), per_head, _lib.ptr(gb),
+            B, Hq, Hkv, T, S, D, float(scale), int(with_qjl), -1 if causal_offset is None else int(causal_offset),
+            int(rotate_q), _lib.ptr(sf), _lib.ptr(out))
+    if lora is None:
+        ws_bytes = L.omni_attn_workspace_size(B, Hq, Hkv, T, S, D)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if ws_bytes else None
+        _lib.check(L.omni_attn(_lib.ptr(qc), qcode, *tail, _lib.ptr(ws), ws_bytes, _lib.stream_of(dev)))
+        return out
+    xc, ac, bc, wcode, idx, hidden, rank, n_loras, alpha = lora
+    ws_bytes = L.omni_attn_lora_workspace_size(B, Hq, Hkv, T, S, D, qcode)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if ws_bytes else None
-    _lib.check(L.omni_attn(
-        _lib.ptr(qc), _lib.dtype_code(qc.dtype), _lib.ptr(kn), _lib.ptr(kq), _lib.ptr(kr),
-        _lib.ptr(vn), _lib.ptr(cb), per_head, _lib.ptr(gb), B, Hq, Hkv, T, S, D, float(scale),
-        int(with_qjl), -1 if causal_offset is None else int(causal_offset), int(rotate_q),
-        _lib.ptr(sf), _lib.ptr(out), _lib.ptr(ws), ws_bytes, _lib.stream_of(dev)))
+    _lib.check(L.omni_attn_lora(_lib.ptr(qc), qcode, _lib.ptr(xc), _lib.ptr(ac), _lib.ptr(bc), wcode, _lib.ptr(idx),
+                                hidden, rank, n_loras, alpha, *tail, _lib.ptr(ws), ws_bytes, _lib.stream_of(dev)))
     return out
 
 
@@ -141,10 +159,8 @@ class OmniAttention(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k_nibbles, k_qjl, k_norms, v_nibbles, codebooks, user_id, scale, with_qjl,
                 g_matrix=None, x=None, lora_a=None, lora_b=None, lora_indices=None, lora_alpha=1.0):
-        q_eff = q
-        if x is not None:
-            q_eff = _apply_lora_to_q(q, x, lora_a, lora_b, lora_indices, lora_alpha)
-        out = _attn(q_eff, k_nibbles, k_qjl, k_norms, v_nibbles, codebooks, user_id, scale, with_qjl)
+        lora = _prep_lora(q, x, lora_a, lora_b, lora_indices, lora_alpha, True) if x is not None else None
+        out = _attn(q, k_nibbles, k_qjl, k_norms, v_nibbles, codebooks, user_id, scale, with_qjl, lora=lora)
         ctx.save_for_backward(q, out)
         return out
 
@@ -166,11 +182,9 @@ def omni_attn(q: torch.Tensor, k_nibbles: torch.Tensor, k_qjl: torch.Tensor, k_n
     if causal_offset is None and not rotate_q and validate:
         return OmniAttention.apply(q, k_nibbles, k_qjl, k_norms, v_nibbles, codebooks, user_id, scale,
                                    with_qjl, g_matrix, x, lora_a, lora_b, lora_indices, lora_alpha)
-    q_eff = q
-    if x is not None:
-        q_eff = _apply_lora_to_q(q, x, lora_a, lora_b, lora_indices, lora_alpha, validate=validate)
-    return _attn(q_eff, k_nibbles, k_qjl, k_norms, v_nibbles, codebooks, user_id, scale, with_qjl,
-                 causal_offset=causal_offset, rotate_q=rotate_q, sign_flip=sign_flip)
+    lora = _prep_lora(q, x, lora_a, lora_b, lora_indices, lora_alpha, validate) if x is not None else None
+    return _attn(q, k_nibbles, k_qjl, k_norms, v_nibbles, codebooks, user_id, scale, with_qjl,
+                 causal_offset=causal_offset, rotate_q=rotate_q, sign_flip=sign_flip, lora=lora)
 
 
 class PackedKVAttention:
@@ -235,12 +249,15 @@ class PackedKVAttention:
                 wdt = torch.float32
             self._la = lora_a.to(device=dev, dtype=wdt).contiguous()
             self._lb = lora_b.to(device=dev, dtype=wdt).contiguous()
-            self.q_eff = torch.empty(self.shape, dtype=q_dtype, device=dev)
             self.lora = (n_loras, rank, hidden, wdt)
-            self._lora_fn = L.omni_lora_apply
-            self._lora_tail = (_lib.ptr(self._la), _lib.ptr(self._lb), _lib.dtype_code(wdt))
-            self._lora_shape = (B, n_heads, q_tokens, D, hidden, rank, n_loras, float(lora_alpha),
-                                _lib.ptr(self.q_eff))
+            # one launch per step: the q update runs inside the attention
+            # call (in the decode kernel's prologue when it serves the shape)
+            self.lora_ws_bytes = L.omni_attn_lora_workspace_size(B, n_heads, Hkv, q_tokens, S, D, self._qcode)
+            self.lora_ws = torch.empty(max(self.lora_ws_bytes, 1), dtype=torch.uint8, device=dev)
+            self._lora_fn = L.omni_attn_lora
+            self._lora_head = (_lib.ptr(self._la), _lib.ptr(self._lb), _lib.dtype_code(wdt))
+            self._lora_mid = (hidden, rank, n_loras, float(lora_alpha))
+            self._lora_args = self._args[:-2] + (_lib.ptr(self.lora_ws), self.lora_ws_bytes)
 
     def run(self, q: torch.Tensor, x: Optional[torch.Tensor] = None,
             lora_indices: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -258,12 +275,12 @@ class PackedKVAttention:
             if (lora_indices is None or lora_indices.dtype != torch.int32 or lora_indices.numel() != B
                     or not lora_indices.is_contiguous()):
                 raise ValueError(f"lora_indices must be a contiguous int32 tensor of {B} entries")
-            la, lb, wcode = self._lora_tail
+            la, lb, wcode = self._lora_head
             rc = self._lora_fn(qp, self._qcode, x.data_ptr(), la, lb, wcode, lora_indices.data_ptr(),
-                               *self._lora_shape, stream)
+                               *self._lora_mid, *self._lora_args, stream)
             if rc:
                 _lib.check(rc)
-            qp = self.q_eff.data_ptr()
+            return self.out
         rc = self._fn(qp, self._qcode, *self._args, stream)
         if rc:
             _lib.check(rc)

@@ -219,6 +219,35 @@ def test_prepared_lora_matches_omni_attn(device):
     _assert_close(got, ref, "prepared lora")
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,T,qdt,wdt,rank,hidden", [
+    (4, 32, 8, 1, torch.bfloat16, torch.bfloat16, 8, 96),    # decode kernel, update fused into its prologue
+    (70, 32, 8, 1, torch.bfloat16, torch.bfloat16, 8, 96),   # two sequences per block
+    (3, 8, 2, 2, torch.float32, torch.float32, 8, 96),
+    (2, 8, 2, 3, torch.float16, torch.bfloat16, 8, 96),
+    (4, 32, 8, 1, torch.bfloat16, torch.bfloat16, 13, 200),  # rank not a multiple of 4, ragged hidden
+    (4, 32, 8, 1, torch.float16, torch.float16, 16, 256),    # largest fused adapter
+    (4, 32, 8, 1, torch.bfloat16, torch.bfloat16, 17, 64),   # rank above the fused bound: gather-apply
+    (4, 32, 8, 1, torch.bfloat16, torch.bfloat16, 4, 300),   # hidden above the fused bound: gather-apply
+    (2, 16, 4, 40, torch.bfloat16, torch.bfloat16, 8, 96),   # prefill kernel: gather-apply into the workspace first
+])
+def test_fused_lora_equals_separate_gather_apply(device, B, Hq, Hkv, T, qdt, wdt, rank, hidden):
+    """omni_attn with adapters (one call) equals the gather-apply kernel
+    followed by attention on its q_eff, bit for bit."""
+    from omnistack_rs.kernels.fused_attention import _apply_lora_to_q, omni_attn
+    S, uid, L = 120, 5, 12
+    kn, kq, kr, vn, cb = (t.to(device) for t in _cache(B, Hkv, S, seed=44 + B, user_id=uid))
+    a, bw = _data.lora_bank(L, rank, hidden, Hq * 128, seed=45)
+    a, bw = a.to(wdt).to(device), bw.to(wdt).to(device)
+    q = _data.query((B, Hq, T, 128), seed=46, dtype=qdt).to(device)
+    x = torch.randn(B, T, hidden, generator=_data.gen(47)).to(wdt).to(device)
+    ids = _data.lora_ids(B, L).to(device)
+    ids[0] = -1
+    got = omni_attn(q, kn, kq, kr, vn, cb, user_id=uid, x=x, lora_a=a, lora_b=bw, lora_indices=ids, lora_alpha=0.5)
+    q_eff = _apply_lora_to_q(q, x, a, bw, ids, 0.5)
+    want = omni_attn(q_eff, kn, kq, kr, vn, cb, user_id=uid)
+    assert torch.equal(got, want)
+
+
 def test_prepared_run_replays_in_hip_graph(device):
     """One LoRA + attention step captured in a HIP graph: every replay, with
     eager work and host syncs between replays, equals the eager result."""

@@ -95,6 +95,24 @@ def test_encode_missing_workspace_is_an_error(L):
     assert rc == _lib.OMNI_EWORKSPACE and "workspace" in _lib.last_error()
 
 
+def test_attn_lora_host_checks(L):
+    from omnistack_rs import _lib
+    tail = (None, None, None, None, None, 0, None, 1, 4, 2, 1, 10, 128, 1.0, 1, -1, 0, None, None, None, 0, None)
+    rc = L.omni_attn_lora(None, 2, None, None, None, 2, None, 128, 65, 4, 1.0, *tail)
+    assert rc == _lib.OMNI_EINVAL and "rank" in _lib.last_error()
+    rc = L.omni_attn_lora(None, 2, None, None, None, 2, None, 128, 8, 4, 1.0, *tail)
+    assert rc == _lib.OMNI_EINVAL and "NULL" in _lib.last_error()
+    empty = (None, None, None, None, None, 0, None, 0, 4, 2, 1, 10, 128, 1.0, 1, -1, 0, None, None, None, 0, None)
+    assert L.omni_attn_lora(None, 2, None, None, None, 2, None, 128, 8, 4, 1.0, *empty) == 0
+    # room for the gather-apply fallback's q_eff after the attention workspace
+    # (whether the update fuses depends on rank and hidden, not arguments here)
+    base = L.omni_attn_workspace_size(4, 32, 8, 1, 300, 128)
+    assert L.omni_attn_lora_workspace_size(4, 32, 8, 1, 300, 128, 0) == ((base + 255) // 256) * 256 + 4 * 32 * 128 * 4
+    base = L.omni_attn_workspace_size(2, 32, 8, 64, 1000, 128)
+    n = L.omni_attn_lora_workspace_size(2, 32, 8, 64, 1000, 128, 2)
+    assert n == ((base + 255) // 256) * 256 + 2 * 32 * 64 * 128 * 2
+
+
 def test_workspace_size_host_only(L):
     # planning is host arithmetic; C3 shape needs split partials
     n = L.omni_attn_workspace_size(32, 32, 8, 1, 8192, 128)
