@@ -176,11 +176,11 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="C3 (and the CPU baseline) only")
     ap.add_argument("--only", default="",
-                    help="comma-separated sections to run (c3, c2, c4, c5, c5d32), for profiling one "
+                    help="comma-separated sections to run (c3, c2, c2pool, c4, c5, c5d32), for profiling one "
                          "configuration; the JSON line then carries only those sections")
     args = ap.parse_args()
     sections = set(args.only.split(",")) if args.only else (
-        {"c3"} if args.no_extras else {"c3", "c2", "c4", "c5", "c5d32"})
+        {"c3"} if args.no_extras else {"c3", "c2", "c2pool", "c4", "c5", "c5d32"})
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -291,6 +291,34 @@ def main() -> int:
                                         "(one launch: the update runs in the decode kernel's prologue); "
                                         "p50/p99 from HIP events per eager call, users/s from a HIP graph of steps"}
         log(f"[bench] C2: p50 {p50 * 1e6:.1f} us p99 {p99 * 1e6:.1f} us (events), "
+            f"{t2 * 1e6:.1f} us/step graph -> {B2 / t2:.0f} users/s")
+
+    if "c2pool" in sections:
+        # the reference serving loop's shape: 64 users drawn with replacement
+        # from a pool of 256 baked users per step; the kernels follow the
+        # index instead of gathering the batch's caches
+        NP, B2, S2, L2, R2, HID = 256, 64, 50, 256, 8, 128
+        log("[bench] C2 pool: 64 of 256 cached users per step, 256 x rank-8 LoRA")
+        knp, kqp, krp, vnp = make_cache(NP, Hkv, S2, D, dev, 53, uid, cb, sign)
+        g2 = torch.Generator(device=dev).manual_seed(44)
+        la = (torch.randn(L2, R2, HID, generator=g2, device=dev) * 0.02).to(torch.bfloat16)
+        lb = (torch.randn(L2, Hq * D, R2, generator=g2, device=dev) * 0.02).to(torch.bfloat16)
+        ids = torch.randint(-1, L2, (B2,), generator=torch.Generator().manual_seed(45), dtype=torch.int32).to(dev)
+        users = torch.randint(0, NP, (B2,), generator=torch.Generator().manual_seed(46)).to(dev)
+        xh = torch.randn(B2, 1, HID, generator=g2, device=dev).to(torch.bfloat16)
+        q2 = torch.randn(B2, Hq, 1, D, generator=g2, device=dev).to(torch.bfloat16)
+        attp = PackedKVAttention(knp, kqp, krp, vnp, cb, n_heads=Hq, user_id=uid, rotate_q=True, sign_flip=sign,
+                                 lora_a=la, lora_b=lb, lora_alpha=1.0, batch=B2)
+        serve = lambda: attp.run(q2, xh, ids, cache_index=users)
+        steps2 = max(args.steps, 100)
+        per2 = sorted(per_call_events(serve, steps2, args.warmup, stream))
+        t2 = wall_graph(serve, steps2, args.warmup)
+        p50, p99 = per2[len(per2) // 2], per2[min(len(per2) - 1, int(0.99 * len(per2)))]
+        result["serving_c2_pool"] = {"p50_us": round(p50 * 1e6, 2), "p99_us": round(p99 * 1e6, 2),
+                                     "users_per_s": round(B2 / t2, 1), "us_per_step_graph": round(t2 * 1e6, 2),
+                                     "note": "C2 with the batch drawn from a pool of 256 cached users (75 % with "
+                                             "an adapter): cache index + LoRA + rotate_q + decode in one launch"}
+        log(f"[bench] C2 pool: p50 {p50 * 1e6:.1f} us p99 {p99 * 1e6:.1f} us (events), "
             f"{t2 * 1e6:.1f} us/step graph -> {B2 / t2:.0f} users/s")
 
     if "c4" in sections:

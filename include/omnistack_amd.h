@@ -187,6 +187,31 @@ int omni_attn_lora(const void *q, int q_dtype,
                    int rotate_q, const int8_t *sign_flip,
                    float *out, void *workspace, size_t workspace_bytes, void *stream);
 
+/*
+ * One serving step over a pool of cached sequences: query b attends cache
+ * sequence cache_index[b] of a pool of n_cache_seqs (k_nib, k_qjl, k_norms,
+ * v_nib are (n_cache_seqs, Hkv, S, ...)); q, x, lora_idx and out have B
+ * entries.  Negative indices count from the end of the pool (tensor
+ * indexing); an index outside [-n_cache_seqs, n_cache_seqs) gives NaN rows
+ * and reads nothing out of bounds.  LoRA as omni_attn_lora when lora_a is
+ * not NULL (x, lora_b, lora_idx then required), none when it is NULL.
+ * workspace: omni_attn_lora_workspace_size(B, ...) bytes with adapters,
+ * omni_attn_workspace_size(B, ...) without.
+ * Replaces the serving loop's gather of the batch's caches followed by
+ * omni_attn (scripts/run_criteo_benchmark.py:554-557, :593-597): the
+ * gather is an index the kernels follow, no copy.
+ */
+int omni_attn_serve(const void *q, int q_dtype, const int64_t *cache_index, int64_t n_cache_seqs,
+                    const void *x, const void *lora_a, const void *lora_b, int w_dtype,
+                    const int32_t *lora_idx, int hidden, int rank, int n_loras, float lora_alpha,
+                    const uint8_t *k_nib, const uint8_t *k_qjl, const float *k_norms,
+                    const uint8_t *v_nib, const float *codebooks, int per_head_codebook,
+                    const uint32_t *g_bits,
+                    int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int head_dim,
+                    float scale, int with_qjl, int64_t causal_offset,
+                    int rotate_q, const int8_t *sign_flip,
+                    float *out, void *workspace, size_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

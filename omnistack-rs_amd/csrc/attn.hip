@@ -53,6 +53,10 @@ struct AttnArgs {
     int with_qjl, rotate_q;
     uint64_t g_magic, rch_magic;   // floor(2^32 / d) + 1 for d = G, n_rchunks
     int64_t B;
+    // cache sequence of batch entry b: seq_index[b] into a pool of n_seqs
+    // sequences (NULL: b itself)
+    const int64_t *seq_index;
+    int64_t n_seqs;
     int spb;                   // D=128 decode: sequences per block (1, or 2 when T * G <= 4)
     // per-user LoRA on q, fused into the D=128 decode prologue (lora_w_dtype < 0: none)
     const void *lora_x, *lora_a, *lora_b;
@@ -66,6 +70,20 @@ struct AttnArgs {
 };
 
 __device__ __forceinline__ int64_t imin64(int64_t x, int64_t y) { return x < y ? x : y; }
+
+// Cache sequence read for batch entry b (wave-uniform).  Negative indices
+// count from the end of the pool, as tensor indexing does; an index outside
+// [-n_seqs, n_seqs) reads sequence 0 and sets `bad` (its rows come out NaN).
+__device__ __forceinline__ int64_t cache_seq(const AttnArgs &a, int64_t b, bool &bad) {
+    if (a.seq_index == nullptr) {
+        bad = false;
+        return b;
+    }
+    int64_t v = a.seq_index[b];
+    v = v < 0 ? v + a.n_seqs : v;
+    bad = v < 0 || v >= a.n_seqs;
+    return bad ? 0 : v;
+}
 
 // floor(x / d) for 0 <= x, d < 2^16 as (x * (floor(2^32 / d) + 1)) >> 32:
 // the excess x * e / 2^32 (0 < e <= 1) stays below 1/d, so the floor is
@@ -265,7 +283,8 @@ __global__ __launch_bounds__(64 * kMaxWaves) void attn_kernel(AttnArgs a) {
     // ── main loop ─────────────────────────────────────────────────────
     const int64_t s_begin = (int64_t)split * a.split_len;
     const int64_t s_end = imin64(a.S, s_begin + a.split_len);
-    const int64_t kv_base = (b * a.Hkv + hk) * a.S;   // token row base of this (b, hk)
+    bool seq_bad;
+    const int64_t kv_base = (cache_seq(a, b, seq_bad) * a.Hkv + hk) * a.S;   // token row base of this (b, hk)
     const int cmask = ncopy - 1;
     const int cl = lane & cmask;
 
@@ -420,6 +439,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void attn_kernel(AttnArgs a) {
         const float rmu = (rmx == -INFINITY) ? 0.0f : rmx;
         float lsum = 0.0f;
         for (int w = 0; w < nw; ++w) lsum = __builtin_fmaf(exp2f(wm[w * kRows + rr] - rmu), wl[w * kRows + rr], lsum);
+        if (seq_bad) lsum = __builtin_nanf("");
         const float osum = ob[rr * D + d];
         if (a.splits == 1) {
             const int64_t t = rr_rho / a.G;
@@ -815,7 +835,8 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     const int s_begin = split * (int)a.split_len;
     const int s_end = (int)imin64(a.S, (int64_t)s_begin + a.split_len);
     auto stream_bufs = [&](int64_t bb) {
-        const int64_t kv_base = (bb * a.Hkv + hk) * a.S;
+        bool bad_unused;
+        const int64_t kv_base = (cache_seq(a, bb, bad_unused) * a.Hkv + hk) * a.S;
         DecBufs Q;
         Q.kn = __builtin_amdgcn_make_buffer_rsrc((void *)(a.k_nib + kv_base * 64), (short)0, s_end * 64, kBufWord3);
         Q.vn = __builtin_amdgcn_make_buffer_rsrc((void *)(a.v_nib + kv_base * 64), (short)0, s_end * 64, kBufWord3);
@@ -1214,6 +1235,11 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
             lsum = __builtin_fmaf(f, wl[w * kDecRows + rr], lsum);
             osum = __builtin_fmaf(f, ob[(w * kDecRows + rr) * kObStride + d], osum);
         }
+        if (a.seq_index != nullptr) {
+            bool bad;
+            (void)cache_seq(a, rr_b, bad);
+            if (bad) lsum = __builtin_nanf("");
+        }
         if (a.splits == 1) {
             const int t = div_small(rr_rho, a.g_magic);
             const int hq = hk * a.G + (rr_rho - t * a.G);
@@ -1436,7 +1462,8 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
         full_end = (int)imin64((int64_t)s_end, lo_lim + 1);
         s_end = (int)imin64((int64_t)s_end, hi_lim + 1);
     }
-    const int64_t kv_base = (b * a.Hkv + hk) * a.S;
+    bool seq_bad;
+    const int64_t kv_base = (cache_seq(a, b, seq_bad) * a.Hkv + hk) * a.S;
     DecBufs P;
     P.kn = __builtin_amdgcn_make_buffer_rsrc((void *)(a.k_nib + kv_base * 64), (short)0, s_end * 64, kBufWord3);
     P.vn = __builtin_amdgcn_make_buffer_rsrc((void *)(a.v_nib + kv_base * 64), (short)0, s_end * 64, kBufWord3);
@@ -1596,7 +1623,7 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
     for (int c = 0; c < NCB; ++c) {
         const int rho = row0 + 16 * c + n;
         if (!rowok[c]) continue;
-        const float l = lacc[c][0];
+        const float l = seq_bad ? __builtin_nanf("") : lacc[c][0];
         if (a.splits == 1) {
             const int t = rho / a.G, hq = hk * a.G + (rho - t * a.G);
             float *o = a.out + ((b * a.Hq + hq) * a.T + t) * D;
@@ -1725,7 +1752,8 @@ static int attn_run(const void *q, int q_dtype, const uint8_t *k_nib, const uint
                     int per_head_codebook, const uint32_t *g_bits, int64_t B, int Hq, int Hkv,
                     int64_t T, int64_t S, int head_dim, float scale, int with_qjl,
                     int64_t causal_offset, int rotate_q, const int8_t *sign_flip, float *out,
-                    void *workspace, size_t workspace_bytes, void *stream, const LoraSpec *lora) {
+                    void *workspace, size_t workspace_bytes, void *stream, const LoraSpec *lora,
+                    const int64_t *seq_index, int64_t n_seqs) {
     OMNI_CHECK_ARG(dtype_ok(q_dtype), "omni_attn: bad q dtype %d", q_dtype);
     OMNI_CHECK_ARG(head_dim_ok(head_dim), "omni_attn: head_dim must be 128 or 32, got %d", head_dim);
     OMNI_CHECK_ARG(B >= 0 && Hq > 0 && Hkv > 0 && T >= 0 && S >= 0, "omni_attn: bad shape");
@@ -1737,6 +1765,7 @@ static int attn_run(const void *q, int q_dtype, const uint8_t *k_nib, const uint
     OMNI_CHECK_ARG(isfinite(scale), "omni_attn: scale must be finite");
     OMNI_CHECK_ARG(S < (int64_t(1) << 25), "omni_attn: S must be < 2^25 tokens per sequence");
     OMNI_CHECK_ARG(T * (Hq / Hkv) < (int64_t(1) << 31), "omni_attn: T * (n_heads / n_kv_heads) must be < 2^31");
+    OMNI_CHECK_ARG(seq_index == nullptr || n_seqs >= 1, "omni_attn: a cache index needs a pool of >= 1 sequences");
     Plan p = make_plan(B, Hq, Hkv, T, S, head_dim, q_dtype == OMNI_F32);
     OMNI_CHECK_ARG(Hkv <= 65535 && ((B + p.spb - 1) / p.spb) * p.n_rchunks <= 65535 && p.splits <= 2147483647,
                    "omni_attn: grid too large (batch x row chunks must be <= 65535)");
@@ -1780,6 +1809,8 @@ static int attn_run(const void *q, int q_dtype, const uint8_t *k_nib, const uint
     a.alpha_c = (float)(sqrt(2.0 / M_PI) / (double)head_dim);
     a.wht_scale = inv_sqrt_dim_f32(head_dim);
     a.B = B;
+    a.seq_index = seq_index;
+    a.n_seqs = seq_index ? n_seqs : B;
     a.spb = p.spb;
     dim3 grid((unsigned)p.splits, (unsigned)Hkv, (unsigned)(((B + p.spb - 1) / p.spb) * p.n_rchunks));
     dim3 block(64 * p.nw);
@@ -1821,7 +1852,7 @@ extern "C" int omni_attn(const void *q, int q_dtype, const uint8_t *k_nib, const
                          void *workspace, size_t workspace_bytes, void *stream) {
     return attn_run(q, q_dtype, k_nib, k_qjl, k_norms, v_nib, codebooks, per_head_codebook, g_bits, B, Hq, Hkv, T,
                     S, head_dim, scale, with_qjl, causal_offset, rotate_q, sign_flip, out, workspace,
-                    workspace_bytes, stream, nullptr);
+                    workspace_bytes, stream, nullptr, nullptr, 0);
 }
 
 extern "C" size_t omni_attn_lora_workspace_size(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int head_dim,
@@ -1851,5 +1882,31 @@ extern "C" int omni_attn_lora(const void *q, int q_dtype, const void *x, const v
     const LoraSpec spec{x, lora_a, lora_b, w_dtype, lora_idx, hidden, rank, n_loras, lora_alpha};
     return attn_run(q, q_dtype, k_nib, k_qjl, k_norms, v_nib, codebooks, per_head_codebook, g_bits, B, Hq, Hkv, T,
                     S, head_dim, scale, with_qjl, causal_offset, rotate_q, sign_flip, out, workspace,
-                    workspace_bytes, stream, &spec);
+                    workspace_bytes, stream, &spec, nullptr, 0);
+}
+
+extern "C" int omni_attn_serve(const void *q, int q_dtype, const int64_t *cache_index, int64_t n_cache_seqs,
+                               const void *x, const void *lora_a, const void *lora_b, int w_dtype,
+                               const int32_t *lora_idx, int hidden, int rank, int n_loras, float lora_alpha,
+                               const uint8_t *k_nib, const uint8_t *k_qjl, const float *k_norms,
+                               const uint8_t *v_nib, const float *codebooks, int per_head_codebook,
+                               const uint32_t *g_bits, int64_t B, int Hq, int Hkv, int64_t T, int64_t S,
+                               int head_dim, float scale, int with_qjl, int64_t causal_offset, int rotate_q,
+                               const int8_t *sign_flip, float *out, void *workspace, size_t workspace_bytes,
+                               void *stream) {
+    if (B > 0 && T > 0) OMNI_CHECK_ARG(cache_index != nullptr, "omni_attn_serve: NULL cache index");
+    OMNI_CHECK_ARG(n_cache_seqs >= 1, "omni_attn_serve: n_cache_seqs must be >= 1");
+    if (lora_a == nullptr)
+        return attn_run(q, q_dtype, k_nib, k_qjl, k_norms, v_nib, codebooks, per_head_codebook, g_bits, B, Hq, Hkv,
+                        T, S, head_dim, scale, with_qjl, causal_offset, rotate_q, sign_flip, out, workspace,
+                        workspace_bytes, stream, nullptr, cache_index, n_cache_seqs);
+    OMNI_CHECK_ARG(dtype_ok(w_dtype), "omni_attn_serve: bad LoRA dtype %d", w_dtype);
+    OMNI_CHECK_ARG(hidden > 0 && rank >= 1 && rank <= 64 && n_loras >= 1,
+                   "omni_attn_serve: need hidden > 0, 1 <= rank <= 64, n_loras >= 1");
+    if (B > 0 && T > 0) OMNI_CHECK_ARG(x && lora_b && lora_idx, "omni_attn_serve: NULL LoRA pointer");
+    OMNI_CHECK_ARG((int64_t)Hq * head_dim <= (int64_t)1 << 30, "omni_attn_serve: n_heads * head_dim too large");
+    const LoraSpec spec{x, lora_a, lora_b, w_dtype, lora_idx, hidden, rank, n_loras, lora_alpha};
+    return attn_run(q, q_dtype, k_nib, k_qjl, k_norms, v_nib, codebooks, per_head_codebook, g_bits, B, Hq, Hkv, T,
+                    S, head_dim, scale, with_qjl, causal_offset, rotate_q, sign_flip, out, workspace,
+                    workspace_bytes, stream, &spec, cache_index, n_cache_seqs);
 }

@@ -5,9 +5,10 @@ API of the reference module omnistack_rs/kernels/fused_attention.py:
 ``_apply_lora_to_q`` (:401-430), ``_fused_attn_python`` (:435-466),
 ``OmniAttention`` (:471-534), ``omni_attn`` (:537-565).
 
-``omni_attn`` runs the LoRA gather-apply kernel (when adapters are given)
-and then ``omni_attn`` of libomnistack_amd.so, which streams the packed
-cache once per GQA group.  Semantics follow the reference's CPU path
+``omni_attn`` is one call into libomnistack_amd.so (``omni_attn``, or
+``omni_attn_lora`` / ``omni_attn_serve`` with adapters or a cache index),
+which streams the packed cache once per GQA group; the per-user LoRA update
+of q runs inside the decode kernel's prologue where the shape allows.  Semantics follow the reference's CPU path
 (``_fused_attn_python``): K with QJL through the encoder's per-head G
 (seed (user_id % 1024) ^ h), V INT4 only, same codebooks, fp32 softmax;
 output float32 (B, n_heads, T, 128) as the reference's device path returns.
@@ -20,8 +21,11 @@ decode agree.
 
 Extensions (keyword-only): ``causal_offset`` (query t attends keys
 s <= causal_offset + t, for chunked prefill), ``rotate_q`` / ``sign_flip``
-(apply the cache's rotation to q inside the kernel), ``validate`` (check
-LoRA indices on the host and raise IndexError like the reference's CPU path).
+(apply the cache's rotation to q inside the kernel), ``cache_index``
+(query b attends cache sequence cache_index[b] of a pool: the serving loop's
+``nibbles[idx]`` gather without the copy), ``validate`` (check LoRA and
+cache indices on the host and raise IndexError like the reference's CPU
+path).
 """
 from __future__ import annotations
 
@@ -94,18 +98,34 @@ def _apply_lora_to_q(q: torch.Tensor, x: torch.Tensor, lora_a: torch.Tensor, lor
     return out if out.dtype == q.dtype else out.to(q.dtype)
 
 
+def _prep_cache_index(cache_index, B: int, n_seqs: int, dev, validate: bool) -> torch.Tensor:
+    """int64 (B,) device copy of a cache index; with `validate`, indices
+    outside [-n_seqs, n_seqs) raise IndexError as tensor indexing does."""
+    idx = torch.as_tensor(cache_index).to(device=dev, dtype=torch.int64).reshape(-1).contiguous()
+    if idx.numel() != B:
+        raise ValueError(f"cache_index must have {B} entries, got {idx.numel()}")
+    if validate and B > 0:
+        lo, hi = int(idx.min()), int(idx.max())
+        bad = hi if hi >= n_seqs else (lo if lo < -n_seqs else None)
+        if bad is not None:
+            raise IndexError(f"index {bad} is out of bounds for dimension 0 with size {n_seqs}")
+    return idx
+
+
 def _attn(q, k_nibbles, k_qjl, k_norms, v_nibbles, codebooks, user_id, scale, with_qjl,
-          causal_offset=None, rotate_q=False, sign_flip=None, lora=None) -> torch.Tensor:
+          causal_offset=None, rotate_q=False, sign_flip=None, lora=None, cache_index=None,
+          validate=True) -> torch.Tensor:
     """`lora`: _prep_lora's tuple; the update of q then runs inside the
-    attention call (omni_attn_lora)."""
+    attention call (omni_attn_lora).  `cache_index`: query b reads cache
+    sequence cache_index[b] of the pool k_nibbles[0..N) (omni_attn_serve)."""
     if q.dim() != 4 or k_nibbles.dim() != 4:
         raise ValueError("q must be (B, n_heads, T, D) and k_nibbles (B, n_kv_heads, S, D/2)")
     B, Hq, T, D = q.shape
     Bk, Hkv, S, nb = k_nibbles.shape
-    if Bk != B or 2 * nb != D:
+    if (Bk != B and cache_index is None) or 2 * nb != D:
         raise ValueError(f"q {tuple(q.shape)} and k_nibbles {tuple(k_nibbles.shape)} disagree")
-    if tuple(v_nibbles.shape) != (B, Hkv, S, nb):
-        raise ValueError(f"v_nibbles must be {(B, Hkv, S, nb)}, got {tuple(v_nibbles.shape)}")
+    if tuple(v_nibbles.shape) != (Bk, Hkv, S, nb):
+        raise ValueError(f"v_nibbles must be {(Bk, Hkv, S, nb)}, got {tuple(v_nibbles.shape)}")
     if Hq % Hkv != 0:
         raise ValueError(f"n_heads={Hq} must be divisible by n_kv_heads={Hkv}")
     dev = _lib.require_device(q, k_nibbles, v_nibbles, k_qjl if with_qjl else None,
@@ -131,14 +151,23 @@ def _attn(q, k_nibbles, k_qjl, k_norms, v_nibbles, codebooks, user_id, scale, wi
             int(rotate_q), _lib.ptr(sf), _lib.ptr(out))
     if lora is None:
         ws_bytes = L.omni_attn_workspace_size(B, Hq, Hkv, T, S, D)
-        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if ws_bytes else None
-        _lib.check(L.omni_attn(_lib.ptr(qc), qcode, *tail, _lib.ptr(ws), ws_bytes, _lib.stream_of(dev)))
-        return out
-    xc, ac, bc, wcode, idx, hidden, rank, n_loras, alpha = lora
-    ws_bytes = L.omni_attn_lora_workspace_size(B, Hq, Hkv, T, S, D, qcode)
+    else:
+        ws_bytes = L.omni_attn_lora_workspace_size(B, Hq, Hkv, T, S, D, qcode)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if ws_bytes else None
-    _lib.check(L.omni_attn_lora(_lib.ptr(qc), qcode, _lib.ptr(xc), _lib.ptr(ac), _lib.ptr(bc), wcode, _lib.ptr(idx),
-                                hidden, rank, n_loras, alpha, *tail, _lib.ptr(ws), ws_bytes, _lib.stream_of(dev)))
+    st = _lib.stream_of(dev)
+    if cache_index is not None:
+        cidx = _prep_cache_index(cache_index, B, Bk, dev, validate)
+        xc, ac, bc, wcode, idx, hidden, rank, n_loras, alpha = lora if lora is not None else \
+            (None, None, None, 0, None, 0, 0, 0, 0.0)
+        _lib.check(L.omni_attn_serve(_lib.ptr(qc), qcode, _lib.ptr(cidx), Bk, _lib.ptr(xc), _lib.ptr(ac),
+                                     _lib.ptr(bc), wcode, _lib.ptr(idx), hidden, rank, n_loras, alpha,
+                                     *tail, _lib.ptr(ws), ws_bytes, st))
+    elif lora is None:
+        _lib.check(L.omni_attn(_lib.ptr(qc), qcode, *tail, _lib.ptr(ws), ws_bytes, st))
+    else:
+        xc, ac, bc, wcode, idx, hidden, rank, n_loras, alpha = lora
+        _lib.check(L.omni_attn_lora(_lib.ptr(qc), qcode, _lib.ptr(xc), _lib.ptr(ac), _lib.ptr(bc), wcode,
+                                    _lib.ptr(idx), hidden, rank, n_loras, alpha, *tail, _lib.ptr(ws), ws_bytes, st))
     return out
 
 
@@ -176,29 +205,33 @@ def omni_attn(q: torch.Tensor, k_nibbles: torch.Tensor, k_qjl: torch.Tensor, k_n
               lora_b: Optional[torch.Tensor] = None, lora_indices: Optional[torch.Tensor] = None,
               lora_alpha: float = 1.0, *, causal_offset: Optional[int] = None,
               rotate_q: bool = False, sign_flip: Optional[torch.Tensor] = None,
-              validate: bool = True) -> torch.Tensor:
+              cache_index: Optional[torch.Tensor] = None, validate: bool = True) -> torch.Tensor:
     """INT4 + QJL compressed-KV attention with optional per-user LoRA on Q
     (fused_attention.py:537-565).  Returns float32 (B, n_heads, T, D)."""
-    if causal_offset is None and not rotate_q and validate:
+    if causal_offset is None and not rotate_q and cache_index is None and validate:
         return OmniAttention.apply(q, k_nibbles, k_qjl, k_norms, v_nibbles, codebooks, user_id, scale,
                                    with_qjl, g_matrix, x, lora_a, lora_b, lora_indices, lora_alpha)
     lora = _prep_lora(q, x, lora_a, lora_b, lora_indices, lora_alpha, validate) if x is not None else None
     return _attn(q, k_nibbles, k_qjl, k_norms, v_nibbles, codebooks, user_id, scale, with_qjl,
-                 causal_offset=causal_offset, rotate_q=rotate_q, sign_flip=sign_flip, lora=lora)
+                 causal_offset=causal_offset, rotate_q=rotate_q, sign_flip=sign_flip, lora=lora,
+                 cache_index=cache_index, validate=validate)
 
 
 class PackedKVAttention:
     """Prepared attention over one fixed packed cache (serving loops).
 
     Validates shapes, converts codebooks, uploads G and allocates the output
-    and split-K workspace once; ``run(q)`` then enqueues a single
-    ``omni_attn`` on the current stream and returns the (reused) float32
-    output buffer.  With a LoRA bank (``lora_a``, ``lora_b``, ``lora_alpha``)
-    ``run(q, x, lora_indices)`` first enqueues ``omni_lora_apply`` into a
-    preallocated q buffer (the semantics of ``_apply_lora_to_q``; indices are
-    not range-checked on the host, an index past the bank gives NaN rows).
-    Safe to capture in a HIP graph (no allocation, no host sync, no memset
-    inside ``run``).
+    and workspace once; ``run(q)`` then enqueues a single library call on
+    the current stream and returns the (reused) float32 output buffer.  With
+    a LoRA bank (``lora_a``, ``lora_b``, ``lora_alpha``),
+    ``run(q, x, lora_indices)`` applies the per-user update of q inside the
+    same call (the semantics of ``_apply_lora_to_q``; indices are not
+    range-checked on the host, an index past the bank gives NaN rows).
+    With ``batch`` given, the cache is a pool of ``k_nibbles.shape[0]``
+    sequences and ``run(..., cache_index=idx)`` serves ``batch`` queries,
+    query b reading pool sequence idx[b] (int64; an index outside the pool
+    gives NaN rows).  Safe to capture in a HIP graph (no allocation, no host
+    sync, no memset inside ``run``).
     """
 
     def __init__(self, k_nibbles, k_qjl, k_norms, v_nibbles, codebooks, n_heads: int, q_tokens: int = 1,
@@ -206,11 +239,16 @@ class PackedKVAttention:
                  q_dtype: torch.dtype = torch.bfloat16, rotate_q: bool = False,
                  sign_flip: Optional[torch.Tensor] = None, causal_offset: Optional[int] = None,
                  lora_a: Optional[torch.Tensor] = None, lora_b: Optional[torch.Tensor] = None,
-                 lora_alpha: float = 1.0):
-        B, Hkv, S, nb = k_nibbles.shape
+                 lora_alpha: float = 1.0, batch: Optional[int] = None):
+        N, Hkv, S, nb = k_nibbles.shape
         D = 2 * nb
         if n_heads % Hkv:
             raise ValueError(f"n_heads={n_heads} must be divisible by n_kv_heads={Hkv}")
+        if tuple(v_nibbles.shape) != (N, Hkv, S, nb):
+            raise ValueError(f"v_nibbles must be {(N, Hkv, S, nb)}, got {tuple(v_nibbles.shape)}")
+        B = N if batch is None else int(batch)
+        if B < 0 or N < 1:
+            raise ValueError("batch must be >= 0 and the cache pool non-empty")
         dev = _lib.require_device(k_nibbles, v_nibbles)
         from .quantize import _prep_codebooks
         self.cb, self.per_head = _prep_codebooks(codebooks, Hkv, dev)
@@ -226,17 +264,15 @@ class PackedKVAttention:
         self.shape = (B, n_heads, q_tokens, D)
         self.q_dtype = q_dtype
         self.device = dev
+        self.pool = None if batch is None else N
         self.out = torch.empty(self.shape, dtype=torch.float32, device=dev)
         L = _lib.lib()
-        self.ws_bytes = L.omni_attn_workspace_size(B, n_heads, Hkv, q_tokens, S, D)
-        self.ws = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device=dev)
-        self._fn = L.omni_attn
-        self._args = (_lib.ptr(self.kn), _lib.ptr(self.kq), _lib.ptr(self.kr), _lib.ptr(self.vn),
+        self._qcode = _lib.dtype_code(q_dtype)
+        self._tail = (_lib.ptr(self.kn), _lib.ptr(self.kq), _lib.ptr(self.kr), _lib.ptr(self.vn),
                       _lib.ptr(self.cb), self.per_head, _lib.ptr(self.gb), B, n_heads, Hkv, q_tokens, S, D,
                       float(1.0 / math.sqrt(D) if scale is None else scale), int(with_qjl),
                       -1 if causal_offset is None else int(causal_offset), int(rotate_q), _lib.ptr(self.sf),
-                      _lib.ptr(self.out), _lib.ptr(self.ws), self.ws_bytes)
-        self._qcode = _lib.dtype_code(q_dtype)
+                      _lib.ptr(self.out))
         self.lora = None
         if (lora_a is None) != (lora_b is None):
             raise ValueError("lora_a and lora_b must be given together")
@@ -250,38 +286,49 @@ class PackedKVAttention:
             self._la = lora_a.to(device=dev, dtype=wdt).contiguous()
             self._lb = lora_b.to(device=dev, dtype=wdt).contiguous()
             self.lora = (n_loras, rank, hidden, wdt)
-            # one launch per step: the q update runs inside the attention
-            # call (in the decode kernel's prologue when it serves the shape)
-            self.lora_ws_bytes = L.omni_attn_lora_workspace_size(B, n_heads, Hkv, q_tokens, S, D, self._qcode)
-            self.lora_ws = torch.empty(max(self.lora_ws_bytes, 1), dtype=torch.uint8, device=dev)
-            self._lora_fn = L.omni_attn_lora
             self._lora_head = (_lib.ptr(self._la), _lib.ptr(self._lb), _lib.dtype_code(wdt))
             self._lora_mid = (hidden, rank, n_loras, float(lora_alpha))
-            self._lora_args = self._args[:-2] + (_lib.ptr(self.lora_ws), self.lora_ws_bytes)
+            self.ws_bytes = L.omni_attn_lora_workspace_size(B, n_heads, Hkv, q_tokens, S, D, self._qcode)
+        else:
+            self.ws_bytes = L.omni_attn_workspace_size(B, n_heads, Hkv, q_tokens, S, D)
+        self.ws = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device=dev)
+        self._ws = (_lib.ptr(self.ws), self.ws_bytes)
+        self._fn, self._lora_fn, self._serve_fn = L.omni_attn, L.omni_attn_lora, L.omni_attn_serve
 
     def run(self, q: torch.Tensor, x: Optional[torch.Tensor] = None,
-            lora_indices: Optional[torch.Tensor] = None) -> torch.Tensor:
+            lora_indices: Optional[torch.Tensor] = None,
+            cache_index: Optional[torch.Tensor] = None) -> torch.Tensor:
         if tuple(q.shape) != self.shape or q.dtype != self.q_dtype or not q.is_contiguous():
             raise ValueError(f"q must be a contiguous {self.q_dtype} tensor of shape {self.shape}")
+        B, Hq, T, D = self.shape
         stream = torch.cuda.current_stream(self.device).cuda_stream
         qp = q.data_ptr()
+        lora_args = None
         if x is not None:
             if self.lora is None:
                 raise ValueError("run(q, x, ...) needs a LoRA bank at construction")
             n_loras, rank, hidden, wdt = self.lora
-            B, Hq, T, D = self.shape
             if tuple(x.shape) != (B, T, hidden) or x.dtype != wdt or not x.is_contiguous():
                 raise ValueError(f"x must be a contiguous {wdt} tensor of shape {(B, T, hidden)}")
             if (lora_indices is None or lora_indices.dtype != torch.int32 or lora_indices.numel() != B
                     or not lora_indices.is_contiguous()):
                 raise ValueError(f"lora_indices must be a contiguous int32 tensor of {B} entries")
             la, lb, wcode = self._lora_head
-            rc = self._lora_fn(qp, self._qcode, x.data_ptr(), la, lb, wcode, lora_indices.data_ptr(),
-                               *self._lora_mid, *self._lora_args, stream)
-            if rc:
-                _lib.check(rc)
-            return self.out
-        rc = self._fn(qp, self._qcode, *self._args, stream)
+            lora_args = (x.data_ptr(), la, lb, wcode, lora_indices.data_ptr(), *self._lora_mid)
+        if self.pool is not None:
+            if (cache_index is None or cache_index.dtype != torch.int64 or cache_index.numel() != B
+                    or not cache_index.is_contiguous()):
+                raise ValueError(f"cache_index must be a contiguous int64 tensor of {B} entries")
+            if lora_args is None:
+                lora_args = (None, None, None, 0, None, 0, 0, 0, 0.0)
+            rc = self._serve_fn(qp, self._qcode, cache_index.data_ptr(), self.pool, *lora_args, *self._tail,
+                                *self._ws, stream)
+        elif cache_index is not None:
+            raise ValueError("run(..., cache_index=...) needs batch= at construction")
+        elif lora_args is not None:
+            rc = self._lora_fn(qp, self._qcode, *lora_args, *self._tail, *self._ws, stream)
+        else:
+            rc = self._fn(qp, self._qcode, *self._tail, *self._ws, stream)
         if rc:
             _lib.check(rc)
         return self.out

@@ -113,6 +113,21 @@ def test_attn_lora_host_checks(L):
     assert n == ((base + 255) // 256) * 256 + 2 * 32 * 64 * 128 * 2
 
 
+def test_attn_serve_host_checks(L):
+    from omnistack_rs import _lib
+    tail = (None, None, None, None, None, 0, None, 1, 4, 2, 1, 10, 128, 1.0, 1, -1, 0, None, None, None, 0, None)
+    no_lora = (None, None, None, 0, None, 0, 0, 0, 0.0)
+    rc = L.omni_attn_serve(None, 2, None, 4, *no_lora, *tail)
+    assert rc == _lib.OMNI_EINVAL and "cache index" in _lib.last_error()
+    rc = L.omni_attn_serve(None, 2, 1, 0, *no_lora, *tail)        # checked before any device access
+    assert rc == _lib.OMNI_EINVAL and "n_cache_seqs" in _lib.last_error()
+    empty = (None, None, None, None, None, 0, None, 0, 4, 2, 1, 10, 128, 1.0, 1, -1, 0, None, None, None, 0, None)
+    assert L.omni_attn_serve(None, 2, None, 4, *no_lora, *empty) == 0
+    # adapters given (lora_a non-NULL) need the other LoRA operands
+    rc = L.omni_attn_serve(None, 2, 1, 4, None, 1, None, 2, None, 128, 8, 4, 1.0, *tail)
+    assert rc == _lib.OMNI_EINVAL and "NULL LoRA" in _lib.last_error()
+
+
 def test_workspace_size_host_only(L):
     # planning is host arithmetic; C3 shape needs split partials
     n = L.omni_attn_workspace_size(32, 32, 8, 1, 8192, 128)
