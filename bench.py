@@ -176,11 +176,11 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="C3 (and the CPU baseline) only")
     ap.add_argument("--only", default="",
-                    help="comma-separated sections to run (c3, c2, c2pool, c4, c5, c5d32), for profiling one "
+                    help="comma-separated sections to run (c3, c2, c2pool, c4, c5, c5d32, calib), for profiling one "
                          "configuration; the JSON line then carries only those sections")
     args = ap.parse_args()
     sections = set(args.only.split(",")) if args.only else (
-        {"c3"} if args.no_extras else {"c3", "c2", "c2pool", "c4", "c5", "c5d32"})
+        {"c3"} if args.no_extras else {"c3", "c2", "c2pool", "c4", "c5", "c5d32", "calib"})
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -374,6 +374,30 @@ def main() -> int:
         del kn6, kq6, kr6, vn6, att6
 
     # ── CPU baseline (reference CPU path restated in oracle/) ────────────
+    if "calib" in sections:
+        # the bake's codebook calibration: one Lloyd-Max codebook per kv head
+        # over every rotated token of a 256-user x 50-token cache
+        from omnistack_rs.kernels.hadamard import _wht_torch
+        from omnistack_rs.quantization.codebook import _lloyd_max_hip
+        NU, SC = 256, 50
+        log("[bench] calibration: 8 heads x 1.64 M samples, 300 Lloyd steps at most")
+        gc = torch.Generator(device=dev).manual_seed(47)
+        raw = torch.randn(NU, Hkv, SC, D, generator=gc, device=dev)
+        raw[..., :3] *= 8.0
+        rot = _wht_torch(raw)
+        runs = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            cbs, iters = _lloyd_max_hip(rot, Hkv, NU, SC * D, Hkv * SC * D, SC * D, 300, 1e-6)
+            torch.cuda.synchronize()
+            runs.append(time.perf_counter() - t0)
+        it = iters.cpu().tolist()
+        result["calibration"] = {"ms": round(min(runs) * 1e3, 2), "heads": Hkv, "samples_per_head": NU * SC * D,
+                                 "lloyd_steps": it,
+                                 "note": "omni_lloyd_max over a (256, 8, 50, 128) rotated f32 cache, wall time "
+                                         "of the call incl. launches; best of 3"}
+        log(f"[bench] calibration: {min(runs) * 1e3:.1f} ms (steps per head {it})")
+
     if not args.no_cpu and "c3" in sections:
         log(f"[bench] CPU baseline: oracle on the C3 batch, ~{args.cpu_budget_s:.0f} s budget")
         t_pass, n_pass, cores, t_seq1, n_seq1 = cpu_baseline_c3(kn, kq, kr, vn, cb, q, sign, uid, args.cpu_budget_s)

@@ -113,6 +113,32 @@ int omni_dequantize(const uint8_t *nibbles, const uint8_t *qjl, const float *nor
                     int with_qjl, float *out, void *stream);
 
 /*
+ * Lloyd-Max INT4 codebooks, one per group of samples:
+ *   init     16 equal-count bins of the sorted samples (bin size n / 16, the
+ *            n % 16 largest in no bin), centroid = bin mean;
+ *   iterate  code = first-index argmin_k fp32 |x - c_k|, c_k = mean of its
+ *            samples (empty cells keep theirs), until max_iters or the
+ *            largest fp32 move < tol;  output sorted ascending (n_groups, 16).
+ * Group g's sample e (e < outer * inner) is
+ *   x[(e / inner) * outer_stride + g * group_stride + e % inner]
+ * (a flat vector: outer = 1; head h of a (B, H, T, D) cache: outer = B,
+ * inner = T*D, outer_stride = H*T*D, group_stride = T*D).  Samples must be
+ * finite, n >= 16.  Means are taken from fp64 sums in a fixed order
+ * (deterministic); the reference's fp32 mean() can differ in the last bits.
+ * iters_out (device int32 per group, nullable) receives the steps run.
+ * workspace: omni_lloyd_max_workspace_size(...) bytes.
+ * Replaces LloydMaxCalibrator.fit / calibrate_codebook / calibrate_per_group
+ * (omnistack_rs/quantization/codebook.py:64-108, :129-172) as the bake calls
+ * them (scripts/run_criteo_benchmark.py:357-362).
+ */
+size_t omni_lloyd_max_workspace_size(int n_groups, int64_t outer, int64_t inner);
+
+int omni_lloyd_max(const void *x, int x_dtype, int n_groups, int64_t outer, int64_t inner,
+                   int64_t outer_stride, int64_t group_stride, int max_iters, float tol,
+                   float *codebooks, int32_t *iters_out, void *workspace, size_t workspace_bytes,
+                   void *stream);
+
+/*
  * Per-user LoRA on queries, branchless gather-apply:
  *   q_out[b] = dtype(q[b] + reshape(((x[b] A[id]^T) B[id]^T) * alpha))  if id = idx[b] >= 0
  *   q_out[b] = q[b]                                                      if id < 0

@@ -1,6 +1,7 @@
 from omnistack_rs.quantization.codebook import (
     LloydMaxCalibrator,
     calibrate_codebook,
+    calibrate_heads,
     calibrate_per_group,
 )
 from omnistack_rs.quantization.qjl import RademacherQJL, qjl_encode, qjl_reconstruct
@@ -9,6 +10,7 @@ __all__ = [
     "LloydMaxCalibrator",
     "calibrate_codebook",
     "calibrate_per_group",
+    "calibrate_heads",
     "RademacherQJL",
     "qjl_encode",
     "qjl_reconstruct",

@@ -6,14 +6,21 @@ API of the reference module omnistack_rs/quantization/codebook.py:
 bins of the sorted samples give the initial centroids; then nearest-centroid
 assignment (first index on ties), per-cell mean update (empty cells keep
 their centroid), stop when the largest centroid move is below the tolerance;
-the result is sorted ascending.  It runs with torch on whatever device the
-samples live on; cell means are reduced with index_add, so the last fp32
-bits can differ from the reference's masked ``mean()``.  Calibration happens
-once per cache, off the encode/decode path.
+the result is sorted ascending.
+
+Samples on a HIP device run ``omni_lloyd_max`` (csrc/calib.hip: radix-select
+initialisation, one pass per Lloyd step, fp64 cell sums in a fixed order);
+``calibrate_heads`` calibrates every head of a (B, H, T, D) cache in one
+call without copying the per-head samples.  CPU samples run the same recipe
+with torch on the CPU, as the reference does.  Either way cell means are not
+the reference's fp32 masked ``mean()``, so the last bits can differ.
+Calibration happens once per cache, off the encode/decode path.
 """
 from __future__ import annotations
 
 import torch
+
+from .. import _lib
 
 N_CENTROIDS: int = 16
 _DEFAULT_MAX_ITERS: int = 300
@@ -27,6 +34,26 @@ def _nearest(x: torch.Tensor, c: torch.Tensor) -> torch.Tensor:
         e = min(x.shape[0], s + _ASSIGN_CHUNK)
         out[s:e] = (x[s:e].unsqueeze(1) - c.unsqueeze(0)).abs().argmin(dim=1)
     return out
+
+
+def _lloyd_max_hip(x: torch.Tensor, groups: int, outer: int, inner: int, outer_stride: int, group_stride: int,
+                   max_iters: int, tol: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """(groups, 16) f32 codebooks and (groups,) int32 step counts from the
+    library, for samples laid out as omni_lloyd_max describes."""
+    if not bool(torch.isfinite(x).all()):
+        raise ValueError("calibration samples must be finite")
+    if x.dtype not in _lib.DTYPE_CODE:
+        x = x.float()
+    dev = x.device
+    L = _lib.lib()
+    ws_bytes = L.omni_lloyd_max_workspace_size(groups, outer, inner)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    out = torch.empty(groups, N_CENTROIDS, dtype=torch.float32, device=dev)
+    iters = torch.empty(groups, dtype=torch.int32, device=dev)
+    _lib.check(L.omni_lloyd_max(_lib.ptr(x), _lib.dtype_code(x.dtype), groups, outer, inner, outer_stride,
+                                group_stride, int(max_iters), float(tol), _lib.ptr(out), _lib.ptr(iters),
+                                _lib.ptr(ws), ws_bytes, _lib.stream_of(dev)))
+    return out, iters
 
 
 class LloydMaxCalibrator:
@@ -48,9 +75,14 @@ class LloydMaxCalibrator:
         return self._codebook
 
     def fit(self, samples: torch.Tensor) -> "LloydMaxCalibrator":
+        if samples.numel() < self.n_centroids:
+            raise ValueError(f"Need at least {self.n_centroids} samples; got {samples.numel()}")
+        if samples.device.type == "cuda":
+            x = samples.reshape(-1).contiguous()
+            cb, self.n_iter = _lloyd_max_hip(x, 1, 1, x.numel(), 0, 0, self.max_iters, self.convergence_tol)
+            self._codebook = cb[0]
+            return self
         x = samples.reshape(-1).float()
-        if x.numel() < self.n_centroids:
-            raise ValueError(f"Need at least {self.n_centroids} samples; got {x.numel()}")
         k = self.n_centroids
         xs = x.sort().values
         bs = xs.shape[0] // k
@@ -83,4 +115,28 @@ def calibrate_per_group(samples_by_group: list[torch.Tensor], max_iters: int = _
                         convergence_tol: float = _DEFAULT_TOL) -> torch.Tensor:
     if len(samples_by_group) == 0:
         raise ValueError("samples_by_group must be non-empty")
+    first = samples_by_group[0]
+    if (first.device.type == "cuda" and first.numel() >= N_CENTROIDS
+            and all(s.device == first.device and s.numel() == first.numel() and s.dtype == first.dtype
+                    for s in samples_by_group)):
+        # equal-size groups: one library call over a (groups, n) stack
+        x = torch.stack([s.reshape(-1) for s in samples_by_group])
+        n = first.numel()
+        return _lloyd_max_hip(x, len(samples_by_group), 1, n, 0, n, max_iters, convergence_tol)[0]
     return torch.stack([calibrate_codebook(s, max_iters, convergence_tol) for s in samples_by_group])
+
+
+def calibrate_heads(x: torch.Tensor, max_iters: int = _DEFAULT_MAX_ITERS,
+                    convergence_tol: float = _DEFAULT_TOL) -> torch.Tensor:
+    """One codebook per head of a (B, H, T, D) device tensor: the bake's
+    calibrate_per_group([x[:, h].reshape(-1) for h in range(H)])
+    (scripts/run_criteo_benchmark.py:357-362) in one call, reading the
+    heads in place.  Returns (H, 16) float32 on x's device."""
+    if x.dim() != 4:
+        raise ValueError(f"x must be (B, H, T, D), got {tuple(x.shape)}")
+    _lib.require_device(x)
+    B, H, T, D = x.shape
+    if B * T * D < N_CENTROIDS:
+        raise ValueError(f"Need at least {N_CENTROIDS} samples per head; got {B * T * D}")
+    xc = x.contiguous()
+    return _lloyd_max_hip(xc, H, B, T * D, H * T * D, T * D, max_iters, convergence_tol)[0]

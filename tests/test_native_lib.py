@@ -128,6 +128,41 @@ def test_attn_serve_host_checks(L):
     assert rc == _lib.OMNI_EINVAL and "NULL LoRA" in _lib.last_error()
 
 
+def test_lloyd_max_host_checks(L):
+    from omnistack_rs import _lib
+    assert L.omni_lloyd_max_workspace_size(0, 1, 100) == 0
+    assert L.omni_lloyd_max_workspace_size(2, 3, 6400) > L.omni_lloyd_max_workspace_size(1, 3, 6400)
+    rc = L.omni_lloyd_max(None, 0, 1, 1, 15, 0, 0, 10, 1e-6, None, None, None, 0, None)
+    assert rc == _lib.OMNI_EINVAL and "16 samples" in _lib.last_error()
+    rc = L.omni_lloyd_max(None, 5, 1, 1, 100, 0, 0, 10, 1e-6, None, None, None, 0, None)
+    assert rc == _lib.OMNI_EINVAL and "dtype" in _lib.last_error()
+    rc = L.omni_lloyd_max(None, 0, 1, 1, 100, 0, 0, -1, 1e-6, None, None, None, 0, None)
+    assert rc == _lib.OMNI_EINVAL and "max_iters" in _lib.last_error()
+    rc = L.omni_lloyd_max(1, 0, 1, 1, 100, 0, 0, 10, 1e-6, 1, None, None, 0, None)
+    assert rc == _lib.OMNI_EWORKSPACE
+
+
+def test_bake_file_format_round_trip(tmp_path):
+    from omnistack_rs.bake import BAKE_KEYS, bake_stats, load_bake, save_bake
+    g = torch.Generator().manual_seed(3)
+    nib = torch.randint(0, 256, (2, 3, 5, 64), generator=g, dtype=torch.uint8)
+    qjl = torch.randint(0, 256, (2, 3, 5, 8), generator=g, dtype=torch.uint8)
+    norms = torch.rand(2, 3, 5, generator=g)
+    cb = torch.linspace(-2, 2, 16).repeat(3, 1)
+    stats = save_bake(tmp_path / "b.pt", nib, qjl, norms, cb)
+    assert stats == {"n_users": 2, "n_kv_heads": 3, "seq_len": 5, "bf16_bytes": 7680, "compressed_bytes": 2280,
+                     "compression_ratio": 3.368, "bits_per_element": 4.75}
+    assert bake_stats(nib, qjl, norms) == stats
+    got = load_bake(tmp_path / "b.pt")
+    assert all(torch.equal(a, b) for a, b in zip(got[:4], (nib, qjl, norms, cb))) and got[4] == stats
+    # a file in the reference's format (plain torch.save of the dict) loads the same way
+    torch.save({k: v for k, v in zip(BAKE_KEYS, (nib, qjl, norms, cb, stats))}, tmp_path / "ref.pt")
+    assert load_bake(tmp_path / "ref.pt")[4] == stats
+    torch.save({"nibbles": nib}, tmp_path / "bad.pt")
+    with pytest.raises(KeyError):
+        load_bake(tmp_path / "bad.pt")
+
+
 def test_workspace_size_host_only(L):
     # planning is host arithmetic; C3 shape needs split partials
     n = L.omni_attn_workspace_size(32, 32, 8, 1, 8192, 128)
