@@ -293,7 +293,9 @@ class PackedKVAttention:
             self.ws_bytes = L.omni_attn_workspace_size(B, n_heads, Hkv, q_tokens, S, D)
         self.ws = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device=dev)
         self._ws = (_lib.ptr(self.ws), self.ws_bytes)
-        self._fn, self._lora_fn, self._serve_fn = L.omni_attn, L.omni_attn_lora, L.omni_attn_serve
+        self._fn = L.omni_attn
+        self._lora_fn = L.omni_attn_lora if self.lora is not None else None
+        self._serve_fn = L.omni_attn_serve if self.pool is not None else None
 
     def run(self, q: torch.Tensor, x: Optional[torch.Tensor] = None,
             lora_indices: Optional[torch.Tensor] = None,
