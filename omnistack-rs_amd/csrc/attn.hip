@@ -561,6 +561,10 @@ __device__ __forceinline__ float dpp_quad_bcast(float v, int i) {
 __device__ __forceinline__ float dpp_row_shl8(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x108, 0xf, 0xf, false));
 }
+// lane i of each 16-lane row reads lane i ^ 8 (rotate by 8)
+__device__ __forceinline__ uint32_t dpp_row_ror8(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xf, 0xf, false);
+}
 
 // LDS byte offset of the LUT entry for byte k of w: (byte << 8) | copy offset.
 __device__ __forceinline__ uint32_t lut_addr(uint32_t w, uint32_t laneoff, int k) {
@@ -1116,7 +1120,8 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
                 // nor the output.
                 float v = acc[i];
                 if (QJL) v = __builtin_fmaf(dpp_quad_bcast(R.nr[u], i), qacc[i], v);
-                sc[4 * u + i] = (v + dpp_row_shl8(v)) * csc;
+                // columns n and n + 8 (hi and lo parts of row n) both get the sum
+                sc[4 * u + i] = (v + __uint_as_float(dpp_row_ror8(__float_as_uint(v)))) * csc;
             }
         }
         if (!full) {
@@ -1142,14 +1147,20 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
             m_run = need ? mt : m_run;
         }
         const float m_use = (m_run == -INFINITY) ? 0.0f : m_run;
+        // lanes n and n + 8 hold the same scores: columns 0-7 exponentiate the
+        // tile's first 16 tokens, columns 8-15 the last 16, and the halves
+        // trade places by a row rotation (B columns 8-15 feed output columns
+        // that are never read, so what they hold does not matter)
+        const float e0 = lo_col ? sc[4] : sc[0], e1 = lo_col ? sc[5] : sc[1];
+        const float e2 = lo_col ? sc[6] : sc[2], e3 = lo_col ? sc[7] : sc[3];
+        const uint32_t my01 = cvt_pk_h2(__builtin_amdgcn_exp2f(e0 - m_use), __builtin_amdgcn_exp2f(e1 - m_use));
+        const uint32_t my23 = cvt_pk_h2(__builtin_amdgcn_exp2f(e2 - m_use), __builtin_amdgcn_exp2f(e3 - m_use));
+        const uint32_t ot01 = dpp_row_ror8(my01), ot23 = dpp_row_ror8(my23);
         half8_t pb[2];
+        pb[0] = as_half8(my01, my01, my23, my23);
+        pb[1] = as_half8(ot01, ot01, ot23, ot23);
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const uint32_t p01 = cvt_pk_h2(__builtin_amdgcn_exp2f(sc[4 * u] - m_use), __builtin_amdgcn_exp2f(sc[4 * u + 1] - m_use));
-            const uint32_t p23 = cvt_pk_h2(__builtin_amdgcn_exp2f(sc[4 * u + 2] - m_use), __builtin_amdgcn_exp2f(sc[4 * u + 3] - m_use));
-            pb[u] = as_half8(p01, p01, p23, p23);
-            lacc_sum = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb[u], lacc_sum, 0, 0, 0);
-        }
+        for (int u = 0; u < 2; ++u) lacc_sum = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb[u], lacc_sum, 0, 0, 0);
 
         // PV: pair bytes interleave the nibbles of two tokens at one d, so
         // each LUT entry is an MFMA-ready (hi pair, lo pair) for that d.
