@@ -75,21 +75,31 @@ __device__ __forceinline__ float lm_load(const LmArgs &a, int64_t o, int64_t i, 
 // Visit this thread's elements of group g in a fixed order:
 // e = start, start + stride, ... (grid-stride over the flattened index,
 // the (row, column) pair advanced without division).
+// Eight loads are issued before the eight samples are used (the loop is
+// otherwise bound by one memory latency per sample).
 template <int DT, typename F>
 __device__ __forceinline__ void lm_for_each(const LmArgs &a, int g, F &&f) {
+    constexpr int U = 8;
     const int64_t stride = (int64_t)a.blocks * kLmThreads;
     const int64_t start = (int64_t)blockIdx.x * kLmThreads + threadIdx.x;
     if (start >= a.n) return;
     const int64_t so = stride / a.inner, si = stride % a.inner;
     int64_t o = start / a.inner, i = start % a.inner;
-    for (int64_t e = start; e < a.n; e += stride) {
-        f(lm_load<DT>(a, o, i, g));
-        o += so;
-        i += si;
-        if (i >= a.inner) {
-            i -= a.inner;
-            ++o;
+    for (int64_t e = start; e < a.n; e += U * stride) {
+        float xv[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            xv[u] = e + u * stride < a.n ? lm_load<DT>(a, o, i, g) : 0.0f;
+            o += so;
+            i += si;
+            if (i >= a.inner) {
+                i -= a.inner;
+                ++o;
+            }
         }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (e + u * stride < a.n) f(xv[u]);
     }
 }
 
@@ -137,29 +147,55 @@ __global__ __launch_bounds__(kLmThreads) void lm_radix_kernel(LmArgs a, int pass
         if (lh[s]) atomicAdd(&h[s], lh[s]);
 }
 
-// After a radix pass: each order statistic picks its digit, the unique
-// prefixes for the next pass are listed, and the histograms are cleared.
-__global__ void lm_select_kernel(LmArgs a) {
+// After a radix pass: each order statistic picks its digit (one wave per
+// statistic: a prefix sum of the 256 bin counts over the lanes, four bins
+// per lane), the unique prefixes for the next pass are listed, and the
+// histograms are cleared.
+__global__ __launch_bounds__(256) void lm_select_kernel(LmArgs a) {
     const int g = blockIdx.y;
     uint32_t *h = a.hist + (size_t)g * kLmK * 256;
     uint32_t *upg = a.uprefix + g * (kLmK + 1);
-    if (threadIdx.x == 0) {
-        const uint32_t nu = upg[0];
-        uint32_t newp[kLmK];
-        for (int j = 0; j < kLmK; ++j) {
-            const uint32_t p = a.prefix[g * kLmK + j];
-            uint32_t u = 0;
-            while (u + 1 < nu && upg[1 + u] != p) ++u;
-            int64_t k = a.krank[g * kLmK + j];
-            int d = 0;
-            for (; d < 255; ++d) {
-                const int64_t c = h[u * 256 + d];
-                if (k < c) break;
-                k -= c;
+    __shared__ uint32_t newp[kLmK];
+    const uint32_t nu = upg[0];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    for (int j = w; j < kLmK; j += 4) {
+        const uint32_t p = a.prefix[g * kLmK + j];
+        uint32_t u = 0;
+        while (u + 1 < nu && upg[1 + u] != p) ++u;
+        const int64_t k = a.krank[g * kLmK + j];
+        const uint4 c4 = reinterpret_cast<const uint4 *>(h + u * 256)[lane];
+        const uint64_t mine = (uint64_t)c4.x + c4.y + c4.z + c4.w;
+        uint64_t incl = mine;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const uint64_t y = __shfl_up(incl, off);
+            if (lane >= off) incl += y;
+        }
+        // the bin holding rank k lies in the first lane whose inclusive count exceeds k
+        const uint64_t over = __ballot(incl > (uint64_t)k);
+        const int L = over ? __ffsll((unsigned long long)over) - 1 : 63;
+        int64_t kk = k - (int64_t)__shfl(incl - mine, L);
+        const uint32_t b0 = __shfl(c4.x, L), b1 = __shfl(c4.y, L), b2 = __shfl(c4.z, L);
+        int d = 4 * L;
+        if (kk >= (int64_t)b0) {
+            kk -= b0;
+            ++d;
+            if (kk >= (int64_t)b1) {
+                kk -= b1;
+                ++d;
+                if (kk >= (int64_t)b2) {
+                    kk -= b2;
+                    ++d;
+                }
             }
-            a.krank[g * kLmK + j] = k;
+        }
+        if (lane == 0) {
+            a.krank[g * kLmK + j] = kk;
             newp[j] = (p << 8) | (uint32_t)d;
         }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
         uint32_t n = 0;
         for (int j = 0; j < kLmK; ++j) {
             a.prefix[g * kLmK + j] = newp[j];
@@ -167,8 +203,15 @@ __global__ void lm_select_kernel(LmArgs a) {
         }
         upg[0] = n;
     }
-    __syncthreads();
-    for (int s = threadIdx.x; s < kLmK * 256; s += blockDim.x) h[s] = 0u;
+    for (int t = threadIdx.x; t < kLmK * 256; t += blockDim.x) h[t] = 0u;
+}
+
+// Adds x to this thread's own LDS slot (fp64 sum, count).  Slots are
+// private to a thread, so the additions happen in its program order (the
+// same sums as register accumulators, without a 17-way select per sample).
+__device__ __forceinline__ void lm_slot_add(double *sum, uint32_t *cnt, float x) {
+    __hip_atomic_fetch_add(sum, (double)x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 // Block-wide fixed-order sum of nq (sum, count) pairs into the partials:
@@ -212,42 +255,64 @@ __device__ __forceinline__ void lm_block_store(const LmArgs &a, int g, double (&
 template <int DT>
 __global__ __launch_bounds__(kLmThreads) void lm_interval_kernel(LmArgs a) {
     const int g = blockIdx.y;
+    __shared__ double ls[kLmIntervals][kLmThreads];
+    __shared__ uint32_t lc[kLmIntervals][kLmThreads];
+    const int th = threadIdx.x;
     float v[kLmK];
 #pragma unroll
     for (int j = 0; j < kLmK; ++j) v[j] = lm_value(a.prefix[g * kLmK + j]);
-    double s[kLmIntervals];
-    uint64_t c[kLmIntervals];
 #pragma unroll
     for (int q = 0; q < kLmIntervals; ++q) {
-        s[q] = 0.0;
-        c[q] = 0;
+        ls[q][th] = 0.0;
+        lc[q][th] = 0u;
     }
     lm_for_each<DT>(a, g, [&](float x) {
         int t = 0;
 #pragma unroll
         for (int j = 0; j < kLmK; ++j) t += v[j] <= x ? 1 : 0;
-#pragma unroll
-        for (int q = 0; q < kLmIntervals; ++q) {
-            s[q] += q == t ? (double)x : 0.0;
-            c[q] += q == t ? 1u : 0u;
-        }
+        lm_slot_add(&ls[t][th], &lc[t][th], x);
     });
+    double s[kLmIntervals];
+    uint64_t c[kLmIntervals];
+#pragma unroll
+    for (int q = 0; q < kLmIntervals; ++q) {
+        s[q] = ls[q][th];
+        c[q] = lc[q][th];
+    }
     lm_block_store(a, g, s, c, kLmIntervals);
 }
 
-// Initial centroids from the order statistics and the interval sums.
-__global__ void lm_init_kernel(LmArgs a) {
+// Initial centroids from the order statistics and the interval sums
+// (thread t < 255 sums interval t / 15 over blocks t % 15, t % 15 + 15, ...;
+// the 15 partial sums of an interval are then added in order).
+__global__ __launch_bounds__(256) void lm_init_kernel(LmArgs a) {
     const int g = blockIdx.y;
-    if (threadIdx.x != 0) return;
+    constexpr int kParts = 15;
+    __shared__ double ps[kLmIntervals][kParts];
+    __shared__ uint64_t pc[kLmIntervals][kParts];
+    const int t = threadIdx.x;
+    if (t < kLmIntervals * kParts) {
+        const int q = t / kParts, part = t % kParts;
+        double s = 0.0;
+        uint64_t n = 0;
+        for (int bl = part; bl < a.blocks; bl += kParts) {
+            const size_t o = ((size_t)g * a.blocks + bl) * kLmIntervals + q;
+            s += a.psum[o];
+            n += a.pcnt[o];
+        }
+        ps[q][part] = s;
+        pc[q][part] = n;
+    }
+    __syncthreads();
+    if (t != 0) return;
     double isum[kLmIntervals];
     uint64_t icnt[kLmIntervals];
     for (int q = 0; q < kLmIntervals; ++q) {
         isum[q] = 0.0;
         icnt[q] = 0;
-        for (int bl = 0; bl < a.blocks; ++bl) {
-            const size_t o = ((size_t)g * a.blocks + bl) * kLmIntervals + q;
-            isum[q] += a.psum[o];
-            icnt[q] += a.pcnt[o];
+        for (int part = 0; part < kParts; ++part) {
+            isum[q] += ps[q][part];
+            icnt[q] += pc[q][part];
         }
     }
     double prev_f = 0.0, s_lt = 0.0;
@@ -269,15 +334,15 @@ template <int DT>
 __global__ __launch_bounds__(kLmThreads) void lm_assign_kernel(LmArgs a) {
     const int g = blockIdx.y;
     if (a.state[2 * g]) return;                      // converged: uniform for the block
+    __shared__ double ls[kLmK][kLmThreads];
+    __shared__ uint32_t lc[kLmK][kLmThreads];
+    const int th = threadIdx.x;
     float c[kLmK];
 #pragma unroll
-    for (int k = 0; k < kLmK; ++k) c[k] = a.cent[g * kLmK + k];
-    double s[kLmIntervals];
-    uint64_t n[kLmIntervals];
-#pragma unroll
-    for (int q = 0; q < kLmIntervals; ++q) {
-        s[q] = 0.0;
-        n[q] = 0;
+    for (int k = 0; k < kLmK; ++k) {
+        c[k] = a.cent[g * kLmK + k];
+        ls[k][th] = 0.0;
+        lc[k][th] = 0u;
     }
     lm_for_each<DT>(a, g, [&](float x) {
         int best = 0;
@@ -290,12 +355,17 @@ __global__ __launch_bounds__(kLmThreads) void lm_assign_kernel(LmArgs a) {
                 best = k;
             }
         }
-#pragma unroll
-        for (int k = 0; k < kLmK; ++k) {
-            s[k] += k == best ? (double)x : 0.0;
-            n[k] += k == best ? 1u : 0u;
-        }
+        lm_slot_add(&ls[best][th], &lc[best][th], x);
     });
+    double s[kLmIntervals];
+    uint64_t n[kLmIntervals];
+#pragma unroll
+    for (int k = 0; k < kLmK; ++k) {
+        s[k] = ls[k][th];
+        n[k] = lc[k][th];
+    }
+    s[kLmK] = 0.0;
+    n[kLmK] = 0;
     lm_block_store(a, g, s, n, kLmK);
 }
 
@@ -405,7 +475,7 @@ static void lm_launch(const LmArgs &a, int groups, hipStream_t st) {
         hipLaunchKernelGGL(lm_select_kernel, one, dim3(256), 0, st, a);
     }
     hipLaunchKernelGGL((lm_interval_kernel<DT>), grid, dim3(kLmThreads), 0, st, a);
-    hipLaunchKernelGGL(lm_init_kernel, one, dim3(64), 0, st, a);
+    hipLaunchKernelGGL(lm_init_kernel, one, dim3(256), 0, st, a);
     for (int it = 0; it < a.max_iters; ++it) {
         hipLaunchKernelGGL((lm_assign_kernel<DT>), grid, dim3(kLmThreads), 0, st, a);
         hipLaunchKernelGGL(lm_update_kernel, one, dim3(256), 0, st, a);
