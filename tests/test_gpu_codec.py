@@ -308,3 +308,50 @@ def test_fast_encoder_matches_row_kernel(device):
     slow = [quantize_heads(x[:, :, i:i + 1].to(device), cb.to(device), user_id=5) for i in range(64)]
     for k in range(3):
         assert torch.equal(fast[k].cpu(), torch.cat([t[k].cpu() for t in slow], dim=2)), f"output {k}"
+
+
+@pytest.mark.parametrize("D,dtype", [(128, torch.float32), (128, torch.bfloat16), (32, torch.float32)])
+def test_qjl_module_matches_oracle(device, D, dtype):
+    """RademacherQJL / qjl_encode / qjl_reconstruct (quantization/qjl.py:46-186)
+    at the codec's shapes run the codec kernels: signs and the reconstruction
+    against the restated reference (fp32 G matmul), norms within 2 ulp."""
+    from omnistack_rs.quantization import RademacherQJL, qjl_encode, qjl_reconstruct
+    head, uid = 5, 1234
+    seed = (uid % 1024) ^ head
+    err = (torch.randn(3, 7, D, generator=_data.gen(60 + D)) * 0.3).to(dtype)
+    qjl = RademacherQJL(head_dim=D, qjl_dim=D // 2)
+    signs, norms = qjl.encode(err.to(device), head, user_id=uid)
+    assert signs.dtype == torch.bool and signs.shape == (3, 7, D // 2)
+    assert norms.dtype == dtype and norms.shape == (3, 7, 1)
+    r_signs, _ = restate.qjl_encode_batch(err.float().reshape(-1, D), seed)
+    assert (signs.cpu().reshape(-1, D // 2) != r_signs).sum().item() <= 1
+    r_norms = err.float().norm(dim=-1, keepdim=True)
+    assert exact.ulp_distance_f32(norms.cpu().float().numpy(), r_norms.to(dtype).float().numpy()).max() <= \
+        (2 if dtype == torch.float32 else 1 << 16)
+    # reconstruction: integer sign sums times one rounded factor, as the reference
+    got = qjl.reconstruct(signs, norms.float(), head, user_id=uid).cpu()
+    s = signs.cpu().reshape(-1, D // 2)
+    packed = torch.zeros(s.shape[0], D // 16, dtype=torch.uint8)
+    for bit in range(8):
+        packed |= s[:, bit::8].to(torch.uint8) << bit
+    want = restate.qjl_reconstruct_batch(packed, norms.cpu().float().reshape(-1), seed, D)
+    assert torch.equal(got.reshape(-1, D), want)
+    # module functions
+    x_orig = torch.randn(4, D, generator=_data.gen(70)).to(device)
+    x_deq = (x_orig * 0.9).contiguous()
+    e, s2, n2 = qjl_encode(x_orig, x_deq, head, qjl_dim=D // 2, user_id=uid)
+    assert torch.equal(e, x_orig - x_deq)
+    rec = qjl_reconstruct(x_deq, s2, n2, head, qjl_dim=D // 2, user_id=uid)
+    assert ((rec - x_orig).norm() < (x_deq - x_orig).norm())         # the residual estimate helps
+
+
+def test_qjl_module_other_dims_on_device(device):
+    """qjl_dim != head_dim / 2 keeps the reference formula (torch on the device)."""
+    from omnistack_rs.quantization import RademacherQJL
+    qjl = RademacherQJL(head_dim=128, qjl_dim=32)
+    err = torch.randn(6, 128, generator=_data.gen(71))
+    signs, norms = qjl.encode(err.to(device), 2, user_id=9)
+    G = qjl._make_G(2, torch.device("cpu"), torch.float32, 9)
+    assert (signs.cpu() != ((err @ G.T) >= 0)).sum().item() <= 1
+    with pytest.raises(RuntimeError, match="HIP devices only"):
+        qjl.encode(err, 2, user_id=9)
