@@ -176,11 +176,11 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="C3 (and the CPU baseline) only")
     ap.add_argument("--only", default="",
-                    help="comma-separated sections to run (c3, c2, c2pool, c4, c5, c5d32, calib), for profiling one "
+                    help="comma-separated sections to run (c3, c2, c2pool, c4, c5, c5d32, calib, dense), for profiling one "
                          "configuration; the JSON line then carries only those sections")
     args = ap.parse_args()
     sections = set(args.only.split(",")) if args.only else (
-        {"c3"} if args.no_extras else {"c3", "c2", "c2pool", "c4", "c5", "c5d32", "calib"})
+        {"c3"} if args.no_extras else {"c3", "c2", "c2pool", "c4", "c5", "c5d32", "calib", "dense"})
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -397,6 +397,30 @@ def main() -> int:
                                  "note": "omni_lloyd_max over a (256, 8, 50, 128) rotated f32 cache, wall time "
                                          "of the call incl. launches; best of 3"}
         log(f"[bench] calibration: {min(runs) * 1e3:.1f} ms (steps per head {it})")
+
+    if "dense" in sections:
+        # the reference CPU path's attention (reference_attn) on the device:
+        # C3's shape with K / V already dequantized to fp32
+        from omnistack_rs.attention import reference_attn
+        log("[bench] dense: reference_attn at C3's shape, fp32 K / V (2.15 GB)")
+        BD, SD = 32, 8192
+        gd = torch.Generator(device=dev).manual_seed(48)
+        kd = torch.randn(BD, Hkv, SD, D, generator=gd, device=dev)
+        vd = torch.randn(BD, Hkv, SD, D, generator=gd, device=dev)
+        qd = torch.randn(BD, Hq, 1, D, generator=gd, device=dev)
+        fn = lambda: reference_attn(qd, kd, vd)
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        per = sorted(per_call_events(fn, 20, 2, stream))
+        td = per[len(per) // 2]
+        dbytes = 2 * kd.numel() * 4 + qd.numel() * 4 + BD * Hq * D * 4
+        result["dense_c3_shape"] = {"us_per_call": round(td * 1e6, 1), "GB_s": round(dbytes / td / 1e9, 1),
+                                    "frac_of_hbm_peak": round(dbytes / td / 8e12, 4), "bytes": dbytes,
+                                    "note": "omni_dense_attn (reference_attn) on fp32 K/V of C3's shape; "
+                                            "median of 20 HIP-event timings"}
+        log(f"[bench] dense: {td * 1e6:.0f} us -> {dbytes / td / 1e9:.0f} GB/s")
+        del kd, vd
 
     if not args.no_cpu and "c3" in sections:
         log(f"[bench] CPU baseline: oracle on the C3 batch, ~{args.cpu_budget_s:.0f} s budget")

@@ -113,6 +113,22 @@ int omni_dequantize(const uint8_t *nibbles, const uint8_t *qjl, const float *nor
                     int with_qjl, float *out, void *stream);
 
 /*
+ * Dense fp32 GQA attention on dequantized K / V:
+ *   out[b, h, t] = softmax_s(scale * q[b, h, t] . k[b, h / G, s] + mask[b, h, t, s]) . v[b, h / G, s]
+ * q (B, Hq, T, D), k and v (B, Hkv, S, D), out (B, Hq, T, D), all f32
+ * contiguous; D in {32, 64, 128, 256}.  mask (nullable) is additive, read at
+ * b * ms[0] + h * ms[1] + t * ms[2] + s * ms[3] (stride 0 broadcasts).
+ * Online softmax in fp32; a row whose first `first_tile` keys are all
+ * masked, or that has a NaN score, comes out NaN as the reference's tile
+ * loop gives it (first_tile = the reference's tile_size).
+ * Replaces reference_attn + repeat_kv (omnistack_rs/attention/reference.py:
+ * 49-67, :72-177) on the device.
+ */
+int omni_dense_attn(const float *q, const float *k, const float *v, const float *mask,
+                    const int64_t *mask_strides, int64_t B, int Hq, int Hkv, int64_t T, int64_t S,
+                    int head_dim, float scale, int64_t first_tile, float *out, void *stream);
+
+/*
  * Lloyd-Max INT4 codebooks, one per group of samples:
  *   init     16 equal-count bins of the sorted samples (bin size n / 16, the
  *            n % 16 largest in no bin), centroid = bin mean;

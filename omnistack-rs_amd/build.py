@@ -24,7 +24,7 @@ OUT_DIR = os.path.join(HERE, "omnistack_rs", "_native")
 LIB = os.path.join(OUT_DIR, "libomnistack_amd.so")
 
 ARCH = os.environ.get("OMNI_OFFLOAD_ARCH", "gfx950")
-SOURCES = ["host_api.cpp", "codec.hip", "attn.hip", "lora.hip", "calib.hip"]
+SOURCES = ["host_api.cpp", "codec.hip", "attn.hip", "lora.hip", "calib.hip", "dense.hip"]
 
 
 def hipcc() -> str:
@@ -68,7 +68,7 @@ def compile_one(src: str) -> str:
 def build(verbose: bool = True) -> str:
     os.makedirs(OBJ_DIR, exist_ok=True)
     os.makedirs(OUT_DIR, exist_ok=True)
-    with cf.ThreadPoolExecutor(max_workers=min(5, len(SOURCES))) as ex:
+    with cf.ThreadPoolExecutor(max_workers=min(6, len(SOURCES))) as ex:
         objs = list(ex.map(compile_one, SOURCES))
     tmp = LIB + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]

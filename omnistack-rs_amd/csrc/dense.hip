@@ -1,0 +1,246 @@
+// Dense fp32 GQA attention on already dequantized K / V (gfx950).
+//
+// Reference: reference_attn (omnistack_rs/attention/reference.py:72-177),
+// the CPU path's attention: fp32 scores q . k * scale (+ an additive mask
+// broadcastable to (B, Hq, T, S)), online softmax over key tiles, fp32
+// P . V, output O / l; kv head of q head h = h / (Hq / Hkv) (repeat_kv,
+// :49-67) without materialising the repeated K / V.
+//
+// One block per (64 query rows of one (batch, kv head), kv head, batch):
+// four waves of 16 rows (row r = t * G + g of that kv head).  Keys go
+// through LDS in tiles of 32; scores and P . V run on
+// v_mfma_f32_16x16x4_f32 (fp32 products, fp32 accumulation), the softmax in
+// fp32 with expf.  The running-max update is the reference's, made safe for
+// tiles whose scores are all -inf (alpha and p are 0 there instead of
+// exp(-inf - -inf)); the reference's own result for a row whose whole first
+// tile of `first_tile` keys is masked (NaN) is reproduced explicitly, and a
+// NaN score makes its row NaN as torch.maximum / amax propagate it.
+#include <math.h>
+
+#include "omni_common.h"
+
+namespace omni {
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+struct DenseArgs {
+    const float *q, *k, *v, *mask;
+    float *out;
+    int64_t ms_b, ms_h, ms_t, ms_s;   // mask strides in elements (0: broadcast)
+    int64_t T, S, rows, first_tile;
+    int Hq, Hkv, G;
+    float scale;
+};
+
+constexpr int kDnKeys = 32;
+constexpr int kDnWaves = 4;
+constexpr int kDnRows = 16 * kDnWaves;
+constexpr int kDnPStride = kDnKeys + 4;
+
+__device__ __forceinline__ float dn_max16(float v) {
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) v = fmaxf(v, __shfl_xor(v, m));
+    return v;
+}
+__device__ __forceinline__ float dn_sum16(float v) {
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) v += __shfl_xor(v, m);
+    return v;
+}
+
+template <int D>
+__global__ __launch_bounds__(64 * kDnWaves) void dense_attn_kernel(DenseArgs a) {
+    constexpr int DP = D + 4;                     // padded LDS row (floats)
+    __shared__ __attribute__((aligned(16))) float ks[kDnKeys * DP];
+    __shared__ __attribute__((aligned(16))) float vs[kDnKeys * DP];
+    __shared__ float ps[kDnWaves][16 * kDnPStride];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = lane & 15, g = lane >> 4;
+    const int hk = blockIdx.y;
+    const int64_t b = blockIdx.z;
+    const int64_t row0 = (int64_t)blockIdx.x * kDnRows + 16 * wave;
+
+    // A operands of the scores: q row (row0 + n), dims 4 s + g
+    float qa[D / 4];
+    {
+        const int64_t r = row0 + n;
+        const bool ok = r < a.rows;
+        const int64_t t = ok ? r / a.G : 0;
+        const int hq = hk * a.G + (ok ? (int)(r % a.G) : 0);
+        const float *qrow = a.q + ((b * a.Hq + hq) * a.T + t) * D;
+#pragma unroll
+        for (int s = 0; s < D / 4; ++s) qa[s] = ok ? qrow[4 * s + g] : 0.0f;
+    }
+    // this lane's output rows row0 + 4 g + i
+    bool rok[4];
+    int64_t rt[4];
+    int rh[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int64_t r = row0 + 4 * g + i;
+        rok[i] = r < a.rows;
+        rt[i] = rok[i] ? r / a.G : 0;
+        rh[i] = hk * a.G + (rok[i] ? (int)(r % a.G) : 0);
+    }
+
+    f32x4_t o[D / 16];
+#pragma unroll
+    for (int j = 0; j < D / 16; ++j) o[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    float m[4], l[4];
+    bool seen0[4], nan_row[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        m[i] = -INFINITY;
+        l[i] = 0.0f;
+        seen0[i] = false;
+        nan_row[i] = false;
+    }
+    const float *kb0 = a.k + ((int64_t)b * a.Hkv + hk) * a.S * D;
+    const float *vb0 = a.v + ((int64_t)b * a.Hkv + hk) * a.S * D;
+    // waves whose 16 rows are all past the end only help stage K / V
+    const bool active = row0 < a.rows;
+
+    // the next tile's K / V sit in registers while the current one is used
+    constexpr int kPer = kDnKeys * D / (4 * 64 * kDnWaves);   // float4 per thread per tile
+    float4 nk[kPer], nv[kPer];
+    auto fetch = [&](int64_t s0) {
+#pragma unroll
+        for (int c = 0; c < kPer; ++c) {
+            const int e = 4 * (tid + c * 64 * kDnWaves);
+            const int key = e / D, d = e - key * D;
+            nk[c] = nv[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (s0 + key < a.S) {
+                nk[c] = *reinterpret_cast<const float4 *>(kb0 + (s0 + key) * D + d);
+                nv[c] = *reinterpret_cast<const float4 *>(vb0 + (s0 + key) * D + d);
+            }
+        }
+    };
+    fetch(0);
+
+    for (int64_t s0 = 0; s0 < a.S; s0 += kDnKeys) {
+        __syncthreads();                          // the previous tile is consumed
+#pragma unroll
+        for (int c = 0; c < kPer; ++c) {
+            const int e = 4 * (tid + c * 64 * kDnWaves);
+            const int key = e / D, d = e - key * D;
+            *reinterpret_cast<float4 *>(ks + key * DP + d) = nk[c];
+            *reinterpret_cast<float4 *>(vs + key * DP + d) = nv[c];
+        }
+        __syncthreads();
+        if (s0 + kDnKeys < a.S) fetch(s0 + kDnKeys);
+        if (!active) continue;
+
+        // scores: key block kb holds keys s0 + 16 kb + n
+        f32x4_t acc[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            acc[kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < D / 4; ++s)
+                acc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[s], ks[(16 * kb + n) * DP + 4 * s + g], acc[kb],
+                                                               0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float sc[2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const int64_t key = s0 + 16 * kb + n;
+                float v = acc[kb][i] * a.scale;
+                if (key < a.S) {
+                    if (a.mask != nullptr && rok[i])
+                        v += a.mask[b * a.ms_b + rh[i] * a.ms_h + rt[i] * a.ms_t + key * a.ms_s];
+                } else {
+                    v = -INFINITY;
+                }
+                sc[kb] = v;
+            }
+            // NaN scores poison the row (torch.maximum / amax propagate NaN)
+            const float isn = (sc[0] != sc[0] || sc[1] != sc[1]) ? 1.0f : 0.0f;
+            nan_row[i] = nan_row[i] || dn_max16(isn) > 0.0f;
+            // any finite score among the reference's first tile of keys
+            float f0 = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+                if (s0 + 16 * kb + n < a.first_tile) f0 = fmaxf(f0, sc[kb]);
+            seen0[i] = seen0[i] || dn_max16(f0) > -INFINITY;
+
+            const float mt = dn_max16(fmaxf(sc[0], sc[1]));
+            const float m_new = fmaxf(m[i], mt);
+            const float alpha = (m[i] == -INFINITY) ? 0.0f : expf(m[i] - m_new);
+            float p[2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) p[kb] = (m_new == -INFINITY) ? 0.0f : expf(sc[kb] - m_new);
+            const float psum = dn_sum16(p[0] + p[1]);
+            l[i] = alpha * l[i] + psum;           // two roundings, as the reference
+#pragma unroll
+            for (int j = 0; j < D / 16; ++j) o[j][i] *= alpha;
+            m[i] = m_new;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) ps[wave][(4 * g + i) * kDnPStride + 16 * kb + n] = p[kb];
+        }
+        // P goes through this wave's own LDS rows: program order suffices
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float pa[kDnKeys / 4];
+#pragma unroll
+        for (int s = 0; s < kDnKeys / 4; ++s) pa[s] = ps[wave][n * kDnPStride + 4 * s + g];
+#pragma unroll
+        for (int j = 0; j < D / 16; ++j)
+#pragma unroll
+            for (int s = 0; s < kDnKeys / 4; ++s)
+                o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[s], vs[(4 * s + g) * DP + 16 * j + n], o[j], 0, 0, 0);
+    }
+
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (!rok[i]) continue;
+        float *orow = a.out + ((b * a.Hq + rh[i]) * a.T + rt[i]) * D;
+        const bool nan_out = nan_row[i] || !seen0[i];
+#pragma unroll
+        for (int j = 0; j < D / 16; ++j) orow[16 * j + n] = nan_out ? __builtin_nanf("") : o[j][i] / l[i];
+    }
+}
+
+}  // namespace omni
+
+using namespace omni;
+
+extern "C" int omni_dense_attn(const float *q, const float *k, const float *v, const float *mask,
+                               const int64_t *mask_strides, int64_t B, int Hq, int Hkv, int64_t T, int64_t S,
+                               int head_dim, float scale, int64_t first_tile, float *out, void *stream) {
+    OMNI_CHECK_ARG(head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256,
+                   "omni_dense_attn: head_dim must be 32, 64, 128 or 256, got %d", head_dim);
+    OMNI_CHECK_ARG(B >= 0 && Hq > 0 && Hkv > 0 && T >= 0 && S >= 0 && Hq % Hkv == 0,
+                   "omni_dense_attn: bad shape");
+    OMNI_CHECK_ARG(first_tile >= 1, "omni_dense_attn: first_tile must be >= 1");
+    if (B == 0 || T == 0) return OMNI_OK;
+    OMNI_CHECK_ARG(q && k && v && out, "omni_dense_attn: NULL pointer");
+    OMNI_CHECK_ARG(mask == nullptr || mask_strides != nullptr, "omni_dense_attn: mask without strides");
+    OMNI_CHECK_ARG(B <= 65535 && Hkv <= 65535, "omni_dense_attn: grid too large");
+    const int G = Hq / Hkv;
+    const int64_t rows = T * G;
+    const int64_t chunks = (rows + kDnRows - 1) / kDnRows;
+    OMNI_CHECK_ARG(chunks <= 2147483647, "omni_dense_attn: too many query rows");
+    DenseArgs a;
+    a.q = q; a.k = k; a.v = v; a.mask = mask; a.out = out;
+    a.ms_b = mask ? mask_strides[0] : 0;
+    a.ms_h = mask ? mask_strides[1] : 0;
+    a.ms_t = mask ? mask_strides[2] : 0;
+    a.ms_s = mask ? mask_strides[3] : 0;
+    a.T = T; a.S = S; a.rows = rows; a.first_tile = first_tile < S ? first_tile : S;
+    a.Hq = Hq; a.Hkv = Hkv; a.G = G;
+    a.scale = scale;
+    if (S == 0) a.first_tile = 0;   // no keys: every row is NaN (0 / 0), as the reference
+    const dim3 grid((unsigned)chunks, (unsigned)Hkv, (unsigned)B), block(64 * kDnWaves);
+    hipStream_t st = as_stream(stream);
+    switch (head_dim) {
+        case 32: hipLaunchKernelGGL(dense_attn_kernel<32>, grid, block, 0, st, a); break;
+        case 64: hipLaunchKernelGGL(dense_attn_kernel<64>, grid, block, 0, st, a); break;
+        case 128: hipLaunchKernelGGL(dense_attn_kernel<128>, grid, block, 0, st, a); break;
+        default: hipLaunchKernelGGL(dense_attn_kernel<256>, grid, block, 0, st, a); break;
+    }
+    OMNI_CHECK_LAUNCH("omni_dense_attn");
+    return OMNI_OK;
+}

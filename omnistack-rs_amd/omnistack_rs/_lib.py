@@ -47,6 +47,8 @@ SIGNATURES = {
     "omni_lloyd_max_workspace_size": (_c_sz, [_c_int, _c_i64, _c_i64]),
     "omni_lloyd_max": (_c_int, [_vp, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_f32,
                                 _vp, _vp, _vp, _c_sz, _vp]),
+    "omni_dense_attn": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_int, _c_int, _c_i64, _c_i64, _c_int,
+                                 _c_f32, _c_i64, _vp, _vp]),
     "omni_attn_serve": (_c_int, [_vp, _c_int, _vp, _c_i64,
                                  _vp, _vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_f32,
                                  _vp, _vp, _vp, _vp, _vp, _c_int, _vp,

@@ -1,10 +1,12 @@
-"""Dense GQA attention utilities kept for API compatibility.
+"""Dense GQA attention on already dequantized tensors.
 
 API of the reference module omnistack_rs/attention/reference.py:
 ``repeat_kv`` (:49-67), ``reference_attn`` (:72-177), ``_lora_delta``
-(:182-200), ``ReferenceAttention`` (:205-327).  These operate on dense
-(already dequantized) tensors with torch on the tensors' device; they are
-not part of the packed-cache path (``kernels.fused_attention.omni_attn``).
+(:182-200), ``ReferenceAttention`` (:205-327).  ``reference_attn`` runs
+``omni_dense_attn`` (csrc/dense.hip: fp32 scores and P . V on MFMA, fp32
+online softmax, GQA without repeating K / V); inputs must live on a HIP
+device.  ``repeat_kv`` is the reference's view-and-copy.  The packed-cache
+path is ``kernels.fused_attention.omni_attn``.
 """
 from __future__ import annotations
 
@@ -28,29 +30,33 @@ def repeat_kv(x: torch.Tensor, n_groups: int) -> torch.Tensor:
 
 def reference_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: Optional[torch.Tensor] = None,
                    scale: Optional[float] = None, tile_size: int = 128) -> torch.Tensor:
-    """fp32 online-softmax GQA attention over key tiles; output in q's dtype."""
-    n_heads, n_kv = q.shape[1], k.shape[1]
-    head_dim = q.shape[-1]
+    """fp32 online-softmax GQA attention; output in q's dtype (reference.py:72-177).
+    `tile_size` keeps its one observable effect: a row whose first tile of
+    keys is fully masked is NaN."""
+    from .. import _lib
+    dev = _lib.require_device(q, k, v, mask)
+    if q.dim() != 4 or k.dim() != 4 or v.shape != k.shape:
+        raise ValueError(f"q (B, H, T, D) and k, v (B, Hkv, S, D) expected, got {tuple(q.shape)}, "
+                         f"{tuple(k.shape)}, {tuple(v.shape)}")
+    B, Hq, T, D = q.shape
+    Hkv, S = k.shape[1], k.shape[2]
+    if k.shape[0] != B or k.shape[3] != D or Hq % Hkv:
+        raise ValueError(f"q {tuple(q.shape)} and k {tuple(k.shape)} disagree")
+    if tile_size < 1:
+        raise ValueError("tile_size must be >= 1")
     if scale is None:
-        scale = 1.0 / math.sqrt(head_dim)
-    g = n_heads // n_kv
-    kf, vf, qf = repeat_kv(k, g).float(), repeat_kv(v, g).float(), q.float()
-    B, T, S = q.shape[0], q.shape[2], k.shape[2]
-    m = qf.new_full((B, n_heads, T, 1), float("-inf"))
-    l = qf.new_zeros(B, n_heads, T, 1)
-    O = qf.new_zeros(B, n_heads, T, head_dim)
-    for s0 in range(0, S, tile_size):
-        s1 = min(s0 + tile_size, S)
-        st = torch.matmul(qf, kf[:, :, s0:s1].transpose(-2, -1).contiguous()) * scale
-        if mask is not None:
-            st = st + mask[..., s0:s1].float()
-        m_new = torch.maximum(m, st.amax(dim=-1, keepdim=True))
-        a = torch.exp(m - m_new)
-        p = torch.exp(st - m_new)
-        l = a * l + p.sum(dim=-1, keepdim=True)
-        O = a * O + torch.matmul(p, vf[:, :, s0:s1])
-        m = m_new
-    return (O / l).to(q.dtype)
+        scale = 1.0 / math.sqrt(D)
+    qf, kf, vf = (t.float().contiguous() for t in (q, k, v))
+    out = torch.empty(B, Hq, T, D, dtype=torch.float32, device=dev)
+    mptr, strides = None, None
+    if mask is not None:
+        mf = torch.broadcast_to(mask.float(), (B, Hq, T, S))
+        strides = torch.tensor(mf.stride(), dtype=torch.int64)
+        mptr = mf.data_ptr()
+    _lib.check(_lib.lib().omni_dense_attn(
+        _lib.ptr(qf), _lib.ptr(kf), _lib.ptr(vf), mptr, None if strides is None else strides.data_ptr(),
+        B, Hq, Hkv, T, S, D, float(scale), int(tile_size), _lib.ptr(out), _lib.stream_of(dev)))
+    return out.to(q.dtype)
 
 
 def _lora_delta(lora_A: torch.Tensor, lora_B: torch.Tensor, alpha: float, rank: int) -> torch.Tensor:
