@@ -118,3 +118,20 @@ def test_bake_round_trip_matches_oracle(device, tmp_path):
     again = bake_kv_cache(None, path)
     assert all(torch.equal(a, b) for a, b in zip(again[:4], (nib, qjl, norms, cb))) and again[4] == stats
     assert load_bake(path)[4] == stats
+
+
+def test_calibrate_heads_16bit_and_d32_bake(device, tmp_path):
+    """bf16 samples calibrate as their fp32 values; a head_dim-32 cache bakes
+    and round-trips like the reference's format."""
+    from omnistack_rs.bake import bake_kv_cache
+    from omnistack_rs.quantization import calibrate_heads
+    x = torch.randn(2, 3, 40, 128, generator=_data.gen(440)).to(torch.bfloat16)
+    got16 = calibrate_heads(x.to(device)).cpu()
+    got32 = calibrate_heads(x.float().to(device)).cpu()
+    assert torch.equal(got16, got32)
+    kv = torch.randn(2, 2, 30, 32, generator=_data.gen(441))
+    nib, qjl, norms, cb, stats = bake_kv_cache(kv, tmp_path / "d32.pt", seed=3)
+    assert nib.shape == (2, 2, 30, 16) and qjl.shape == (2, 2, 30, 2) and cb.shape == (2, 16)
+    r_nib, _, _ = restate.quantize_heads(restate.wht(kv), cb, user_id=3)
+    assert torch.equal(nib, r_nib)
+    assert stats["seq_len"] == 30 and stats["n_kv_heads"] == 2

@@ -145,3 +145,23 @@ def test_prepared_pool_run_and_graph_replay(device):
         assert torch.equal(att.out, eager), f"replay {i} differs from the eager result"
         att.run(q, x, ids, cache_index=other)                # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_serve_prefill_rows_with_lora_and_empty_batch(device):
+    """T > 1 (prefill kernel, LoRA through the gather-apply kernel) with a
+    pool index, and an empty batch (no launch)."""
+    from omnistack_rs.kernels.fused_attention import omni_attn
+    N, B, Hq, Hkv, T, S, uid, L = 5, 3, 8, 2, 20, 96, 15, 4
+    kn, kq, kr, vn, cb = (t.to(device) for t in _pool(N, Hkv, S, seed=340, uid=uid))
+    a, bw = _data.lora_bank(L, 8, 64, Hq * 128, seed=341)
+    a, bw = a.to(torch.bfloat16).to(device), bw.to(torch.bfloat16).to(device)
+    q = _data.query((B, Hq, T, 128), seed=342).to(device)
+    x = torch.randn(B, T, 64, generator=_data.gen(343)).to(torch.bfloat16).to(device)
+    ids = _data.lora_ids(B, L).to(device)
+    idx = torch.tensor([4, -5, 2], device=device)
+    kw = dict(user_id=uid, x=x, lora_a=a, lora_b=bw, lora_indices=ids, lora_alpha=0.25, causal_offset=S - T)
+    got = omni_attn(q, kn, kq, kr, vn, cb, cache_index=idx, **kw)
+    want = omni_attn(q, kn[idx], kq[idx], kr[idx], vn[idx], cb, **kw)
+    assert torch.equal(got, want)
+    empty = omni_attn(q[:0], kn, kq, kr, vn, cb, user_id=uid, cache_index=idx[:0])
+    assert empty.shape == (0, Hq, T, 128)
