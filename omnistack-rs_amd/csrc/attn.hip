@@ -815,6 +815,11 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     float *qs = reinterpret_cast<float *>(smem + kDecQsOff);
     float *gq = qs + kDecRows * D;
 
+    // the arguments the prologue needs are requested together with the first
+    // kernel-argument loads (the compiler would otherwise fetch some after
+    // the cache-index test: one more round trip before the first cache load)
+    asm volatile("" ::"s"(a.q), "s"(a.k_nib), "s"(a.k_qjl), "s"(a.k_norms), "s"(a.v_nib), "s"(a.codebooks),
+                 "s"(a.g_bits), "s"(a.sign_flip), "s"(a.rotate_q), "s"(a.qscale), "s"(a.alpha_c), "s"(a.wht_scale));
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int split = blockIdx.x, hk = blockIdx.y;
