@@ -203,6 +203,171 @@ __global__ __launch_bounds__(64 * kDnWaves) void dense_attn_kernel(DenseArgs a) 
     }
 }
 
+// Few query rows per (batch, kv head) (decode: T * G <= 16): the NW waves
+// share one group of 16 rows and split every 16 NW-key tile (wave w takes
+// keys 16 w .. 16 w + 15), each keeping its own online-softmax state; the
+// states are merged in LDS at the end (max, then the exp-weighted sums in
+// wave order).
+#ifndef OMNI_DN_KS_WAVES
+#define OMNI_DN_KS_WAVES 8
+#endif
+constexpr int kDnKsWaves = OMNI_DN_KS_WAVES;
+
+template <int D, int NW>
+__global__ __launch_bounds__(64 * NW) void dense_attn_ks_kernel(DenseArgs a) {
+    constexpr int kDnKsKeys = 16 * NW;
+    constexpr int DP = D + 4;
+    constexpr int kTileF = kDnKsKeys * DP;
+    __shared__ __attribute__((aligned(16))) float ks[kTileF];
+    __shared__ __attribute__((aligned(16))) float vs[kTileF];
+    __shared__ float ps[NW][16 * 20];
+    __shared__ float wst[NW][16][4];             // per wave and row: m, l, seen0, nan
+    static_assert(NW * 16 * DP <= kTileF, "wave partials fit the key tile buffer");
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = lane & 15, g = lane >> 4;
+    const int hk = blockIdx.y;
+    const int64_t b = blockIdx.z;
+    const int64_t row0 = (int64_t)blockIdx.x * 16;
+
+    float qa[D / 4];
+    {
+        const int64_t r = row0 + n;
+        const bool ok = r < a.rows;
+        const int64_t t = ok ? r / a.G : 0;
+        const int hq = hk * a.G + (ok ? (int)(r % a.G) : 0);
+        const float *qrow = a.q + ((b * a.Hq + hq) * a.T + t) * D;
+#pragma unroll
+        for (int s = 0; s < D / 4; ++s) qa[s] = ok ? qrow[4 * s + g] : 0.0f;
+    }
+    bool rok[4];
+    int64_t rt[4];
+    int rh[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int64_t r = row0 + 4 * g + i;
+        rok[i] = r < a.rows;
+        rt[i] = rok[i] ? r / a.G : 0;
+        rh[i] = hk * a.G + (rok[i] ? (int)(r % a.G) : 0);
+    }
+    f32x4_t o[D / 16];
+#pragma unroll
+    for (int j = 0; j < D / 16; ++j) o[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    float m[4], l[4];
+    bool seen0[4], nan_row[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        m[i] = -INFINITY;
+        l[i] = 0.0f;
+        seen0[i] = false;
+        nan_row[i] = false;
+    }
+    const float *kb0 = a.k + ((int64_t)b * a.Hkv + hk) * a.S * D;
+    const float *vb0 = a.v + ((int64_t)b * a.Hkv + hk) * a.S * D;
+    constexpr int kPer = kDnKsKeys * D / (4 * 64 * NW);
+    float4 nk[kPer], nv[kPer];
+    auto fetch = [&](int64_t s0) {
+#pragma unroll
+        for (int c = 0; c < kPer; ++c) {
+            const int e = 4 * (tid + c * 64 * NW);
+            const int key = e / D, d = e - key * D;
+            nk[c] = nv[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (s0 + key < a.S) {
+                nk[c] = *reinterpret_cast<const float4 *>(kb0 + (s0 + key) * D + d);
+                nv[c] = *reinterpret_cast<const float4 *>(vb0 + (s0 + key) * D + d);
+            }
+        }
+    };
+    fetch(0);
+    for (int64_t s0 = 0; s0 < a.S; s0 += kDnKsKeys) {
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < kPer; ++c) {
+            const int e = 4 * (tid + c * 64 * NW);
+            const int key = e / D, d = e - key * D;
+            *reinterpret_cast<float4 *>(ks + key * DP + d) = nk[c];
+            *reinterpret_cast<float4 *>(vs + key * DP + d) = nv[c];
+        }
+        __syncthreads();
+        if (s0 + kDnKsKeys < a.S) fetch(s0 + kDnKsKeys);
+        const int kbase = 16 * wave;                 // this wave's keys in the tile
+        f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < D / 4; ++s)
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[s], ks[(kbase + n) * DP + 4 * s + g], acc, 0, 0, 0);
+        const int64_t key = s0 + kbase + n;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float v = acc[i] * a.scale;
+            if (key < a.S) {
+                if (a.mask != nullptr && rok[i]) v += a.mask[b * a.ms_b + rh[i] * a.ms_h + rt[i] * a.ms_t + key * a.ms_s];
+            } else {
+                v = -INFINITY;
+            }
+            nan_row[i] = nan_row[i] || dn_max16(v != v ? 1.0f : 0.0f) > 0.0f;
+            seen0[i] = seen0[i] || dn_max16(key < a.first_tile ? v : -INFINITY) > -INFINITY;
+            const float mt = dn_max16(v);
+            const float m_new = fmaxf(m[i], mt);
+            const float alpha = (m[i] == -INFINITY) ? 0.0f : expf(m[i] - m_new);
+            const float p = (m_new == -INFINITY) ? 0.0f : expf(v - m_new);
+            l[i] = alpha * l[i] + dn_sum16(p);
+#pragma unroll
+            for (int j = 0; j < D / 16; ++j) o[j][i] *= alpha;
+            m[i] = m_new;
+            ps[wave][(4 * g + i) * 20 + n] = p;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float pa[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) pa[s] = ps[wave][n * 20 + 4 * s + g];
+#pragma unroll
+        for (int j = 0; j < D / 16; ++j)
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+                o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[s], vs[(kbase + 4 * s + g) * DP + 16 * j + n], o[j], 0, 0, 0);
+    }
+
+    // merge the four waves' states
+    __syncthreads();                                  // tiles are dead: reuse them for the partials
+    float *op = ks;                                   // [wave][row][DP]
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < D / 16; ++j) op[(wave * 16 + 4 * g + i) * DP + 16 * j + n] = o[j][i];
+        if (n == 0) {
+            wst[wave][4 * g + i][0] = m[i];
+            wst[wave][4 * g + i][1] = l[i];
+            wst[wave][4 * g + i][2] = seen0[i] ? 1.0f : 0.0f;
+            wst[wave][4 * g + i][3] = nan_row[i] ? 1.0f : 0.0f;
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e < 16 * D; e += 64 * NW) {
+        const int r = e / D, d = e - r * D;
+        const int64_t row = row0 + r;
+        if (row >= a.rows) continue;
+        float mx = -INFINITY;
+        bool s0seen = false, isnan_row = false;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            mx = fmaxf(mx, wst[w][r][0]);
+            s0seen = s0seen || wst[w][r][2] != 0.0f;
+            isnan_row = isnan_row || wst[w][r][3] != 0.0f;
+        }
+        float lsum = 0.0f, osum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const float f = (wst[w][r][0] == -INFINITY) ? 0.0f : expf(wst[w][r][0] - mx);
+            lsum += f * wst[w][r][1];
+            osum += f * op[(w * 16 + r) * DP + d];
+        }
+        const int64_t t = row / a.G;
+        const int hq = hk * a.G + (int)(row % a.G);
+        a.out[((b * a.Hq + hq) * a.T + t) * D + d] = (isnan_row || !s0seen) ? __builtin_nanf("") : osum / lsum;
+    }
+}
+
 }  // namespace omni
 
 using namespace omni;
@@ -233,8 +398,17 @@ extern "C" int omni_dense_attn(const float *q, const float *k, const float *v, c
     a.Hq = Hq; a.Hkv = Hkv; a.G = G;
     a.scale = scale;
     if (S == 0) a.first_tile = 0;   // no keys: every row is NaN (0 / 0), as the reference
-    const dim3 grid((unsigned)chunks, (unsigned)Hkv, (unsigned)B), block(64 * kDnWaves);
     hipStream_t st = as_stream(stream);
+    if (rows <= 16 && head_dim <= 128) {
+        // few rows: the waves split the keys instead of the rows
+        const dim3 grid(1u, (unsigned)Hkv, (unsigned)B), block(64 * kDnKsWaves);
+        if (head_dim == 32) hipLaunchKernelGGL((dense_attn_ks_kernel<32, kDnKsWaves>), grid, block, 0, st, a);
+        else if (head_dim == 64) hipLaunchKernelGGL((dense_attn_ks_kernel<64, kDnKsWaves>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((dense_attn_ks_kernel<128, kDnKsWaves>), grid, block, 0, st, a);
+        OMNI_CHECK_LAUNCH("omni_dense_attn");
+        return OMNI_OK;
+    }
+    const dim3 grid((unsigned)chunks, (unsigned)Hkv, (unsigned)B), block(64 * kDnWaves);
     switch (head_dim) {
         case 32: hipLaunchKernelGGL(dense_attn_kernel<32>, grid, block, 0, st, a); break;
         case 64: hipLaunchKernelGGL(dense_attn_kernel<64>, grid, block, 0, st, a); break;

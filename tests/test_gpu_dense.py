@@ -31,7 +31,7 @@ def _close(got, want, tag):
 
 @pytest.mark.parametrize("B,Hq,Hkv,T,S,D", [
     (2, 8, 2, 5, 300, 128), (1, 4, 4, 1, 33, 128), (2, 32, 8, 3, 100, 64), (1, 6, 3, 70, 40, 32),
-    (1, 2, 1, 2, 129, 256), (3, 4, 2, 1, 1, 128),
+    (1, 2, 1, 2, 129, 256), (3, 4, 2, 1, 1, 128), (2, 16, 2, 2, 200, 32), (1, 8, 1, 2, 77, 128),
 ])
 def test_dense_attn_matches_oracle(device, B, Hq, Hkv, T, S, D):
     from omnistack_rs.attention import reference_attn
@@ -62,13 +62,14 @@ def test_dense_attn_masks_scale_and_dtype(device):
            restate.reference_attn(q.float(), k, v, mask=bias), "bias (B,1,T,S)")
 
 
-@pytest.mark.parametrize("tile_size", [16, 128])
-def test_dense_attn_nan_rules_follow_the_reference(device, tile_size):
+@pytest.mark.parametrize("tile_size,T", [(16, 4), (128, 4), (16, 12), (128, 12)])
+def test_dense_attn_nan_rules_follow_the_reference(device, tile_size, T):
     """A row whose first tile of keys is all -inf is NaN in the reference's
     loop (exp(-inf - -inf)); later fully masked tiles are harmless; a NaN
-    key poisons its rows."""
+    key poisons its rows.  T=4 (8 rows per kv head) runs the key-split
+    launch, T=12 (24 rows) the row-split one."""
     from omnistack_rs.attention import reference_attn
-    B, Hq, Hkv, T, S, D = 1, 4, 2, 4, 200, 64
+    B, Hq, Hkv, S, D = 1, 4, 2, 200, 64
     g = _data.gen(520)
     q = torch.randn(B, Hq, T, D, generator=g)
     k = torch.randn(B, Hkv, S, D, generator=g)
