@@ -523,9 +523,15 @@ constexpr int kSlutOff = kLutBytes;
 constexpr int kSlutBytes = 16 * 256;
 static_assert((kSlutOff & (kSlutOff - 1)) == 0 && kSlutOff >= kSlutBytes, "sign LUT address is formed with an OR");
 constexpr int kDecQsOff = kSlutOff + kSlutBytes;
-constexpr int kDecBkOff = kDecQsOff + kDecRows * (128 + 64) * 4;   // [row][quad][hi, lo] 16 B
+constexpr int kDecGqStride = 64 + 2;   // G q rows: the pad spreads the rows of one read over the banks
+constexpr int kDecBkOff = kDecQsOff + kDecRows * (128 + kDecGqStride) * 4;   // [row][quad][hi, lo] 16 B
 constexpr int kDecGaOff = kDecBkOff + kDecRows * 32 * 2 * 16;        // [row][8-dim group][hi, lo] 16 B
 constexpr int kDecCscOff = kDecGaOff + kDecRows * 16 * 2 * 16;      // per row: scale * log2(e) / 2^k
+// 16-byte chunk c of a row's operand image is stored at c ^ 2 (row % 8): the
+// eight rows read by one instruction then fall in different bank groups
+// (unswizzled, every row starts on the same bank and one read serializes
+// ~32 ways)
+__device__ __forceinline__ int dec_chunk(int row, int c) { return c ^ (2 * (row & 7)); }
 constexpr int kDecCntOff = kDecCscOff + kDecRows * 4;                // next unclaimed tile of the block
 constexpr int kDecLdsBytes = kDecCntOff + 16;
 // epilogue reuse of [0, 68K): per-wave O slabs (rows padded to 132 floats),
@@ -986,7 +992,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
             float l[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) l[j] = h[j] - f16_to_f32(f32_to_f16_rne(h[j]));
-            uint4 *dst = reinterpret_cast<uint4 *>(smem + kDecBkOff + (wave * 32 + lane) * 32);
+            uint4 *dst = reinterpret_cast<uint4 *>(smem + kDecBkOff + dec_chunk(wave, (wave * 32 + lane) * 2) * 16);
             dst[0] = make_uint4(pack_h2(h[0], h[1]), pack_h2(h[0], h[1]), pack_h2(h[2], h[3]), pack_h2(h[2], h[3]));
             dst[1] = make_uint4(pack_h2(l[0], l[1]), 0u, pack_h2(l[2], l[3]), 0u);
         } else if (QJL && lane < 48) {
@@ -1001,7 +1007,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
                 lw[k] = pack_h2(x[2 * k] - f16_to_f32(f32_to_f16_rne(x[2 * k])),
                                 x[2 * k + 1] - f16_to_f32(f32_to_f16_rne(x[2 * k + 1])));
             }
-            uint4 *dst = reinterpret_cast<uint4 *>(smem + kDecGaOff + (wave * 16 + j) * 32);
+            uint4 *dst = reinterpret_cast<uint4 *>(smem + kDecGaOff + dec_chunk(wave, (wave * 16 + j) * 2) * 16);
             dst[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
             dst[1] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
         }
@@ -1019,7 +1025,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
         for (int s = 0; s < 4; ++s) {
             uint4 hv = make_uint4(0u, 0u, 0u, 0u), lv = hv;
             if (n < kDecRows) {
-                const uint4 *src = reinterpret_cast<const uint4 *>(smem + kDecGaOff + (n * 16 + 4 * s + g) * 32);
+                const uint4 *src = reinterpret_cast<const uint4 *>(smem + kDecGaOff + dec_chunk(n, (n * 16 + 4 * s + g) * 2) * 16);
                 hv = src[0];
                 lv = src[1];
             }
@@ -1038,7 +1044,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            if (4 * g + i < kDecRows) gq[(4 * g + i) * QD + o] = acc[i];
+            if (4 * g + i < kDecRows) gq[(4 * g + i) * kDecGqStride + o] = acc[i];
     }
     __syncthreads();
 
@@ -1049,7 +1055,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
         // quad 8g + s of row rn: columns 0-7 take the hi image, 8-15 the lo image
-        const uint4 v = *reinterpret_cast<const uint4 *>(smem + kDecBkOff + ((rn * 32 + 8 * g + s) * 2 + (lo_col ? 1 : 0)) * 16);
+        const uint4 v = *reinterpret_cast<const uint4 *>(smem + kDecBkOff + (dec_chunk(rn, (rn * 32 + 8 * g + s) * 2) + (lo_col ? 1 : 0)) * 16);
         bk[s] = as_half8(v.x, v.y, v.z, v.w);
     }
     // QJL B operand carries sqrt(2/pi) / D on G (2^k q) (fp16 in columns
@@ -1062,7 +1068,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
         uint32_t w[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const float *row = gq + rn * QD + 32 * s + 8 * g + 2 * j;
+            const float *row = gq + rn * kDecGqStride + 32 * s + 8 * g + 2 * j;
             float g0 = row[0] * gscale, g1 = row[1] * gscale;
             if (lo_col) {
                 g0 -= (float)(_Float16)g0;
