@@ -720,9 +720,10 @@ __device__ __forceinline__ void wht128_lanes(float &lo, float &hi, int lane) {
 // of lora_kernel (per-lane fma over hidden = lane, lane + 64, ...; xor-tree
 // wave sum; sequential fma over the rank), so the fused and the separate
 // paths round q_eff identically.  id < 0: unchanged; id >= n: NaN.
-// The fused path takes 16-bit adapters with rank <= 16 and hidden <= 256
-// (the host sends others to the gather-apply kernel); every load is a
-// branch-free 16-bit buffer load whose range ends at the row it serves.
+// The fused path takes 16-bit adapters of rank 8 or 16 and hidden <= 256
+// with a 16-byte aligned B bank (the host sends others to the gather-apply
+// kernel); every load is a branch-free buffer load whose range ends at the
+// row it serves, B rows as 16-byte loads of eight rank components.
 __device__ __forceinline__ float lora_wave_sum(float v) {
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
@@ -773,8 +774,20 @@ __device__ __forceinline__ void lora_row(float &lo, float &hi, const AttnArgs &a
 #pragma unroll
             for (int kh = 0; kh < 4; ++kh)
                 aw[jj][kh] = __builtin_amdgcn_raw_buffer_load_b16(AR, 2u * (j * hidden + 64 * kh + lane), 0, 0);
-            bl[jj] = __builtin_amdgcn_raw_buffer_load_b16(BR, 2u * (lane * rank + j), 0, 0);
-            bh[jj] = __builtin_amdgcn_raw_buffer_load_b16(BR, 2u * ((64 + lane) * rank + j), 0, 0);
+        }
+        {
+            // B rows lane and 64 + lane, components j0 .. j0 + 7: one 16-byte
+            // load each (rank % 8 == 0 and a 16-byte aligned bank)
+            const u32x4_t l4 = __builtin_amdgcn_raw_buffer_load_b128(BR, 2u * (lane * rank + j0), 0, 0);
+            const u32x4_t h4 = __builtin_amdgcn_raw_buffer_load_b128(BR, 2u * ((64 + lane) * rank + j0), 0, 0);
+            const uint32_t lw[4] = {l4.x, l4.y, l4.z, l4.w}, hw[4] = {h4.x, h4.y, h4.z, h4.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                bl[2 * k] = lw[k] & 0xffffu;
+                bl[2 * k + 1] = lw[k] >> 16;
+                bh[2 * k] = hw[k] & 0xffffu;
+                bh[2 * k + 1] = hw[k] >> 16;
+            }
         }
         float dr[8];
 #pragma unroll
@@ -1794,7 +1807,8 @@ static int attn_run(const void *q, int q_dtype, const uint8_t *k_nib, const uint
     // LoRA: fused into the D=128 decode prologue; other kernels read q_eff
     // written by the gather-apply kernel into the workspace tail
     const bool lora_fused = lora != nullptr && p.dec128 && lora->w_dtype != OMNI_F32 &&
-                            lora->rank <= kLoraFusedMaxRank && lora->hidden <= kLoraFusedMaxHidden;
+                            lora->rank <= kLoraFusedMaxRank && lora->rank % 8 == 0 &&
+                            lora->hidden <= kLoraFusedMaxHidden && ((uintptr_t)lora->Bw % 16) == 0;
     const size_t q_bytes = (size_t)B * Hq * T * head_dim * (q_dtype == OMNI_F32 ? 4 : 2);
     const size_t ws_need = (lora != nullptr && !lora_fused) ? align256(p.ws_bytes) + q_bytes : p.ws_bytes;
     if (ws_need > 0 && (workspace == nullptr || workspace_bytes < ws_need)) {

@@ -224,8 +224,9 @@ def test_prepared_lora_matches_omni_attn(device):
     (70, 32, 8, 1, torch.bfloat16, torch.bfloat16, 8, 96),   # two sequences per block
     (3, 8, 2, 2, torch.float32, torch.float32, 8, 96),
     (2, 8, 2, 3, torch.float16, torch.bfloat16, 8, 96),
-    (4, 32, 8, 1, torch.bfloat16, torch.bfloat16, 13, 200),  # rank not a multiple of 4, ragged hidden
+    (4, 32, 8, 1, torch.bfloat16, torch.bfloat16, 13, 200),  # rank not a multiple of 8: gather-apply
     (4, 32, 8, 1, torch.float16, torch.float16, 16, 256),    # largest fused adapter
+    (4, 32, 8, 1, torch.bfloat16, torch.bfloat16, 16, 200),  # two fused rank groups, ragged hidden
     (4, 32, 8, 1, torch.bfloat16, torch.bfloat16, 17, 64),   # rank above the fused bound: gather-apply
     (4, 32, 8, 1, torch.bfloat16, torch.bfloat16, 4, 300),   # hidden above the fused bound: gather-apply
     (2, 16, 4, 40, torch.bfloat16, torch.bfloat16, 8, 96),   # prefill kernel: gather-apply into the workspace first
@@ -246,6 +247,25 @@ def test_fused_lora_equals_separate_gather_apply(device, B, Hq, Hkv, T, qdt, wdt
     q_eff = _apply_lora_to_q(q, x, a, bw, ids, 0.5)
     want = omni_attn(q_eff, kn, kq, kr, vn, cb, user_id=uid)
     assert torch.equal(got, want)
+
+
+def test_fused_lora_misaligned_bank(device):
+    """A B bank that is not 16-byte aligned (a view at an odd element offset)
+    takes the gather-apply path and gives the same bits as an aligned copy."""
+    from omnistack_rs.kernels.fused_attention import omni_attn
+    B, Hq, Hkv, S, uid, L, rank, hidden = 4, 32, 8, 90, 5, 6, 8, 128
+    kn, kq, kr, vn, cb = (t.to(device) for t in _cache(B, Hkv, S, seed=48, user_id=uid))
+    a, bw = _data.lora_bank(L, rank, hidden, Hq * 128, seed=49)
+    a, bw = a.to(torch.bfloat16).to(device), bw.to(torch.bfloat16).to(device)
+    buf = torch.empty(bw.numel() + 8, dtype=bw.dtype, device=device)
+    bw_odd = buf[1:1 + bw.numel()].view(bw.shape)
+    bw_odd.copy_(bw)
+    assert bw_odd.data_ptr() % 16 != 0
+    q = _data.query((B, Hq, 1, 128), seed=50).to(device)
+    x = torch.randn(B, 1, hidden, generator=_data.gen(51)).to(torch.bfloat16).to(device)
+    ids = _data.lora_ids(B, L).to(device)
+    kw = dict(user_id=uid, x=x, lora_a=a, lora_indices=ids, lora_alpha=0.5)
+    assert torch.equal(omni_attn(q, kn, kq, kr, vn, cb, lora_b=bw_odd, **kw), omni_attn(q, kn, kq, kr, vn, cb, lora_b=bw, **kw))
 
 
 def test_prepared_run_replays_in_hip_graph(device):
