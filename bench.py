@@ -250,6 +250,26 @@ def main() -> int:
         log(f"[bench] C3: {t_step * 1e6:.1f} us/step (eager), {t_graph * 1e6:.1f} us/step (graph), "
             f"{ev_mean * 1e6:.1f} us/call (events) -> {value:.0f} GB/s ({value / HBM_PEAK_GBS:.1%} of peak)")
 
+        # Plain streaming-read kernel over as many bytes as one C3 call, timed
+        # the same ways: the read rate this device reaches without any decode
+        # work, for comparison with `value`.
+        from omnistack_rs import _lib
+        rbuf = torch.empty(-(-bytes_step // 16) * 4, dtype=torch.int32, device=dev)
+        rpart = torch.empty(8 * props.multi_processor_count, dtype=torch.int32, device=dev)
+        rbytes = rbuf.numel() * 4
+        read = lambda: _lib.hbm_read_probe(rbuf, rpart)
+        t_read = wall_eager(read, args.steps, args.warmup)
+        read_ev = statistics.fmean(per_call_events(read, args.steps, 2, stream))
+        read_gbs = rbytes / t_read / 1e9
+        log(f"[bench] read probe: {t_read * 1e6:.1f} us/call (eager), {read_ev * 1e6:.1f} us/call (events) "
+            f"-> {read_gbs:.0f} GB/s over {rbytes} B; C3 runs at {value / read_gbs:.1%} of it")
+        result["hbm_read_probe"] = {
+            "GB_s": round(read_gbs, 1), "GB_s_events": round(rbytes / read_ev / 1e9, 1), "bytes": rbytes,
+            "us_per_call": round(t_read * 1e6, 2), "c3_frac_of_probe": round(value / read_gbs, 4),
+            "note": "omni_hbm_read_probe: plain streaming read (16-byte loads, 8 in flight per thread, "
+                    f"{rpart.numel()} blocks) of C3's byte count, K back-to-back calls like C3"}
+        del rbuf, rpart
+
         c3_traffic = round(1024 * (C3_TRAFFIC["fetch_kib"] * C3_TRAFFIC["fetch_scale"]
                                     + C3_TRAFFIC["write_kib"] * C3_TRAFFIC["write_scale"]))
         result.update({

@@ -254,6 +254,16 @@ int omni_attn_serve(const void *q, int q_dtype, const int64_t *cache_index, int6
                     int rotate_q, const int8_t *sign_flip,
                     float *out, void *workspace, size_t workspace_bytes, void *stream);
 
+/*
+ * Measurement helper with no counterpart in the reference: streams `bytes`
+ * (a multiple of 16, 16-byte aligned device buffer) once with n_partials
+ * blocks and writes one XOR fold per block to partials[0 .. n_partials),
+ * so the XOR of the partials is the XOR of every 32-bit word of `buf`.
+ * Its rate is the plain-kernel HBM read bandwidth that the decode
+ * kernel's rate is compared with.
+ */
+int omni_hbm_read_probe(const void *buf, size_t bytes, uint32_t *partials, int n_partials, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

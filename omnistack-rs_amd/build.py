@@ -24,7 +24,7 @@ OUT_DIR = os.path.join(HERE, "omnistack_rs", "_native")
 LIB = os.path.join(OUT_DIR, "libomnistack_amd.so")
 
 ARCH = os.environ.get("OMNI_OFFLOAD_ARCH", "gfx950")
-SOURCES = ["host_api.cpp", "codec.hip", "attn.hip", "lora.hip", "calib.hip", "dense.hip"]
+SOURCES = ["host_api.cpp", "codec.hip", "attn.hip", "lora.hip", "calib.hip", "dense.hip", "probe.hip"]
 
 
 def hipcc() -> str:

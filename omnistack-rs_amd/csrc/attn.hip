@@ -567,9 +567,27 @@ __device__ __forceinline__ float dpp_quad_bcast(float v, int i) {
 __device__ __forceinline__ float dpp_row_shl8(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x108, 0xf, 0xf, false));
 }
-// lane i of each 16-lane row reads lane i ^ 8 (rotate by 8)
+// lane i of each 16-lane row reads lane i ^ 8 (rotate by 8).  A row rotate
+// reads a valid lane for every lane, so no prior value of the destination is
+// kept (no move to initialise it).
 __device__ __forceinline__ uint32_t dpp_row_ror8(uint32_t v) {
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xf, 0xf, false);
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xf, 0xf, true);
+}
+
+// max(a, b) and max(a, b, c) as single instructions.  fmaxf on values the
+// compiler cannot prove canonical (lane moves, selects) first quiets each
+// operand with an extra v_max; no signalling NaN reaches these call sites
+// (every operand is an arithmetic result or a lane move of one), where the
+// plain instruction already returns fmaxf's result.
+__device__ __forceinline__ float vmax2(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
 }
 
 // LDS byte offset of the LUT entry for byte k of w: (byte << 8) | copy offset.
@@ -653,9 +671,9 @@ __device__ __forceinline__ uint32_t cvt_pk_h2(float x, float y) {
 // max over lanes {l, l^16, l^32, l^48} without LDS (v_permlane16/32_swap).
 __device__ __forceinline__ float max_over_groups(float m) {
     auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
-    m = fmaxf(__uint_as_float(t[0]), __uint_as_float(t[1]));
+    m = vmax2(__uint_as_float(t[0]), __uint_as_float(t[1]));
     auto u = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
-    return fmaxf(__uint_as_float(u[0]), __uint_as_float(u[1]));
+    return vmax2(__uint_as_float(u[0]), __uint_as_float(u[1]));
 }
 
 // One lane per (d, d + 64) of a 128-wide row: the normalized WHT of
@@ -925,21 +943,23 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
         (void *)(a.g_bits + (QJL ? (int64_t)hk * QD * 4 : 0)), (short)0, (QJL && wave < QD / 16) ? QD * 16 : 0, kBufWord3);
     const u32x4_t gw = __builtin_amdgcn_raw_buffer_load_b128(GB, (uint32_t)(16 * wave + n) * 16u, 0, 0);
 
-    // ── first cache tile in flight (tile `wave` of the split).  Loads are
-    //    unconditional (past the split end they read 0), so the compiler
-    //    counts outstanding loads exactly and waits only for the tile it
-    //    consumes. ──────────────────────────────────────────────────────
+    // ── both ring slots in flight (tiles `wave` and `wave + nw` of the
+    //    split) before the prologue's work, so the cache streams while the
+    //    prologue runs.  Loads are unconditional (past the split end they
+    //    read 0 and touch no memory), so the compiler counts outstanding
+    //    loads exactly and waits only for the tile it consumes. ─────────
     TileRaw ring[PF];
     // claim index i -> (sequence, token offset); i >= ntiles is past the end
     auto tile_seq = [&](int i) { return (nseq > 1 && i >= tps) ? 1 : 0; };
     auto tile_tok = [&](int i) { return s_begin + (i - tile_seq(i) * tps) * kDecTile; };
-    tile_load<QJL>(ring[0], wave >= tps ? P1 : P, OFS, tile_tok(wave));
+    tile_load<QJL>(ring[0], tile_seq(wave) ? P1 : P, OFS, tile_tok(wave));
+    tile_load<QJL>(ring[1], tile_seq(wave + nw) ? P1 : P, OFS, tile_tok(wave + nw));
 
     // ── centroid lane % 16 as an (fp16 hi, fp16 remainder) pair ────────
     const uint16_t cb_h16 = f32_to_f16_rne(cb_mine);
     const uint32_t cb_pair = (uint32_t)cb_h16 | ((uint32_t)f32_to_f16_rne(cb_mine - f16_to_f32(cb_h16)) << 16);
-    // tiles 0 .. nw - 1 are taken statically (one per wave, already in flight)
-    if (tid == 0) *reinterpret_cast<int *>(smem + kDecCntOff) = nw;
+    // tiles 0 .. 2 nw - 1 are taken statically (two per wave, already in flight)
+    if (tid == 0) *reinterpret_cast<int *>(smem + kDecCntOff) = 2 * nw;
     // ── sign table (threads 0..511) ───────────────────────────────────
     if (tid < 512) sign_table_store(smem, tid);
     if (wave >= kDecRows) {
@@ -1112,7 +1132,11 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
 #pragma unroll
     for (int k = 0; k < 8; ++k) oacc[k] = float4_t{0.f, 0.f, 0.f, 0.f};
     lacc_sum = float4_t{0.f, 0.f, 0.f, 0.f};
-    float m_run = -INFINITY;
+    // running max starts at -FLT_MAX rather than -inf, so it can serve as the
+    // exponent offset directly: a tile whose keys are all masked (-inf)
+    // still gives exp2(-inf - m) = 0, and the first finite maximum replaces
+    // it (scaling the empty accumulators by exp2(-FLT_MAX - mt) = 0)
+    float m_run = -__FLT_MAX__;
 
     // One 32-token tile: scores, online softmax, PV.
     auto tile_step = [&](TileRaw &R, const int tt, const int tseq) {
@@ -1160,7 +1184,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
 
         // online softmax (exp2 domain), lazy rescale.  Logits are rounded
         // before the max is taken, so every exponent below is <= 8 exactly.
-        float mt = fmaxf(fmaxf(fmaxf(fmaxf(sc[0], sc[1]), sc[2]), fmaxf(fmaxf(sc[3], sc[4]), sc[5])), fmaxf(sc[6], sc[7]));
+        float mt = vmax3(vmax3(sc[0], sc[1], sc[2]), vmax3(sc[3], sc[4], sc[5]), vmax2(sc[6], sc[7]));
         mt = max_over_groups(mt);
         const bool need = mt > m_run + 8.0f;
         if (__builtin_amdgcn_ballot_w64(need)) {
@@ -1170,7 +1194,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
             lacc_sum *= f;
             m_run = need ? mt : m_run;
         }
-        const float m_use = (m_run == -INFINITY) ? 0.0f : m_run;
+        const float m_use = m_run;
         // lanes n and n + 8 hold the same scores: columns 0-7 exponentiate the
         // tile's first 16 tokens, columns 8-15 the last 16, and the halves
         // trade places by a row rotation (B columns 8-15 feed output columns
@@ -1212,30 +1236,45 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     // Tiles are claimed dynamically from the block's LDS counter: the waves
     // sharing a SIMD do not progress at the same rate (the issue arbiter
     // favours the oldest), and static round-robin tiles would leave the
-    // youngest waves running alone at the end.  Each step claims the tile
-    // after next (its result is needed one step later, so the atomic's
+    // youngest waves running alone at the end.  Each loop step claims the
+    // tile after next (its result is needed one step later, so the atomic's
     // latency hides behind the LUT traffic), prefetches the next tile
     // (unconditionally: past the split end it reads 0 and touches no
-    // memory) and consumes the current one.
+    // memory) and consumes the current one.  A wave's claims increase, so
+    // the first tile past the end means every later one is past it too.
+    // The first two tiles (both slots, issued before the prologue) are
+    // consumed ahead of the loop, so only one slot is live at its head.
     static_assert(PF == 2, "the dynamic tile loop alternates two ring slots");
     int *tile_cnt = reinterpret_cast<int *>(smem + kDecCntOff);
     int i_cur = wave;
     int c_nxt = claim_tile(tile_cnt, lane);
-    for (;;) {
-        if (i_cur >= ntiles) break;
-        const int i_nxt = c_nxt;
-        c_nxt = claim_tile(tile_cnt, lane);
-        __builtin_amdgcn_sched_barrier(0);
-        tile_load<QJL>(ring[1], tile_seq(i_nxt) ? P1 : P, OFS, tile_tok(i_nxt));
-        __builtin_amdgcn_sched_barrier(0);
+    if (i_cur < ntiles) {
         tile_step(ring[0], tile_tok(i_cur), tile_seq(i_cur));
-        if (i_nxt >= ntiles) break;
-        i_cur = c_nxt;
-        c_nxt = claim_tile(tile_cnt, lane);
-        __builtin_amdgcn_sched_barrier(0);
-        tile_load<QJL>(ring[0], tile_seq(i_cur) ? P1 : P, OFS, tile_tok(i_cur));
-        __builtin_amdgcn_sched_barrier(0);
-        tile_step(ring[1], tile_tok(i_nxt), tile_seq(i_nxt));
+        const int i_pre = wave + nw;
+        if (i_pre < ntiles) {
+            i_cur = c_nxt;
+            c_nxt = claim_tile(tile_cnt, lane);
+            __builtin_amdgcn_sched_barrier(0);
+            tile_load<QJL>(ring[0], tile_seq(i_cur) ? P1 : P, OFS, tile_tok(i_cur));
+            __builtin_amdgcn_sched_barrier(0);
+            tile_step(ring[1], tile_tok(i_pre), tile_seq(i_pre));
+            for (;;) {
+                if (i_cur >= ntiles) break;
+                const int i_nxt = c_nxt;
+                c_nxt = claim_tile(tile_cnt, lane);
+                __builtin_amdgcn_sched_barrier(0);
+                tile_load<QJL>(ring[1], tile_seq(i_nxt) ? P1 : P, OFS, tile_tok(i_nxt));
+                __builtin_amdgcn_sched_barrier(0);
+                tile_step(ring[0], tile_tok(i_cur), tile_seq(i_cur));
+                if (i_nxt >= ntiles) break;
+                i_cur = c_nxt;
+                c_nxt = claim_tile(tile_cnt, lane);
+                __builtin_amdgcn_sched_barrier(0);
+                tile_load<QJL>(ring[0], tile_seq(i_cur) ? P1 : P, OFS, tile_tok(i_cur));
+                __builtin_amdgcn_sched_barrier(0);
+                tile_step(ring[1], tile_tok(i_nxt), tile_seq(i_nxt));
+            }
+        }
     }
 
     // ── combine waves (in wave order) ───────────────────────────────
@@ -1588,7 +1627,7 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
                         if (tn >= s_end || tn > lim[c]) sc[4 * u + i] = -INFINITY;
                     }
             }
-            float mt = fmaxf(fmaxf(fmaxf(fmaxf(sc[0], sc[1]), sc[2]), fmaxf(fmaxf(sc[3], sc[4]), sc[5])), fmaxf(sc[6], sc[7]));
+            float mt = vmax3(vmax3(sc[0], sc[1], sc[2]), vmax3(sc[3], sc[4], sc[5]), vmax2(sc[6], sc[7]));
             mt = max_over_groups(mt);
             const bool need = mt > m_run[c] + 8.0f;
             if (__builtin_amdgcn_ballot_w64(need)) {

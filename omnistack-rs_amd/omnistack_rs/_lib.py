@@ -54,6 +54,7 @@ SIGNATURES = {
                                  _vp, _vp, _vp, _vp, _vp, _c_int, _vp,
                                  _c_i64, _c_int, _c_int, _c_i64, _c_i64, _c_int,
                                  _c_f32, _c_int, _c_i64, _c_int, _vp, _vp, _vp, _c_sz, _vp]),
+    "omni_hbm_read_probe": (_c_int, [_vp, _c_sz, _vp, _c_int, _vp]),
 }
 
 
@@ -167,3 +168,14 @@ def sign_flip_i8(sign_flip: torch.Tensor, head_dim: int, device: torch.device) -
 def head_seeds(user_id: int, n_heads: int) -> tuple:
     """(user_id % 1024) ^ h for each kv head (quantize.py:293-295, :583)."""
     return tuple((user_id % 1024) ^ h for h in range(n_heads))
+
+
+def hbm_read_probe(buf: torch.Tensor, partials: torch.Tensor) -> None:
+    """Stream `buf` (contiguous device tensor, size a multiple of 16 bytes)
+    once, one XOR fold per block into the int32 `partials` (one block per
+    element), on the current stream: the read-bandwidth probe."""
+    require_device(buf, partials)
+    if not (buf.is_contiguous() and partials.is_contiguous() and partials.dtype == torch.int32):
+        raise ValueError("hbm_read_probe: contiguous buffer and int32 partials required")
+    nbytes = buf.numel() * buf.element_size()
+    check(lib().omni_hbm_read_probe(ptr(buf), nbytes, ptr(partials), partials.numel(), stream_of(buf.device)))

@@ -68,6 +68,9 @@ def test_validation_errors_before_any_device_work(L):
     with pytest.raises(ValueError):
         _lib.check(rc)
     assert L.omni_qjl_g_bits(1, 64, None) == _lib.OMNI_EINVAL
+    assert L.omni_hbm_read_probe(None, 24, None, 4, None) == _lib.OMNI_EINVAL
+    assert "multiple of 16" in _lib.last_error()
+    assert L.omni_hbm_read_probe(None, 0, None, 0, None) == _lib.OMNI_EINVAL
 
 
 def test_empty_shapes_are_noops(L):
