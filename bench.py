@@ -11,8 +11,10 @@ call with inputs resident in HBM (K back-to-back calls).
 
 Also reported (extra keys): C2 serving (B=64, S=50, 32q/8kv, 256-adapter
 rank-8 LoRA gather on Q) p50/p99 latency and users/s; C4 encode GB/s
-(16 x 4096 x 8 kv heads, K and V, fused rotation); the reference's CPU path
-(the oracle restatement) timed on a bounded C3 sample on this host.
+(16 x 4096 x 8 kv heads, K and V, fused rotation); a plain streaming read of
+C3's byte count (the device's achievable read rate, for comparison with
+`value`); the reference's CPU path (the oracle restatement) timed on a
+bounded C3 sample on this host.
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 5]
 Prints one JSON line on stdout; progress goes to stderr.
@@ -42,7 +44,7 @@ BYTES_PER_TOKEN_HEAD = 64 + 8 + 4 + 64     # K nibbles + K signs + K norm (f32) 
 # (FETCH_SIZE reads half the copied bytes -> x2.0; WRITE_SIZE reads them
 # exactly -> x1.0).  Recorded in profiles/attn_decode128_c3.md; re-measure
 # after any change to the decode kernel.
-C3_TRAFFIC = {"fetch_kib": 143632.9, "fetch_scale": 2.0, "write_kib": 512.0, "write_scale": 1.0}
+C3_TRAFFIC = {"fetch_kib": 143655.5, "fetch_scale": 2.0, "write_kib": 512.0, "write_scale": 1.0}
 
 
 def log(msg: str) -> None:
@@ -255,7 +257,7 @@ def main() -> int:
         # work, for comparison with `value`.
         from omnistack_rs import _lib
         rbuf = torch.empty(-(-bytes_step // 16) * 4, dtype=torch.int32, device=dev)
-        rpart = torch.empty(8 * props.multi_processor_count, dtype=torch.int32, device=dev)
+        rpart = torch.empty(props.multi_processor_count, dtype=torch.int32, device=dev)   # one block per CU reads fastest
         rbytes = rbuf.numel() * 4
         read = lambda: _lib.hbm_read_probe(rbuf, rpart)
         t_read = wall_eager(read, args.steps, args.warmup)
