@@ -1305,7 +1305,8 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
         const float rmu = (rmx == -INFINITY) ? 0.0f : rmx;
         float lsum = 0.0f, osum = 0.0f;
         for (int w = 0; w < nw; ++w) {
-            const float f = exp2f(wm[w * kDecRows + rr] - rmu);
+            // merge weights lie in [0, 1]; the hardware exp2 is within 1 ulp
+            const float f = __builtin_amdgcn_exp2f(wm[w * kDecRows + rr] - rmu);
             lsum = __builtin_fmaf(f, wl[w * kDecRows + rr], lsum);
             osum = __builtin_fmaf(f, ob[(w * kDecRows + rr) * kObStride + d], osum);
         }
