@@ -36,7 +36,7 @@ import torch
 
 from .. import _lib
 from .hadamard import HEAD_DIM
-from .quantize import QJL_DIM, dequantize_heads
+from .quantize import QJL_DIM, _check_packed, dequantize_heads
 
 BLOCK_T: int = 16     # kept for API compatibility; the HIP kernel tiles 16 tokens x 16 query rows
 BLOCK_S: int = 64
@@ -124,8 +124,9 @@ def _attn(q, k_nibbles, k_qjl, k_norms, v_nibbles, codebooks, user_id, scale, wi
     Bk, Hkv, S, nb = k_nibbles.shape
     if (Bk != B and cache_index is None) or 2 * nb != D:
         raise ValueError(f"q {tuple(q.shape)} and k_nibbles {tuple(k_nibbles.shape)} disagree")
-    if tuple(v_nibbles.shape) != (Bk, Hkv, S, nb):
-        raise ValueError(f"v_nibbles must be {(Bk, Hkv, S, nb)}, got {tuple(v_nibbles.shape)}")
+    if tuple(v_nibbles.shape) != (Bk, Hkv, S, nb) or v_nibbles.dtype != torch.uint8:
+        raise ValueError(f"v_nibbles must be uint8 {(Bk, Hkv, S, nb)}, got {v_nibbles.dtype} {tuple(v_nibbles.shape)}")
+    _check_packed(k_nibbles, k_qjl if with_qjl else None, k_norms if with_qjl else None, "k_nibbles")
     if Hq % Hkv != 0:
         raise ValueError(f"n_heads={Hq} must be divisible by n_kv_heads={Hkv}")
     dev = _lib.require_device(q, k_nibbles, v_nibbles, k_qjl if with_qjl else None,
@@ -244,12 +245,15 @@ class PackedKVAttention:
         D = 2 * nb
         if n_heads % Hkv:
             raise ValueError(f"n_heads={n_heads} must be divisible by n_kv_heads={Hkv}")
-        if tuple(v_nibbles.shape) != (N, Hkv, S, nb):
-            raise ValueError(f"v_nibbles must be {(N, Hkv, S, nb)}, got {tuple(v_nibbles.shape)}")
+        if tuple(v_nibbles.shape) != (N, Hkv, S, nb) or v_nibbles.dtype != torch.uint8:
+            raise ValueError(f"v_nibbles must be uint8 {(N, Hkv, S, nb)}, got {v_nibbles.dtype} {tuple(v_nibbles.shape)}")
+        if D not in (128, 32):
+            raise ValueError(f"head_dim must be 128 (or 32), got {D}")
+        _check_packed(k_nibbles, k_qjl if with_qjl else None, k_norms if with_qjl else None, "k_nibbles")
         B = N if batch is None else int(batch)
         if B < 0 or N < 1:
             raise ValueError("batch must be >= 0 and the cache pool non-empty")
-        dev = _lib.require_device(k_nibbles, v_nibbles)
+        dev = _lib.require_device(k_nibbles, v_nibbles, k_qjl if with_qjl else None, k_norms if with_qjl else None)
         from .quantize import _prep_codebooks
         self.cb, self.per_head = _prep_codebooks(codebooks, Hkv, dev)
         if not bool((self.cb.abs() <= 65504.0).all()):
@@ -302,6 +306,14 @@ class PackedKVAttention:
             cache_index: Optional[torch.Tensor] = None) -> torch.Tensor:
         if tuple(q.shape) != self.shape or q.dtype != self.q_dtype or not q.is_contiguous():
             raise ValueError(f"q must be a contiguous {self.q_dtype} tensor of shape {self.shape}")
+        # every pointer handed to the kernel must be memory of this device
+        # (a host pointer would fault the GPU); host-only checks, safe under
+        # graph capture
+        dev = self.device
+        if q.device != dev or (x is not None and x.device != dev) or \
+                (lora_indices is not None and lora_indices.device != dev) or \
+                (cache_index is not None and cache_index.device != dev):
+            raise ValueError(f"q, x, lora_indices and cache_index must be on {dev}")
         B, Hq, T, D = self.shape
         stream = torch.cuda.current_stream(self.device).cuda_stream
         qp = q.data_ptr()

@@ -6,8 +6,9 @@ API of the reference module omnistack_rs/kernels/quantize.py: constants
 (:593-640), ``quantize_rows`` / ``dequantize_rows`` (:456-537).
 
 ``quantize_heads`` runs ``omni_encode`` (nibbles and QJL sign bytes are
-bit-identical to the reference's CPU encoder; norms are the correctly
-rounded fp32 norm, within 2 ulp of torch's fp32 reduction), and
+bit-identical to the reference's CPU encoder; norms are within 1 ulp of the
+correctly rounded fp32 norm, where torch's fp32 reduction, whose order is
+not pinned, can sit an ulp or two away), and
 ``dequantize_heads`` runs ``omni_dequantize`` (bit-identical).  The
 row-seeded ``quantize_rows`` / ``dequantize_rows`` follow the reference's
 torch branch (seed (user_id % 1024) ^ (base + row)), not its Triton/Philox
@@ -75,6 +76,23 @@ def _batch_xor_unpack(nib_flat: torch.Tensor) -> torch.Tensor:
 
 # ── head-level codec ────────────────────────────────────────────────────
 
+def _check_packed(nibbles: torch.Tensor, qjl: Optional[torch.Tensor], norms: Optional[torch.Tensor],
+                  what: str = "nibbles") -> None:
+    """Packed cache operands must agree before their pointers reach a kernel
+    (the kernels address them from the nibbles' shape): nibbles (B, H, T, D/2)
+    and signs (B, H, T, D/16) uint8, norms (B, H, T)."""
+    if nibbles.dtype != torch.uint8:
+        raise ValueError(f"{what} must be uint8, got {nibbles.dtype}")
+    B, H, T, nb = nibbles.shape
+    if qjl is not None:
+        if qjl.dtype != torch.uint8:
+            raise ValueError(f"qjl sign bytes must be uint8, got {qjl.dtype}")
+        if tuple(qjl.shape) != (B, H, T, nb // 8):
+            raise ValueError(f"qjl sign bytes must be {(B, H, T, nb // 8)}, got {tuple(qjl.shape)}")
+    if norms is not None and tuple(norms.shape) != (B, H, T):
+        raise ValueError(f"norms must be {(B, H, T)}, got {tuple(norms.shape)}")
+
+
 def _prep_codebooks(codebooks: torch.Tensor, n_heads: int, device) -> tuple[torch.Tensor, int]:
     per_head = codebooks.dim() == 2
     if per_head:
@@ -137,6 +155,9 @@ def dequantize_heads(nibbles: torch.Tensor, qjl_packed: torch.Tensor, norms: tor
         raise ValueError(f"nibbles must be (B, n_heads, T, D/2), got {tuple(nibbles.shape)}")
     B, H, T, nb = nibbles.shape
     D = 2 * nb
+    if D not in (128, 32):
+        raise ValueError(f"head_dim must be {HEAD_DIM} (or 32), got {D}")
+    _check_packed(nibbles, qjl_packed if with_qjl else None, norms if with_qjl else None)
     dev = _lib.require_device(nibbles, qjl_packed if with_qjl else None, norms if with_qjl else None)
     cb, per_head = _prep_codebooks(codebooks, H, dev)
     nib = nibbles.contiguous()
@@ -191,11 +212,16 @@ def dequantize_rows(nibbles: torch.Tensor, qjl_packed: torch.Tensor, norms: torc
     """Row-seeded reconstruction (quantize.py:502-537)."""
     nb = nibbles.shape[-1]
     D = 2 * nb
-    dev = _lib.require_device(nibbles)
+    if D not in (128, 32):
+        raise ValueError(f"head_dim must be {HEAD_DIM} (or 32), got {D}")
+    if nibbles.dtype != torch.uint8 or (with_qjl and qjl_packed.dtype != torch.uint8):
+        raise ValueError("nibbles and qjl sign bytes must be uint8")
+    dev = _lib.require_device(nibbles, qjl_packed if with_qjl else None, norms if with_qjl else None)
     nib = nibbles.reshape(-1, nb).contiguous()
     N = nib.shape[0]
-    q = qjl_packed.reshape(N, D // 16).contiguous()
-    n = norms.reshape(N).to(torch.float32).contiguous()
+    # reshape raises when the signs or norms do not have one entry per row
+    q = qjl_packed.reshape(N, D // 16).contiguous() if with_qjl else None
+    n = norms.reshape(N).to(torch.float32).contiguous() if with_qjl else None
     out = torch.empty(N, D, dtype=torch.float32, device=dev)
     cb = codebook.reshape(16)
     for s in range(0, N, _ROW_CHUNK):
@@ -206,6 +232,7 @@ def dequantize_rows(nibbles: torch.Tensor, qjl_packed: torch.Tensor, norms: torc
             seeds = tuple(_make_qjl_seed(user_id, base_head_idx + i) for i in range(s, e))
             gb = _lib.g_bits(seeds, D, dev)
         _lib.check(_lib.lib().omni_dequantize(
-            _lib.ptr(nib[s:e]), _lib.ptr(q[s:e]), _lib.ptr(n[s:e]), _lib.ptr(cbd), 0, _lib.ptr(gb),
+            _lib.ptr(nib[s:e]), None if q is None else _lib.ptr(q[s:e]),
+            None if n is None else _lib.ptr(n[s:e]), _lib.ptr(cbd), 0, _lib.ptr(gb),
             1, e - s, 1, D, int(with_qjl), _lib.ptr(out[s:e]), _lib.stream_of(dev)))
     return out.reshape(*nibbles.shape[:-1], D)

@@ -52,6 +52,11 @@ PINS = {
                               "1e-5; V=const -> const; single unmasked key -> v0",
     "restate.apply_lora_to_q": "merged-weight closed form q + x (B A)^T alpha "
                                "in fp64; sentinel -1 exactly unchanged",
+    "restate.lloyd_max": "tests/test_oracle_pins.py: 16 repeated dyadic levels "
+                         "are recovered exactly; max_iters=0 gives the equal-count "
+                         "bin means (math.fsum, n % 16 largest left out); the "
+                         "N(0,1) quantile grid converges to Max's 1960 table "
+                         "(levels within 2.5e-3, MSE 0.009497)",
     "exact.projection_signs_exact": "tests/test_oracle_pins.py::"
                                     "test_exact_projection_signs_survive_cancellation: "
                                     "rows whose fp64 sum loses the small terms after "

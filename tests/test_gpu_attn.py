@@ -49,6 +49,7 @@ def _assert_close(got, want, tag):
 @pytest.mark.parametrize("B,Hq,Hkv,T,S", [
     (1, 4, 2, 8, 32), (2, 8, 4, 16, 64), (1, 8, 8, 1, 128), (2, 4, 2, 32, 48),   # reference test shapes
     (4, 8, 4, 1, 256), (2, 32, 8, 1, 50), (3, 32, 8, 1, 1000), (1, 4, 1, 1, 17), (2, 2, 2, 5, 1),
+    (1, 8, 2, 1, 960),       # one split of 30 tiles: the decode kernel's dynamic tile claims (tiles 24-29)
 ])
 @pytest.mark.parametrize("with_qjl", [True, False])
 def test_attn_matches_oracle(device, B, Hq, Hkv, T, S, with_qjl):
@@ -170,6 +171,46 @@ def test_attn_head_dim_32(device):
     _assert_close(got, want, "d32 extreme rows")
 
 
+def _proj32_cache(B, Hkv, S, seed, uid):
+    """The head_dim-32 config recipe: 128-dim K/V (outlier channels x8)
+    projected by the seeded orthonormal 128 x 32 matrix, rotated (WHT 32)
+    and encoded by the oracle."""
+    import bench
+    P = bench.ortho_proj()
+    x = _data.kv((2, B, Hkv, S, 128), seed=seed, dtype=torch.bfloat16).float() @ P
+    x = x.to(torch.bfloat16)
+    k, v = restate.wht(x[0]), restate.wht(x[1])
+    cb = torch.stack([restate.lloyd_max(k[:, h].reshape(-1)[:50000].float(), max_iters=60) for h in range(Hkv)])
+    kn, kq, kr = restate.quantize_heads(k, cb, user_id=uid)
+    vn, _, _ = restate.quantize_heads(v, cb, user_id=uid)
+    return kn, kq, kr, vn, cb, P
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,T,S", [
+    (2, 32, 8, 64, 600),     # C5 at head_dim 32, scaled down: two splits per (b, kv head) + combine
+    (1, 8, 2, 16, 100),      # one split
+    (3, 8, 2, 5, 77),        # ragged rows and tokens
+])
+def test_attn_head_dim_32_causal(device, B, Hq, Hkv, T, S):
+    """head_dim 32 with the chunked-prefill causal mask (query t sees keys
+    <= S - T + t) on the projected recipe, against the masked oracle."""
+    uid, off = 13, S - T
+    print(f"[d32 causal] B={B} Hq={Hq} Hkv={Hkv} T={T} S={S}", flush=True)
+    kn, kq, kr, vn, cb, P = _proj32_cache(B, Hkv, S, seed=60 + S, uid=uid)
+    q = (_data.query((B, Hq, T, 128), seed=61 + S).float() @ P).to(torch.bfloat16)
+    got = _run(device, q, kn, kq, kr, vn, cb, uid, causal_offset=off)
+    want = restate.fused_attn_python(q.float(), kn, kq, kr, vn, cb, uid, 1 / math.sqrt(32), True,
+                                     mask=_causal_mask(T, S, off))
+    assert torch.isfinite(got).all()
+    _assert_close(got, want, f"d32 causal B{B} Hq{Hq} Hkv{Hkv} T{T} S{S}")
+    # a query that sees only the first key returns that key's V exactly
+    # (first row of a chunk placed at the start of the cache)
+    got0 = _run(device, q[:, :, :1].contiguous(), kn, kq, kr, vn, cb, uid, causal_offset=0)
+    v0 = restate.dequantize_heads(vn[:, :, :1], kq[:, :, :1], kr[:, :, :1], cb, user_id=uid, with_qjl=False)
+    want0 = v0.repeat_interleave(Hq // Hkv, dim=1)
+    assert (got0.cpu() - want0).abs().max().item() <= 1e-6
+
+
 def test_attn_shared_codebook(device):
     kn, kq, kr, vn, cb = _cache(1, 2, 70, seed=24, user_id=0)
     cb1 = cb[0]
@@ -185,9 +226,39 @@ def test_attn_rejects_bad_shapes(device):
         _run(device, torch.randn(1, 3, 1, 128), kn, kq, kr, vn, cb, 0)
     with pytest.raises(ValueError):
         _run(device, torch.randn(1, 4, 1, 128), kn, kq, kr, vn[:, :, :8], cb, 0)
+    q = torch.randn(1, 4, 1, 128)
+    # QJL signs / norms that do not match the nibbles, non-byte nibbles
+    for bad in ((kn, kq[:, :, :8], kr, vn), (kn, kq[..., :4], kr, vn), (kn, kq, kr[:, :, :8], vn),
+                (kn, kq, kr[:, :1], vn), (kn.to(torch.int16), kq, kr, vn), (kn, kq.to(torch.int32), kr, vn),
+                (kn, kq, kr, vn.to(torch.int32))):
+        with pytest.raises(ValueError):
+            _run(device, q, *bad, cb, 0)
     from omnistack_rs.kernels.fused_attention import PackedKVAttention
+    from omnistack_rs.kernels.quantize import dequantize_heads
+    with pytest.raises(ValueError):
+        dequantize_heads(kn.to(device), kq[:, :, :8].to(device), kr.to(device), cb.to(device))
+    with pytest.raises(ValueError):
+        PackedKVAttention(*(t.to(device) for t in (kn, kq, kr[:, :, :8], vn)), cb.to(device), n_heads=4)
     with pytest.raises(ValueError, match="fp16 range"):
         PackedKVAttention(*(t.to(device) for t in (kn, kq, kr, vn)), (cb * 1e5).to(device), n_heads=4, user_id=0)
+
+
+def test_prepared_run_rejects_host_tensors(device):
+    """run() hands raw pointers to the kernel: tensors that are not on the
+    attention's device raise ValueError before any launch."""
+    att, _, q, x, ids = _prepared(device)
+    before = att.out.clone()
+    for args in ((q.cpu(), x, ids), (q, x.cpu(), ids), (q, x, ids.cpu())):
+        with pytest.raises(ValueError, match="must be on"):
+            att.run(*args)
+    from omnistack_rs.kernels.fused_attention import PackedKVAttention
+    kn, kq, kr, vn, cb = _cache(4, 2, 60, seed=52, user_id=0)
+    pool = PackedKVAttention(*(t.to(device) for t in (kn, kq, kr, vn, cb)), n_heads=8, batch=3)
+    qp = _data.query((3, 8, 1, 128), seed=53).to(device)
+    with pytest.raises(ValueError, match="must be on"):
+        pool.run(qp, cache_index=torch.tensor([0, 1, 2]))
+    torch.cuda.synchronize()
+    assert torch.equal(att.out, before)
 
 
 def _prepared(device, B=4, Hq=32, Hkv=8, S=300, uid=9, L=16, rank=8, hidden=128):

@@ -5,7 +5,8 @@ dequantizer run through libomnistack_amd.so on cuda:0 and are compared with
 oracle.restate on the same seeded inputs.  Sign bits must equal the exact
 (fp64) projection sign everywhere and the oracle's fp32-BLAS sign except
 where |P|/||e|| < 1e-6 (boundary rule); norms must be within 1 ulp of the
-correctly rounded fp64 norm and 2 ulp of the oracle's fp32 torch norm.
+correctly rounded fp64 norm (the oracle's fp32 torch norm, whose reduction
+order is not pinned, may itself sit an ulp or two from it).
 """
 import json
 import math
@@ -17,44 +18,9 @@ import torch
 
 from oracle import exact, restate
 from tests import _data
+from tests._checks import check_encode as _check_encode
 
 pytestmark = pytest.mark.gpu
-
-
-def _check_encode(x_rot_cpu, cb_cpu, user_id, nib, qjl, nrm, tag=""):
-    """x_rot_cpu: the rotated fp input on CPU exactly as the encoder sees it."""
-    B, H, T, D = x_rot_cpu.shape
-    r_nib, r_qjl, r_nrm = restate.quantize_heads(x_rot_cpu, cb_cpu, user_id=user_id)
-    nib, qjl, nrm = nib.cpu(), qjl.cpu(), nrm.cpu()
-    assert torch.equal(nib, r_nib), f"{tag}: nibbles differ at {(nib != r_nib).nonzero()[:5].tolist()}"
-    # residuals + exact projections per head
-    per_head = cb_cpu.dim() == 2
-    n_mis_oracle = 0
-    for h in range(H):
-        cb = (cb_cpu[h] if per_head else cb_cpu).float()
-        xh = x_rot_cpu[:, h].reshape(-1, D).float()
-        _, deq = restate.quantize_int4(xh, cb)
-        e = (xh - deq).numpy()
-        Gh = exact.g_from_mt(restate.make_qjl_seed(user_id, h), D)
-        P = exact.projections_fp64(e, Gh)
-        ebits = exact.pack_bits_lsb(exact.projection_signs_exact(e, Gh).astype(np.uint8))
-        g = qjl[:, h].reshape(-1, D // 16).numpy()
-        finite = np.isfinite(e).all(axis=1)
-        assert np.array_equal(g[finite], ebits[finite]), f"{tag}: sign bits differ from exact sign (head {h})"
-        o = r_qjl[:, h].reshape(-1, D // 16).numpy()
-        diff = np.unpackbits(g ^ o, axis=1, bitorder="little").astype(bool)
-        if diff.any():
-            en = np.linalg.norm(e.astype(np.float64), axis=1, keepdims=True)
-            rel = np.abs(P) / np.where(en > 0, en, 1)
-            assert (rel[diff] < 1e-6).all(), f"{tag}: sign mismatch outside the boundary rule"
-            n_mis_oracle += int(diff.sum())
-        gn = nrm[:, h].reshape(-1).numpy()
-        en32 = exact.residual_norm(e)
-        fin = np.isfinite(en32)
-        assert np.array_equal(np.isposinf(gn), np.isposinf(en32)), f"{tag}: norm overflow rule"
-        assert exact.ulp_distance_f32(gn[fin], en32[fin]).max(initial=0) <= 1, f"{tag}: norm vs exact"
-        assert exact.ulp_distance_f32(gn[fin], r_nrm[:, h].reshape(-1).numpy()[fin]).max(initial=0) <= 2
-    return n_mis_oracle
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
@@ -143,6 +109,24 @@ def test_encode_kv_fused_rotation(device):
     cb = _data.gaussian_codebook(8)
     nib, qjl, nrm = encode_kv(x.to(device), cb.to(device), user_id=42, sign_flip=s.to(device))
     _check_encode(restate.rotate(x, s), cb, 42, nib, qjl, nrm, tag="fused")
+
+
+def test_encode_c4_full_size(device):
+    """The C4 encode config at full size: K of 16 sequences x 8 kv heads x
+    4096 tokens (524,288 rows, bf16 with outlier channels), rotation with the
+    seeded sign flip fused in, per-head codebooks.  Nibbles bit-exact; every
+    sign bit equals the exact projection sign (boundary rule vs the fp32
+    oracle); norms within 1 ulp of the exact norm."""
+    from omnistack_rs.kernels.quantize import encode_kv
+    print("[encode] C4 full size 16 x 8 x 4096", flush=True)
+    x = _data.kv((16, 8, 4096, 128), seed=46)
+    s = _data.sign_flip()
+    cb = _data.gaussian_codebook(8) * torch.linspace(0.9, 1.2, 8).reshape(8, 1)
+    nib, qjl, nrm = encode_kv(x.to(device), cb.to(device), user_id=42, sign_flip=s.to(device))
+    torch.cuda.synchronize()
+    n_mis = _check_encode(restate.rotate(x, s), cb, 42, nib, qjl, nrm, tag="C4 full")
+    print(f"[encode] C4 full size ok; {n_mis} sign bits differ from the fp32 oracle inside the boundary rule",
+          flush=True)
 
 
 def test_encode_head_dim_32(device):

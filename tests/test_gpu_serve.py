@@ -31,7 +31,10 @@ def _pool(N, Hkv, S, seed, uid, D=128):
 CASES = [
     ("decode", 7, 5, 32, 8, 1, 120, 128, True),
     ("decode-2-per-block", 9, 40, 32, 8, 1, 50, 128, True),
-    ("decode-split", 3, 3, 8, 2, 1, 4096, 128, False),    # > 12 tiles per split: wave order varies
+    ("decode-split", 3, 3, 8, 2, 1, 4096, 128, True),     # split-K, 16 tiles per split: all assigned statically
+    # 30 tiles in one split: tiles past the first 2 per wave (24) are claimed
+    # dynamically, so the summation order can vary between runs
+    ("decode-dynamic", 3, 3, 8, 2, 1, 960, 128, False),
     ("prefill", 4, 3, 8, 2, 40, 200, 128, True),
     ("d32", 5, 3, 8, 2, 3, 120, 32, True),
 ]

@@ -316,3 +316,60 @@ def test_exact_projection_signs_survive_cancellation():
     assert bits[0].tolist() == [True, True, True]
     assert bits[1].tolist() == [False, False, True]
     assert exact.exact_dot(e[0], G[0]) == 0.5 + 2.0 ** -20
+
+
+# ── Lloyd-Max calibration ───────────────────────────────────────────────
+
+def test_lloyd_max_recovers_repeated_levels_exactly():
+    """Samples that take 16 distinct values, each equally often, are their
+    own Lloyd-Max fixed point: the equal-count initial bins hold one value
+    each, every sample sits on its centroid, and the means are exact (the
+    levels are multiples of 1/8, so every partial sum is exact in fp32)."""
+    levels = torch.tensor([-23, -17, -12, -9, -6, -4, -2, -1, 1, 3, 5, 7, 10, 14, 19, 26],
+                          dtype=torch.float32) / 8
+    x = levels.repeat(100)[torch.randperm(1600, generator=torch.Generator().manual_seed(3))]
+    cb = restate.lloyd_max(x)
+    assert cb.dtype == torch.float32 and cb.shape == (16,)
+    assert torch.equal(cb, levels)
+
+
+@pytest.mark.parametrize("n", [16 * 100, 16 * 100 + 7, 16 * 997 + 15])
+def test_lloyd_max_initial_bins_are_fsum_means(n):
+    """max_iters = 0 returns the initial codebook: the means of 16 equal bins
+    of the sorted samples, bin size n // 16, the n % 16 largest samples in no
+    bin (codebook.py:79-85).  Dyadic samples make torch's fp32 mean exact
+    (equal to math.fsum / size); Gaussian samples agree to fp32 rounding."""
+    g = torch.Generator().manual_seed(n)
+    dy = torch.randint(-4000, 4000, (n,), generator=g).float() / 64
+    ga = torch.randn(n, generator=g)
+    for x, exact_eq in ((dy, True), (ga, False)):
+        xs = sorted(x.tolist())
+        bs = n // 16
+        want = torch.tensor([math.fsum(xs[i * bs:(i + 1) * bs]) / bs for i in range(16)], dtype=torch.float64)
+        got = restate.lloyd_max(x, max_iters=0).double()
+        if exact_eq:
+            assert torch.equal(got, want.float().double())
+        else:
+            assert (got - want).abs().max().item() <= 4e-7 * want.abs().max().item() + 1e-7
+    # the samples left out of every bin must not move the initial codebook
+    if n % 16:
+        big = torch.cat([dy[:16 * (n // 16)].sort().values, torch.full((n % 16,), 1e6)])
+        assert torch.equal(restate.lloyd_max(big, max_iters=0), restate.lloyd_max(big[:16 * (n // 16)], max_iters=0))
+
+
+def test_lloyd_max_gaussian_matches_max_1960():
+    """On the N(0,1) quantile grid the iteration converges to Max's optimum
+    16-level Gaussian quantizer (J. Max, IRE Trans. Inf. Theory IT-6, 1960,
+    Table I: outputs +-0.1284, 0.3881, 0.6568, 0.9424, 1.256, 1.618, 2.069,
+    2.733; mean squared error 0.009497).  The grid's truncated tails move the
+    outer level by < 2e-3."""
+    from scipy.stats import norm
+    N = 1 << 17
+    x = torch.tensor(norm.ppf((np.arange(N) + 0.5) / N), dtype=torch.float32)
+    cb = restate.lloyd_max(x, max_iters=300)
+    max_y = torch.tensor([0.1284, 0.3881, 0.6568, 0.9424, 1.256, 1.618, 2.069, 2.733], dtype=torch.float64)
+    assert (cb[8:].double() - max_y).abs().max().item() < 2.5e-3
+    assert (cb[:8].flip(0).double() + max_y).abs().max().item() < 2.5e-3
+    code = exact.argmin_first(x.numpy(), cb.numpy())
+    mse = float(((x.double() - cb.double()[torch.from_numpy(code).long()]) ** 2).mean())
+    assert abs(mse - 0.009497) < 2e-5
