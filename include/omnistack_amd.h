@@ -230,6 +230,30 @@ int omni_attn_lora(const void *q, int q_dtype,
                    float *out, void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * omni_attn without a workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * The split-K partials live in a static device array of
+ * omni_attn_noalloc_scratch_bytes() bytes (16 MiB) that each device holds
+ * until the process ends; a launch needing more
+ * (omni_attn_workspace_size(...) > that) returns OMNI_EWORKSPACE without
+ * launching.  Calls on one device share the array: calls that overlap on
+ * one device (several streams or threads) race.  The first call on a
+ * device looks up the array's address (make it outside graph capture).
+ * Results are those of omni_attn with the same arguments.
+ */
+size_t omni_attn_noalloc_scratch_bytes(void);
+
+int omni_attn_noalloc(const void *q, int q_dtype,
+                      const uint8_t *k_nib, const uint8_t *k_qjl, const float *k_norms,
+                      const uint8_t *v_nib, const float *codebooks, int per_head_codebook,
+                      const uint32_t *g_bits,
+                      int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int head_dim,
+                      float scale, int with_qjl, int64_t causal_offset,
+                      int rotate_q, const int8_t *sign_flip,
+                      float *out, void *stream);
+
+/*
  * One serving step over a pool of cached sequences: query b attends cache
  * sequence cache_index[b] of a pool of n_cache_seqs (k_nib, k_qjl, k_norms,
  * v_nib are (n_cache_seqs, Hkv, S, ...)); q, x, lora_idx and out have B

@@ -25,6 +25,9 @@
 // the PV product; the softmax denominator sums the same rounded P.
 #include <math.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "omni_common.h"
 
 namespace omni {
@@ -1985,4 +1988,75 @@ extern "C" int omni_attn_serve(const void *q, int q_dtype, const int64_t *cache_
     return attn_run(q, q_dtype, k_nib, k_qjl, k_norms, v_nib, codebooks, per_head_codebook, g_bits, B, Hq, Hkv, T,
                     S, head_dim, scale, with_qjl, causal_offset, rotate_q, sign_flip, out, workspace,
                     workspace_bytes, stream, &spec, cache_index, n_cache_seqs);
+}
+
+// ── allocation-free variant of omni_attn ─────────────────────────────────
+//
+// For callers that cannot allocate device memory (code under HIP graph
+// capture, serving loops, harnesses that forbid hipMalloc): the split-K
+// partials live in this file-scope array instead of a caller workspace.
+// Each device holds its own copy for the life of the process.  In host code
+// `scratch` names a host-side stand-in, never the device memory: its device
+// address is looked up once per device (hipGetSymbolAddress, with that
+// device current) and only that address is handed to kernels.  Every call on
+// a device shares the array, so calls that overlap on one device (several
+// streams, several host threads) race; nothing in it needs to start at zero
+// (each launch writes every partial it reads back).
+namespace omni {
+
+constexpr size_t kScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kScratchMaxDevices = 64;
+static std::atomic<void *> g_scratch_addr[kScratchMaxDevices];
+static std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the current device (looked up on the first
+// call per device).
+static int scratch_address(void **out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchMaxDevices) {
+        set_error("omni_attn_noalloc: no usable current device (%d)", dev);
+        return OMNI_ERUNTIME;
+    }
+    void *p = g_scratch_addr[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch_addr[dev].load(std::memory_order_relaxed);
+        if (p == nullptr) {
+            const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e != hipSuccess || p == nullptr) {
+                set_error("omni_attn_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                          hipGetErrorString(e));
+                return OMNI_ERUNTIME;
+            }
+            g_scratch_addr[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return OMNI_OK;
+}
+
+}  // namespace omni
+
+extern "C" size_t omni_attn_noalloc_scratch_bytes(void) { return omni::kScratchBytes; }
+
+extern "C" int omni_attn_noalloc(const void *q, int q_dtype, const uint8_t *k_nib, const uint8_t *k_qjl,
+                                 const float *k_norms, const uint8_t *v_nib, const float *codebooks,
+                                 int per_head_codebook, const uint32_t *g_bits, int64_t B, int Hq, int Hkv,
+                                 int64_t T, int64_t S, int head_dim, float scale, int with_qjl,
+                                 int64_t causal_offset, int rotate_q, const int8_t *sign_flip, float *out,
+                                 void *stream) {
+    const size_t need = omni_attn_workspace_size(B, Hq, Hkv, T, S, head_dim);
+    if (need > kScratchBytes) {
+        set_error("omni_attn_noalloc: this launch needs %zu bytes of split-K scratch, more than the %zu-byte "
+                  "static array; call omni_attn with a workspace instead", need, kScratchBytes);
+        return OMNI_EWORKSPACE;
+    }
+    void *ws = nullptr;
+    const int rc = scratch_address(&ws);
+    if (rc != OMNI_OK) return rc;
+    return attn_run(q, q_dtype, k_nib, k_qjl, k_norms, v_nib, codebooks, per_head_codebook, g_bits, B, Hq, Hkv, T,
+                    S, head_dim, scale, with_qjl, causal_offset, rotate_q, sign_flip, out, ws, kScratchBytes,
+                    stream, nullptr, nullptr, 0);
 }
