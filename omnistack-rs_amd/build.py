@@ -48,9 +48,15 @@ def common_flags() -> list[str]:
     ]
 
 
+# Per-source flags.  attn.hip: the decode kernel's tile claims are one
+# lane-0 LDS atomic each; the backend's atomic optimizer would wrap every
+# one in a wave reduction (mbcnt / popcount / broadcast) it does not need.
+EXTRA_FLAGS = {"attn.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"]}
+
+
 def compile_one(src: str) -> str:
     obj = os.path.join(OBJ_DIR, os.path.basename(src) + ".o")
-    cmd = [hipcc(), *common_flags(), "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [hipcc(), *common_flags(), *EXTRA_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
     if src.endswith(".cpp"):
         cmd = [hipcc(), "-O2", "-fPIC", "-std=c++17", f"-I{INCLUDE}", f"-I{CSRC}", "-c",
                os.path.join(CSRC, src), "-o", obj]

@@ -839,12 +839,17 @@ __device__ __forceinline__ void lora_row(float &lo, float &hi, const AttnArgs &a
     hi = active ? uhi : (bad ? __builtin_nanf("") : hi);
 }
 
-// Next tile index of the block (wave-uniform): lane 0 bumps the LDS counter.
-__device__ __forceinline__ int claim_tile(int *cnt, int lane) {
+// Tile claims from the block's LDS counter: claim_issue() has lane 0 bump
+// it and returns the register the old value lands in; claim_value() makes
+// it wave-uniform.  The loop reads a claim one step after issuing it, so
+// the atomic's latency hides behind that step's LUT traffic (LDS operations
+// complete in order) instead of stalling the next tile's loads.
+__device__ __forceinline__ int claim_issue(int *cnt, int lane) {
     int v = 0;
     if (lane == 0) v = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    return __builtin_amdgcn_readfirstlane(v);
+    return v;
 }
+__device__ __forceinline__ int claim_value(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 template <bool QJL, int PF, int SPB, bool LORA>
 __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs a) {
@@ -1187,10 +1192,13 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
 
         // online softmax (exp2 domain), lazy rescale.  Logits are rounded
         // before the max is taken, so every exponent below is <= 8 exactly.
+        // m_run is the same in the four lane groups of a row (it only ever
+        // takes a cross-group maximum), so each lane tests its own 8 scores
+        // and the cross-group maximum is formed only when some lane rescales.
         float mt = vmax3(vmax3(sc[0], sc[1], sc[2]), vmax3(sc[3], sc[4], sc[5]), vmax2(sc[6], sc[7]));
-        mt = max_over_groups(mt);
-        const bool need = mt > m_run + 8.0f;
-        if (__builtin_amdgcn_ballot_w64(need)) {
+        if (__builtin_amdgcn_ballot_w64(mt > m_run + 8.0f)) {
+            mt = max_over_groups(mt);
+            const bool need = mt > m_run + 8.0f;
             const float f = need ? __builtin_amdgcn_exp2f(m_run - mt) : 1.0f;
 #pragma unroll
             for (int k = 0; k < 8; ++k) oacc[k] *= f;
@@ -1250,28 +1258,28 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     static_assert(PF == 2, "the dynamic tile loop alternates two ring slots");
     int *tile_cnt = reinterpret_cast<int *>(smem + kDecCntOff);
     int i_cur = wave;
-    int c_nxt = claim_tile(tile_cnt, lane);
+    int c_raw = claim_issue(tile_cnt, lane);
     if (i_cur < ntiles) {
         tile_step(ring[0], tile_tok(i_cur), tile_seq(i_cur));
         const int i_pre = wave + nw;
         if (i_pre < ntiles) {
-            i_cur = c_nxt;
-            c_nxt = claim_tile(tile_cnt, lane);
+            i_cur = claim_value(c_raw);
+            c_raw = claim_issue(tile_cnt, lane);
             __builtin_amdgcn_sched_barrier(0);
             tile_load<QJL>(ring[0], tile_seq(i_cur) ? P1 : P, OFS, tile_tok(i_cur));
             __builtin_amdgcn_sched_barrier(0);
             tile_step(ring[1], tile_tok(i_pre), tile_seq(i_pre));
             for (;;) {
                 if (i_cur >= ntiles) break;
-                const int i_nxt = c_nxt;
-                c_nxt = claim_tile(tile_cnt, lane);
+                const int i_nxt = claim_value(c_raw);
+                c_raw = claim_issue(tile_cnt, lane);
                 __builtin_amdgcn_sched_barrier(0);
                 tile_load<QJL>(ring[1], tile_seq(i_nxt) ? P1 : P, OFS, tile_tok(i_nxt));
                 __builtin_amdgcn_sched_barrier(0);
                 tile_step(ring[0], tile_tok(i_cur), tile_seq(i_cur));
                 if (i_nxt >= ntiles) break;
-                i_cur = c_nxt;
-                c_nxt = claim_tile(tile_cnt, lane);
+                i_cur = claim_value(c_raw);
+                c_raw = claim_issue(tile_cnt, lane);
                 __builtin_amdgcn_sched_barrier(0);
                 tile_load<QJL>(ring[0], tile_seq(i_cur) ? P1 : P, OFS, tile_tok(i_cur));
                 __builtin_amdgcn_sched_barrier(0);
