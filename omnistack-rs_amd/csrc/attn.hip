@@ -1729,11 +1729,380 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
     }
 }
 
+// ── chunked-prefill kernel at head_dim 32 ────────────────────────────────
+//
+// The D = 128 prefill scheme for the generalized codec at D = 32 (16-byte
+// nibble rows, 2 sign bytes, QJL_DIM 16).  Each wave owns 16 * NCB query rows
+// and streams every key tile of its split; per 32-token tile, 16-token half u
+// and column block:
+//   K pass  2 MFMAs: lane (n, g) holds dword g of token n (dims 8g .. 8g + 7),
+//           two cache bytes per k-step through the byte LUT (fp16 hi +
+//           remainder slots); B = the exact fp16 q row (per-row 2^k scale)
+//   QJL     1 MFMA: A = the token's 16 sign bits as +-1 halves, twice (k-slots
+//           0-15 and 16-31), B = sqrt(2/pi)/D (G q) as fp16 hi in slots 0-15
+//           and its fp16 remainder in 16-31; the fp32 norm (quad broadcast)
+//           scales it into the score
+//   PV      2 MFMAs (even and odd dims): lane (n, g) loads byte n of tokens
+//           4g .. 4g + 3 and forms pair bytes (two tokens' nibbles at dim 2n
+//           or 2n + 1), whose LUT entries are MFMA-ready (hi, lo) pairs
+// Online softmax in the exp2 domain with P in fp16, summed by an MFMA
+// against ones, as in the other kernels.
+constexpr int kP32Waves = 8;
+constexpr int kP32CbOff = kSlutOff + kSlutBytes;                          // 16 x (fp16 hi | remainder << 16)
+constexpr int kP32StageOff = kP32CbOff + 64;                               // per wave: q rows fp16 (+ remainder plane), then G q f32
+constexpr int kP32StageBytes = 32 * 32 * 2 * 2;
+constexpr int kP32QsrOff = kP32StageOff + kP32Waves * kP32StageBytes;     // per wave: 32 f32 score scales
+constexpr int kP32LdsBytes = kP32QsrOff + kP32Waves * 32 * 4;
+
+// One 32-token tile at D = 32 as loaded.
+struct TileRaw32 {
+    uint32_t k[2];     // K dword g of token 16u + (lane % 16)
+    uint32_t sg[2];    // the 2 sign bytes of the same token
+    float nr[2];       // norm of token 16u + 4g + lane % 4
+    uint32_t v[8];     // V byte (lane % 16) of token 16(i / 4) + 4g + i % 4 (low byte)
+};
+
+template <bool QJL>
+__device__ __forceinline__ void tile_load32(TileRaw32 &R, const DecBufs &P, int n, int g, int t0) {
+    const uint32_t t = (uint32_t)t0;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const uint32_t tk = t + 16u * u + (uint32_t)n;
+        R.k[u] = __builtin_amdgcn_raw_buffer_load_b32(P.kn, tk * 16u + 4u * g, 0, 0);
+        if (QJL) {
+            R.sg[u] = __builtin_amdgcn_raw_buffer_load_b16(P.kq, tk * 2u, 0, 0);
+            R.nr[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                P.kr, (t + 16u * u + 4u * g + ((uint32_t)n & 3u)) * 4u, 0, 0));
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        R.v[i] = __builtin_amdgcn_raw_buffer_load_b8(P.vn, (t + 16u * (i / 4) + 4u * g + (i % 4)) * 16u + (uint32_t)n, 0, 0);
+}
+
+// Normalized 32-point WHT of the element (lane % 32) of each half-wave's
+// row (_wht_torch order, fp32; an fma with +-1 rounds as the add/subtract).
+__device__ __forceinline__ float wht32_lane(float x, int lane) {
+    x = __builtin_fmaf((lane & 1) ? -1.0f : 1.0f, x, xor_partner<1>(x, lane));
+    x = __builtin_fmaf((lane & 2) ? -1.0f : 1.0f, x, xor_partner<2>(x, lane));
+    x = __builtin_fmaf((lane & 4) ? -1.0f : 1.0f, x, xor_partner<4>(x, lane));
+    x = __builtin_fmaf((lane & 8) ? -1.0f : 1.0f, x, xor_partner<8>(x, lane));
+    x = __builtin_fmaf((lane & 16) ? -1.0f : 1.0f, x, xor_partner<16>(x, lane));
+    return x;
+}
+
+template <bool QJL, int NCB, bool QLO>
+__global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs a) {
+    constexpr int D = 32, QD = 16, RW = 16 * NCB;       // rows per wave
+    static_assert(!QLO || NCB == 1, "the f32 remainder plane shares the stage area");
+    __shared__ __attribute__((aligned(16))) unsigned char smem[kP32LdsBytes];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n = lane & 15, g = lane >> 4;
+    const int split = blockIdx.x, hk = blockIdx.y;
+    const int64_t bz = blockIdx.z;
+    const int64_t b = bz / a.n_rchunks;
+    const int rc = (int)(bz % a.n_rchunks);
+    const int nrows_total = (int)(a.T * a.G);
+    const int row0 = rc * a.rows + wave * RW;
+    uint16_t *stage = reinterpret_cast<uint16_t *>(smem + kP32StageOff + wave * kP32StageBytes);
+    float *qsr_l = reinterpret_cast<float *>(smem + kP32QsrOff) + wave * 32;
+
+    // ── codebook pairs and the sign table ───────────────────────────────
+    {
+        const __amdgpu_buffer_rsrc_t CB = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(a.codebooks + (a.per_head ? hk * 16 : 0)), (short)0, 16 * 4, kBufWord3);
+        const float c = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(CB, 4u * (lane & 15), 0, 0));
+        const uint16_t h = f32_to_f16_rne(c);
+        *reinterpret_cast<uint32_t *>(smem + kP32CbOff + 4 * (lane & 15)) =
+            (uint32_t)h | ((uint32_t)f32_to_f16_rne(c - f16_to_f32(h)) << 16);
+    }
+    sign_table_store(smem, tid);      // 512 threads
+
+    // ── this wave's query rows, two per pass (half-waves): (sign flip,)
+    //    WHT, round; per-row power-of-2 scale into fp16 range; fp16 stage ──
+    {
+        const int e = lane & 31, half = lane >> 5;
+        const bool flip = a.rotate_q && a.sign_flip && a.sign_flip[e] < 0;
+        for (int rp = 0; rp < RW; rp += 2) {
+            const int rr = rp + half;
+            const int rho = row0 + rr;
+            const bool ok = rho < nrows_total;
+            const int rcl = ok ? rho : nrows_total - 1;
+            const int t = rcl / a.G, hq = hk * a.G + (rcl - t * a.G);
+            float x = load_as_f32(a.q, a.q_dtype, ((b * a.Hq + hq) * a.T + t) * D + e);
+            x = flip ? -x : x;
+            if (a.rotate_q) x = round_to_dtype(wht32_lane(x, lane) * a.wht_scale, a.q_dtype);
+            if (!ok) x = 0.0f;
+            float m = fabsf(x);
+#pragma unroll
+            for (int sh = 16; sh >= 1; sh >>= 1) m = fmaxf(m, __shfl_xor(m, sh));
+            int ex = 0;
+            if (m > 0.0f && m < INFINITY) frexpf(m, &ex);
+            const float sr = ldexpf(1.0f, 15 - imax(ex, -100));
+            const uint16_t x16 = f32_to_f16_rne(x * sr);
+            stage[rr * D + e] = x16;
+            if constexpr (QLO) stage[16 * D + rr * D + e] = f32_to_f16_rne(x * sr - f16_to_f32(x16));
+            if (e == 0) qsr_l[rr] = a.qscale / sr;
+        }
+    }
+    __syncthreads();
+
+    // ── byte LUT (after the codebook pairs are visible) ───────────────────
+    {
+        const uint32_t *cbh = reinterpret_cast<const uint32_t *>(smem + kP32CbOff);
+        const uint32_t w0 = cbh[(tid >> 4) & 15];
+        uint32_t w1[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w1[i] = cbh[(tid >> 8) + 2 * i];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int e = (tid >> 4) + 32 * i;
+            const uint32_t hp = __builtin_amdgcn_perm(w1[i], w0, 0x05040100u);
+            const uint32_t lp = __builtin_amdgcn_perm(w1[i], w0, 0x07060302u);
+            *reinterpret_cast<uint4 *>(smem + kLutOff + e * 256 + (tid & 15) * 16) = make_uint4(hp, lp, hp, lp);
+        }
+    }
+
+    // ── per-lane B operands: q (exact fp16) for the scores ───────────────
+    half8_t bk[NCB][2], bkl[QLO ? NCB : 1][2], bgq[NCB];
+    float qsr[NCB];
+#pragma unroll
+    for (int c = 0; c < NCB; ++c) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const uint2 w = *reinterpret_cast<const uint2 *>(stage + (16 * c + n) * D + 8 * g + 4 * s);
+            bk[c][s] = as_half8(w.x, w.x, w.y, w.y);
+            if constexpr (QLO) {
+                const uint2 wl = *reinterpret_cast<const uint2 *>(stage + 16 * D + (16 * c + n) * D + 8 * g + 4 * s);
+                bkl[c][s] = as_half8(wl.x, wl.x, wl.y, wl.y);
+            }
+        }
+        qsr[c] = qsr_l[16 * c + n];
+    }
+    __syncthreads();   // sign table visible
+    // G q (staged scale) on MFMA: A = q rows (k = the 32 dims), B = G rows
+    // expanded by the sign table; lane (n, g) gets row 16 c + 4 g + i,
+    // projection n
+    float4_t gacc[NCB];
+#pragma unroll
+    for (int c = 0; c < NCB; ++c) gacc[c] = float4_t{0.f, 0.f, 0.f, 0.f};
+    if (QJL) {
+        const uint32_t gw = a.g_bits[(int64_t)hk * QD + n];
+        const half8_t bg = sign_halves(smem, gw, 8u * g, (uint32_t)kSlutOff | ((uint32_t)(lane & 31) * 8u));
+#pragma unroll
+        for (int c = 0; c < NCB; ++c) {
+            const uint4 qv = *reinterpret_cast<const uint4 *>(stage + (16 * c + n) * D + 8 * g);
+            gacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(qv.x, qv.y, qv.z, qv.w), bg, gacc[c], 0, 0, 0);
+            if constexpr (QLO) {
+                const uint4 lv = *reinterpret_cast<const uint4 *>(stage + 16 * D + (16 * c + n) * D + 8 * g);
+                gacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(lv.x, lv.y, lv.z, lv.w), bg, gacc[c], 0, 0, 0);
+            }
+        }
+    }
+    // through the stage area (q is no longer read) into the QJL B layout:
+    // column n = row 16 c + n; k-slots 8g .. 8g + 7 = projections 8 (g % 2)
+    // .. + 7 as fp16 hi (g < 2) or fp16 remainder (g >= 2)
+    float *gqs = reinterpret_cast<float *>(stage);      // [RW][16]
+#pragma unroll
+    for (int c = 0; c < NCB; ++c)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) gqs[(16 * c + 4 * g + i) * QD + n] = gacc[c][i];
+#pragma unroll
+    for (int c = 0; c < NCB; ++c) {
+        const float *row = gqs + (16 * c + n) * QD + 8 * (g & 1);
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float g0 = row[2 * j] * a.alpha_c, g1 = row[2 * j + 1] * a.alpha_c;
+            w[j] = !QJL ? 0u : (g < 2 ? pack_h2(g0, g1) : pack_h2(g0 - (float)(_Float16)g0, g1 - (float)(_Float16)g1));
+        }
+        bgq[c] = as_half8(w[0], w[1], w[2], w[3]);
+    }
+    __syncthreads();   // byte LUT complete
+
+    // ── key range of this wave: causal limits of its rows ─────────────────
+    const int s_begin = split * (int)a.split_len;
+    int s_end = (int)imin64(a.S, (int64_t)s_begin + a.split_len);
+    int lim[NCB];
+    bool rowok[NCB];
+#pragma unroll
+    for (int c = 0; c < NCB; ++c) {
+        const int rho = row0 + 16 * c + n;
+        rowok[c] = rho < nrows_total;
+        lim[c] = (a.causal_offset >= 0) ? (int)imin64(a.causal_offset + (rowok[c] ? rho : 0) / a.G, 0x7fffffff)
+                                        : 0x7fffffff;
+    }
+    int full_end = s_end;
+    if (a.causal_offset >= 0) {
+        const int rlo = imin(row0, nrows_total - 1), rhi = imin(row0 + RW - 1, nrows_total - 1);
+        const int64_t lo_lim = a.causal_offset + rlo / a.G, hi_lim = a.causal_offset + rhi / a.G;
+        full_end = (int)imin64((int64_t)s_end, lo_lim + 1);
+        s_end = (int)imin64((int64_t)s_end, hi_lim + 1);
+    }
+    bool seq_bad;
+    const int64_t kv_base = (cache_seq(a, b, seq_bad) * a.Hkv + hk) * a.S;
+    DecBufs P;
+    P.kn = __builtin_amdgcn_make_buffer_rsrc((void *)(a.k_nib + kv_base * 16), (short)0, s_end * 16, kBufWord3);
+    P.vn = __builtin_amdgcn_make_buffer_rsrc((void *)(a.v_nib + kv_base * 16), (short)0, s_end * 16, kBufWord3);
+    P.kq = __builtin_amdgcn_make_buffer_rsrc((void *)(QJL ? a.k_qjl + kv_base * 2 : a.k_nib), (short)0,
+                                             QJL ? s_end * 2 : 0, kBufWord3);
+    P.kr = __builtin_amdgcn_make_buffer_rsrc((void *)(QJL ? a.k_norms + kv_base : (const float *)a.k_nib), (short)0,
+                                             QJL ? s_end * 4 : 0, kBufWord3);
+    const uint32_t laneoff = (uint32_t)(lane & 31) * 8u;
+    const uint32_t slane = (uint32_t)kSlutOff | laneoff;
+    const half8_t ones = as_half8(0x3C003C00u, 0u, 0x3C003C00u, 0u);
+    const unsigned char *lut = smem + kLutOff;
+
+    float4_t oacc[NCB][2], lacc[NCB];
+    float m_run[NCB];
+#pragma unroll
+    for (int c = 0; c < NCB; ++c) {
+        oacc[c][0] = oacc[c][1] = float4_t{0.f, 0.f, 0.f, 0.f};
+        lacc[c] = float4_t{0.f, 0.f, 0.f, 0.f};
+        m_run[c] = -INFINITY;
+    }
+
+    auto tile_step = [&](TileRaw32 &R, const int tt) {
+        const bool full = tt + kDecTile <= full_end;
+        float4_t acc[NCB][2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            // K pass: bytes 2s, 2s + 1 of the lane's dword are dims 8g + 4s .. + 3
+            const half8_t ak0 = pair_half8(*reinterpret_cast<const uint2 *>(lut + lut_addr(R.k[u], laneoff, 0)),
+                                           *reinterpret_cast<const uint2 *>(lut + lut_addr(R.k[u], laneoff, 1)));
+            const half8_t ak1 = pair_half8(*reinterpret_cast<const uint2 *>(lut + lut_addr(R.k[u], laneoff, 2)),
+                                           *reinterpret_cast<const uint2 *>(lut + lut_addr(R.k[u], laneoff, 3)));
+#pragma unroll
+            for (int c = 0; c < NCB; ++c) {
+                float4_t ac = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak0, bk[c][0], float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                if constexpr (QLO) ac = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak0, bkl[c][0], ac, 0, 0, 0);
+                ac = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak1, bk[c][1], ac, 0, 0, 0);
+                if constexpr (QLO) ac = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak1, bkl[c][1], ac, 0, 0, 0);
+                acc[c][u] = ac;
+            }
+            if (QJL) {
+                // k-slots 8g .. 8g + 7 take sign byte g % 2 (projections 8 (g % 2) ..)
+                const half8_t s8 = sign_halves(smem, R.sg[u], 8u * (uint32_t)(g & 1), slane);
+#pragma unroll
+                for (int c = 0; c < NCB; ++c) {
+                    const float4_t qacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(s8, bgq[c], float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[c][u][i] = __builtin_fmaf(dpp_quad_bcast(R.nr[u], i), qacc[i], acc[c][u][i]);
+                }
+            }
+        }
+        half8_t pb[NCB][2];
+#pragma unroll
+        for (int c = 0; c < NCB; ++c) {
+            float sc[8];
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) sc[4 * u + i] = acc[c][u][i] * qsr[c];
+            if (!full) {
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int tn = tt + 16 * u + 4 * g + i;
+                        if (tn >= s_end || tn > lim[c]) sc[4 * u + i] = -INFINITY;
+                    }
+            }
+            float mt = vmax3(vmax3(sc[0], sc[1], sc[2]), vmax3(sc[3], sc[4], sc[5]), vmax2(sc[6], sc[7]));
+            mt = max_over_groups(mt);
+            const bool need = mt > m_run[c] + 8.0f;
+            if (__builtin_amdgcn_ballot_w64(need)) {
+                const float f = need ? __builtin_amdgcn_exp2f(m_run[c] - mt) : 1.0f;
+                oacc[c][0] *= f;
+                oacc[c][1] *= f;
+                lacc[c] *= f;
+                m_run[c] = need ? mt : m_run[c];
+            }
+            const float m_use = (m_run[c] == -INFINITY) ? 0.0f : m_run[c];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const uint32_t p01 = cvt_pk_h2(__builtin_amdgcn_exp2f(sc[4 * u] - m_use), __builtin_amdgcn_exp2f(sc[4 * u + 1] - m_use));
+                const uint32_t p23 = cvt_pk_h2(__builtin_amdgcn_exp2f(sc[4 * u + 2] - m_use), __builtin_amdgcn_exp2f(sc[4 * u + 3] - m_use));
+                pb[c][u] = as_half8(p01, p01, p23, p23);
+                lacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb[c][u], lacc[c], 0, 0, 0);
+            }
+        }
+        // PV: pair bytes of tokens (4g, 4g + 1) and (4g + 2, 4g + 3) at dims
+        // 2n (low nibbles) and 2n + 1 (high nibbles)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const uint32_t b0 = R.v[4 * u], b1 = R.v[4 * u + 1], b2 = R.v[4 * u + 2], b3 = R.v[4 * u + 3];
+            const uint32_t ev01 = __builtin_amdgcn_ubfe(b0, 0, 4) | ((b1 & 0x0Fu) << 4);
+            const uint32_t ev23 = __builtin_amdgcn_ubfe(b2, 0, 4) | ((b3 & 0x0Fu) << 4);
+            const uint32_t od01 = (b0 >> 4) | (b1 & 0xF0u);
+            const uint32_t od23 = (b2 >> 4) | (b3 & 0xF0u);
+            const half8_t ae = pair_half8(*reinterpret_cast<const uint2 *>(lut + lut_addr(ev01, laneoff, 0)),
+                                          *reinterpret_cast<const uint2 *>(lut + lut_addr(ev23, laneoff, 0)));
+            const half8_t ao = pair_half8(*reinterpret_cast<const uint2 *>(lut + lut_addr(od01, laneoff, 0)),
+                                          *reinterpret_cast<const uint2 *>(lut + lut_addr(od23, laneoff, 0)));
+#pragma unroll
+            for (int c = 0; c < NCB; ++c) {
+                oacc[c][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ae, pb[c][u], oacc[c][0], 0, 0, 0);
+                oacc[c][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ao, pb[c][u], oacc[c][1], 0, 0, 0);
+            }
+        }
+    };
+
+    // every key tile, in order, with a two-slot ring of unconditional loads
+    // (past the split end they read 0 and touch no memory)
+    constexpr int stride = kDecTile;
+    TileRaw32 ring[2];
+    tile_load32<QJL>(ring[0], P, n, g, s_begin);
+    int tt0 = s_begin;
+    for (; tt0 + stride < s_end; tt0 += 2 * stride) {
+        __builtin_amdgcn_sched_barrier(0);
+        tile_load32<QJL>(ring[1], P, n, g, tt0 + stride);
+        __builtin_amdgcn_sched_barrier(0);
+        tile_step(ring[0], tt0);
+        __builtin_amdgcn_sched_barrier(0);
+        tile_load32<QJL>(ring[0], P, n, g, tt0 + 2 * stride);
+        __builtin_amdgcn_sched_barrier(0);
+        tile_step(ring[1], tt0 + stride);
+    }
+    if (tt0 < s_end) tile_step(ring[0], tt0);
+
+    // ── rows out (or split partials): oacc[c][p][i] is dim 8g + 2i + p ────
+    const int64_t unit = (b * a.Hkv + hk) * a.n_rchunks + rc;
+#pragma unroll
+    for (int c = 0; c < NCB; ++c) {
+        const int rho = row0 + 16 * c + n;
+        if (!rowok[c]) continue;
+        const float l = seq_bad ? __builtin_nanf("") : lacc[c][0];
+        float *o;
+        if (a.splits == 1) {
+            const int t = rho / a.G, hq = hk * a.G + (rho - t * a.G);
+            o = a.out + ((b * a.Hq + hq) * a.T + t) * D;
+        } else {
+            const int rr = wave * RW + 16 * c + n;
+            o = a.ws + ((unit * a.splits + split) * a.rows + rr) * (D + 2);
+            if (g == 0) { o[D] = m_run[c]; o[D + 1] = l; }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float e0 = oacc[c][0][i], e1 = oacc[c][1][i];
+            if (a.splits == 1) {
+                o[8 * g + 2 * i] = e0 / l;
+                o[8 * g + 2 * i + 1] = e1 / l;
+            } else {
+                o[8 * g + 2 * i] = e0;
+                o[8 * g + 2 * i + 1] = e1;
+            }
+        }
+    }
+}
+
 // ── launch planning ─────────────────────────────────────────────────────
 
 struct Plan {
     bool dec128;       // D == 128: decode kernel with 8 query rows per block
     bool prefill;      // D == 128 with many rows per kv head: prefill kernel
+    bool prefill32;    // D == 32 with many rows per kv head: head_dim-32 prefill kernel
     int rows, n_rchunks, splits, nw, ncopy;
     int spb;           // decode kernel: sequences sharing a block's 8 row slots
     int64_t split_len;
@@ -1759,8 +2128,10 @@ static Plan make_plan(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int D, b
     const int G = Hq / Hkv;
     const int cus = device_cus();
     p.prefill = (D == 128) && T * G > kPrefillMinRows;
+    p.prefill32 = (D == 32) && T * G > kPrefillMinRows;
     p.dec128 = (D == 128) && !p.prefill;
-    p.rows = p.prefill ? kPreWaves * 16 * (q32 ? 1 : kPreNcb) : (p.dec128 ? kDecRows : kRows);
+    p.rows = p.prefill ? kPreWaves * 16 * (q32 ? 1 : kPreNcb)
+                       : (p.prefill32 ? kP32Waves * 16 * (q32 ? 1 : 2) : (p.dec128 ? kDecRows : kRows));
     p.n_rchunks = (int)((T * G + p.rows - 1) / p.rows);
     // Short decode steps of many sequences (more (sequence, kv head) pairs
     // than CUs, at most 4 query rows each): two sequences share a block's 8
@@ -1768,15 +2139,15 @@ static Plan make_plan(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int D, b
     // idling any slot.
     p.spb = (p.dec128 && T * G <= kDecRows / 2 && B >= 2 && B * (int64_t)Hkv > cus) ? 2 : 1;
     const int64_t units = ((B + p.spb - 1) / p.spb) * (int64_t)Hkv * p.n_rchunks;
-    if (p.prefill) {
+    if (p.prefill || p.prefill32) {
         const int64_t tiles = (S + kDecTile - 1) / kDecTile;
         int64_t splits = clamp64((cus + units - 1) / (units > 0 ? units : 1), 1, (tiles / 16) > 1 ? tiles / 16 : 1);
         const int64_t tps = (tiles + splits - 1) / splits;
         p.splits = (int)splits;
         p.split_len = tps * kDecTile;
-        p.nw = kPreWaves;
+        p.nw = p.prefill ? kPreWaves : kP32Waves;
         p.ncopy = 32;
-        p.lds = kPreLdsBytes;
+        p.lds = p.prefill ? kPreLdsBytes : kP32LdsBytes;
     } else if (p.dec128) {
         const int64_t tiles = (S + kDecTile - 1) / kDecTile;
         int64_t splits = clamp64((cus + units - 1) / (units > 0 ? units : 1), 1, (tiles / 16) > 1 ? tiles / 16 : 1);
@@ -1909,6 +2280,16 @@ static int attn_run(const void *q, int q_dtype, const uint8_t *k_nib, const uint
         } else {
             if (qlo) hipLaunchKernelGGL((attn_prefill128_kernel<false, 1, 2, true>), grid, block, 0, as_stream(stream), a);
             else hipLaunchKernelGGL((attn_prefill128_kernel<false, kPreNcb, 2, false>), grid, block, 0, as_stream(stream), a);
+        }
+    } else if (p.prefill32) {
+        const bool qlo = q_dtype == OMNI_F32;
+        hipStream_t st = as_stream(stream);
+        if (with_qjl) {
+            if (qlo) hipLaunchKernelGGL((attn_prefill32_kernel<true, 1, true>), grid, block, 0, st, a);
+            else hipLaunchKernelGGL((attn_prefill32_kernel<true, 2, false>), grid, block, 0, st, a);
+        } else {
+            if (qlo) hipLaunchKernelGGL((attn_prefill32_kernel<false, 1, true>), grid, block, 0, st, a);
+            else hipLaunchKernelGGL((attn_prefill32_kernel<false, 2, false>), grid, block, 0, st, a);
         }
     } else if (p.dec128) {
         hipStream_t st = as_stream(stream);

@@ -211,6 +211,49 @@ def test_attn_head_dim_32_causal(device, B, Hq, Hkv, T, S):
     assert (got0.cpu() - want0).abs().max().item() <= 1e-6
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,T,S,causal,dtype", [
+    (2, 32, 8, 64, 600, True, torch.bfloat16),      # C5 at head_dim 32, scaled down
+    (1, 8, 1, 40, 3000, True, torch.bfloat16),      # one kv head: split-K + combine
+    (2, 16, 4, 37, 500, False, torch.float16),      # ragged rows (148 per kv head), no mask
+    (1, 32, 8, 20, 256, True, torch.float32),       # f32 q: fp16 remainder plane
+])
+@pytest.mark.parametrize("with_qjl", [True, False])
+def test_prefill_d32_matches_oracle(device, B, Hq, Hkv, T, S, causal, dtype, with_qjl):
+    """The head_dim-32 chunked-prefill MFMA kernel (more than 32 query rows
+    per kv head) against the generalized oracle on the projected recipe."""
+    uid = 17
+    print(f"[prefill d32] B={B} Hq={Hq} Hkv={Hkv} T={T} S={S} causal={causal} {dtype} qjl={with_qjl}", flush=True)
+    kn, kq, kr, vn, cb, P = _proj32_cache(B, Hkv, S, seed=90 + S, uid=uid)
+    q = (_data.query((B, Hq, T, 128), seed=91 + S, dtype=torch.float32) @ P).to(dtype)
+    off = S - T if causal else None
+    got = _run(device, q, kn, kq, kr, vn, cb, uid, with_qjl, causal_offset=off)
+    mask = _causal_mask(T, S, off) if causal else None
+    want = restate.fused_attn_python(q.float(), kn, kq, kr, vn, cb, uid, 1 / math.sqrt(32), with_qjl, mask=mask)
+    assert torch.isfinite(got).all()
+    _assert_close(got, want, f"prefill d32 B{B} Hq{Hq} Hkv{Hkv} T{T} S{S} {dtype} qjl{int(with_qjl)}")
+
+
+def test_prefill_d32_rotate_q_and_extreme_rows(device):
+    """In-kernel 32-point rotation with a sign flip, a sharp softmax (q x 200)
+    and rows far outside fp16 range on the head_dim-32 prefill kernel."""
+    B, Hq, Hkv, T, S, uid = 2, 16, 4, 24, 400, 8
+    kn, kq, kr, vn, cb, P = _proj32_cache(B, Hkv, S, seed=95, uid=uid)
+    q = (_data.query((B, Hq, T, 128), seed=96, dtype=torch.float32) @ P).to(torch.bfloat16)
+    s = _data.sign_flip(32)
+    got = _run(device, q, kn, kq, kr, vn, cb, uid, rotate_q=True, sign_flip=s.to(device), causal_offset=S - T)
+    want = restate.fused_attn_python(restate.rotate(q, s).float(), kn, kq, kr, vn, cb, uid, 1 / math.sqrt(32), True,
+                                     mask=_causal_mask(T, S, S - T))
+    _assert_close(got, want, "prefill d32 rotate_q")
+    q2 = q.float() * 200.0
+    q2[0, 0] *= 3e5
+    q2[1, 1] *= 1e-9
+    q2 = q2.to(torch.bfloat16)
+    got = _run(device, q2, kn, kq, kr, vn, cb, uid, scale=0.1)
+    want = restate.fused_attn_python(q2.float(), kn, kq, kr, vn, cb, uid, 0.1, True)
+    assert torch.isfinite(got).all()
+    _assert_close(got, want, "prefill d32 extreme rows")
+
+
 def test_attn_shared_codebook(device):
     kn, kq, kr, vn, cb = _cache(1, 2, 70, seed=24, user_id=0)
     cb1 = cb[0]
