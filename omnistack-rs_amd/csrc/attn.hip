@@ -1747,12 +1747,16 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
 //           or 2n + 1), whose LUT entries are MFMA-ready (hi, lo) pairs
 // Online softmax in the exp2 domain with P in fp16, summed by an MFMA
 // against ones, as in the other kernels.
-constexpr int kP32Waves = 8;
+#ifndef OMNI_P32_WAVES
+#define OMNI_P32_WAVES 8
+#endif
+constexpr int kP32Waves = OMNI_P32_WAVES;
 constexpr int kP32CbOff = kSlutOff + kSlutBytes;                          // 16 x (fp16 hi | remainder << 16)
 constexpr int kP32StageOff = kP32CbOff + 64;                               // per wave: q rows fp16 (+ remainder plane), then G q f32
-constexpr int kP32StageBytes = 32 * 32 * 2 * 2;
-constexpr int kP32QsrOff = kP32StageOff + kP32Waves * kP32StageBytes;     // per wave: 32 f32 score scales
-constexpr int kP32LdsBytes = kP32QsrOff + kP32Waves * 32 * 4;
+constexpr int kP32StageBytes = 64 * 32 * 2;
+constexpr int kP32Ncb = 4;                                                 // column blocks per wave for 16-bit q (f32 q: 2)
+constexpr int kP32QsrOff = kP32StageOff + kP32Waves * kP32StageBytes;     // per wave: 64 f32 score scales
+constexpr int kP32LdsBytes = kP32QsrOff + kP32Waves * 64 * 4;
 
 // One 32-token tile at D = 32 as loaded.
 struct TileRaw32 {
@@ -1794,7 +1798,8 @@ __device__ __forceinline__ float wht32_lane(float x, int lane) {
 template <bool QJL, int NCB, bool QLO>
 __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs a) {
     constexpr int D = 32, QD = 16, RW = 16 * NCB;       // rows per wave
-    static_assert(!QLO || NCB == 1, "the f32 remainder plane shares the stage area");
+    static_assert(RW * D * 2 * (QLO ? 2 : 1) <= kP32StageBytes && RW * QD * 4 <= kP32StageBytes,
+                  "q rows (and the f32 remainder plane), then G q, fit the wave's stage area");
     __shared__ __attribute__((aligned(16))) unsigned char smem[kP32LdsBytes];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1806,7 +1811,7 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
     const int nrows_total = (int)(a.T * a.G);
     const int row0 = rc * a.rows + wave * RW;
     uint16_t *stage = reinterpret_cast<uint16_t *>(smem + kP32StageOff + wave * kP32StageBytes);
-    float *qsr_l = reinterpret_cast<float *>(smem + kP32QsrOff) + wave * 32;
+    float *qsr_l = reinterpret_cast<float *>(smem + kP32QsrOff) + wave * 64;
 
     // ── codebook pairs and the sign table ───────────────────────────────
     {
@@ -1817,13 +1822,16 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
         *reinterpret_cast<uint32_t *>(smem + kP32CbOff + 4 * (lane & 15)) =
             (uint32_t)h | ((uint32_t)f32_to_f16_rne(c - f16_to_f32(h)) << 16);
     }
-    sign_table_store(smem, tid);      // 512 threads
+    if (tid < 512) sign_table_store(smem, tid);
 
     // ── this wave's query rows, two per pass (half-waves): (sign flip,)
-    //    WHT, round; per-row power-of-2 scale into fp16 range; fp16 stage ──
+    //    WHT, round; per-row power-of-2 scale into fp16 range; fp16 stage.
+    //    The score scale's sign goes into the staged rows (exact), so every
+    //    row's score scale qsr is >= 0 and the exponent takes it in an fma ──
     {
         const int e = lane & 31, half = lane >> 5;
         const bool flip = a.rotate_q && a.sign_flip && a.sign_flip[e] < 0;
+        const float ssign = a.qscale < 0.0f ? -1.0f : 1.0f;
         for (int rp = 0; rp < RW; rp += 2) {
             const int rr = rp + half;
             const int rho = row0 + rr;
@@ -1840,27 +1848,25 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
             int ex = 0;
             if (m > 0.0f && m < INFINITY) frexpf(m, &ex);
             const float sr = ldexpf(1.0f, 15 - imax(ex, -100));
-            const uint16_t x16 = f32_to_f16_rne(x * sr);
+            const float xs = ssign * x * sr;
+            const uint16_t x16 = f32_to_f16_rne(xs);
             stage[rr * D + e] = x16;
-            if constexpr (QLO) stage[16 * D + rr * D + e] = f32_to_f16_rne(x * sr - f16_to_f32(x16));
-            if (e == 0) qsr_l[rr] = a.qscale / sr;
+            if constexpr (QLO) stage[RW * D + rr * D + e] = f32_to_f16_rne(xs - f16_to_f32(x16));
+            if (e == 0) qsr_l[rr] = fabsf(a.qscale) / sr;
         }
     }
     __syncthreads();
 
-    // ── byte LUT (after the codebook pairs are visible) ───────────────────
+    // ── byte LUT (after the codebook pairs are visible): entry e, 16-byte
+    //    chunk k (two of its 32 copies) per item ───────────────────────────
     {
         const uint32_t *cbh = reinterpret_cast<const uint32_t *>(smem + kP32CbOff);
-        const uint32_t w0 = cbh[(tid >> 4) & 15];
-        uint32_t w1[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) w1[i] = cbh[(tid >> 8) + 2 * i];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int e = (tid >> 4) + 32 * i;
-            const uint32_t hp = __builtin_amdgcn_perm(w1[i], w0, 0x05040100u);
-            const uint32_t lp = __builtin_amdgcn_perm(w1[i], w0, 0x07060302u);
-            *reinterpret_cast<uint4 *>(smem + kLutOff + e * 256 + (tid & 15) * 16) = make_uint4(hp, lp, hp, lp);
+        for (int it = tid; it < 256 * 16; it += 64 * kP32Waves) {
+            const int e = it >> 4;
+            const uint32_t w0 = cbh[e & 15], w1 = cbh[e >> 4];
+            const uint32_t hp = __builtin_amdgcn_perm(w1, w0, 0x05040100u);
+            const uint32_t lp = __builtin_amdgcn_perm(w1, w0, 0x07060302u);
+            *reinterpret_cast<uint4 *>(smem + kLutOff + e * 256 + (it & 15) * 16) = make_uint4(hp, lp, hp, lp);
         }
     }
 
@@ -1874,7 +1880,7 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
             const uint2 w = *reinterpret_cast<const uint2 *>(stage + (16 * c + n) * D + 8 * g + 4 * s);
             bk[c][s] = as_half8(w.x, w.x, w.y, w.y);
             if constexpr (QLO) {
-                const uint2 wl = *reinterpret_cast<const uint2 *>(stage + 16 * D + (16 * c + n) * D + 8 * g + 4 * s);
+                const uint2 wl = *reinterpret_cast<const uint2 *>(stage + RW * D + (16 * c + n) * D + 8 * g + 4 * s);
                 bkl[c][s] = as_half8(wl.x, wl.x, wl.y, wl.y);
             }
         }
@@ -1895,7 +1901,7 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
             const uint4 qv = *reinterpret_cast<const uint4 *>(stage + (16 * c + n) * D + 8 * g);
             gacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(qv.x, qv.y, qv.z, qv.w), bg, gacc[c], 0, 0, 0);
             if constexpr (QLO) {
-                const uint4 lv = *reinterpret_cast<const uint4 *>(stage + 16 * D + (16 * c + n) * D + 8 * g);
+                const uint4 lv = *reinterpret_cast<const uint4 *>(stage + RW * D + (16 * c + n) * D + 8 * g);
                 gacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(lv.x, lv.y, lv.z, lv.w), bg, gacc[c], 0, 0, 0);
             }
         }
@@ -1955,12 +1961,14 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
     const unsigned char *lut = smem + kLutOff;
 
     float4_t oacc[NCB][2], lacc[NCB];
+    // running maximum (scaled, log2 domain) from -FLT_MAX: it serves as the
+    // exponent offset as is (the first finite maximum replaces it)
     float m_run[NCB];
 #pragma unroll
     for (int c = 0; c < NCB; ++c) {
         oacc[c][0] = oacc[c][1] = float4_t{0.f, 0.f, 0.f, 0.f};
         lacc[c] = float4_t{0.f, 0.f, 0.f, 0.f};
-        m_run[c] = -INFINITY;
+        m_run[c] = -__FLT_MAX__;
     }
 
     auto tile_step = [&](TileRaw32 &R, const int tt) {
@@ -1995,35 +2003,52 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
         half8_t pb[NCB][2];
 #pragma unroll
         for (int c = 0; c < NCB; ++c) {
+            // raw scores; the row scale qsr >= 0 enters each exponent's fma
             float sc[8];
 #pragma unroll
             for (int u = 0; u < 2; ++u)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) sc[4 * u + i] = acc[c][u][i] * qsr[c];
+                for (int i = 0; i < 4; ++i) sc[4 * u + i] = acc[c][u][i];
+            uint32_t dead = 0u;
             if (!full) {
 #pragma unroll
                 for (int u = 0; u < 2; ++u)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int tn = tt + 16 * u + 4 * g + i;
-                        if (tn >= s_end || tn > lim[c]) sc[4 * u + i] = -INFINITY;
+                        if (tn >= s_end || tn > lim[c]) {
+                            sc[4 * u + i] = -INFINITY;
+                            dead |= 1u << (4 * u + i);
+                        }
                     }
             }
-            float mt = vmax3(vmax3(sc[0], sc[1], sc[2]), vmax3(sc[3], sc[4], sc[5]), vmax2(sc[6], sc[7]));
-            mt = max_over_groups(mt);
-            const bool need = mt > m_run[c] + 8.0f;
-            if (__builtin_amdgcn_ballot_w64(need)) {
+            // the scaled maximum of a row is the scale times its raw maximum
+            // (rounding is monotonic and qsr >= 0); m_run is the same in the
+            // four lane groups of a row, so each lane tests its own maximum
+            // and the cross-group maximum is formed only when a lane rescales
+            const float mr = vmax3(vmax3(sc[0], sc[1], sc[2]), vmax3(sc[3], sc[4], sc[5]), vmax2(sc[6], sc[7]));
+            float mt = mr == -INFINITY ? -INFINITY : mr * qsr[c];
+            if (__builtin_amdgcn_ballot_w64(mt > m_run[c] + 8.0f)) {
+                mt = max_over_groups(mt);
+                const bool need = mt > m_run[c] + 8.0f;
                 const float f = need ? __builtin_amdgcn_exp2f(m_run[c] - mt) : 1.0f;
                 oacc[c][0] *= f;
                 oacc[c][1] *= f;
                 lacc[c] *= f;
                 m_run[c] = need ? mt : m_run[c];
             }
-            const float m_use = (m_run[c] == -INFINITY) ? 0.0f : m_run[c];
+            const float nm = -m_run[c];
+            float ex[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) ex[k] = __builtin_fmaf(sc[k], qsr[c], nm);
+            if (!full) {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) ex[k] = (dead >> k) & 1u ? -INFINITY : ex[k];
+            }
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
-                const uint32_t p01 = cvt_pk_h2(__builtin_amdgcn_exp2f(sc[4 * u] - m_use), __builtin_amdgcn_exp2f(sc[4 * u + 1] - m_use));
-                const uint32_t p23 = cvt_pk_h2(__builtin_amdgcn_exp2f(sc[4 * u + 2] - m_use), __builtin_amdgcn_exp2f(sc[4 * u + 3] - m_use));
+                const uint32_t p01 = cvt_pk_h2(__builtin_amdgcn_exp2f(ex[4 * u]), __builtin_amdgcn_exp2f(ex[4 * u + 1]));
+                const uint32_t p23 = cvt_pk_h2(__builtin_amdgcn_exp2f(ex[4 * u + 2]), __builtin_amdgcn_exp2f(ex[4 * u + 3]));
                 pb[c][u] = as_half8(p01, p01, p23, p23);
                 lacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb[c][u], lacc[c], 0, 0, 0);
             }
@@ -2131,7 +2156,7 @@ static Plan make_plan(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int D, b
     p.prefill32 = (D == 32) && T * G > kPrefillMinRows;
     p.dec128 = (D == 128) && !p.prefill;
     p.rows = p.prefill ? kPreWaves * 16 * (q32 ? 1 : kPreNcb)
-                       : (p.prefill32 ? kP32Waves * 16 * (q32 ? 1 : 2) : (p.dec128 ? kDecRows : kRows));
+                       : (p.prefill32 ? kP32Waves * 16 * (q32 ? 2 : kP32Ncb) : (p.dec128 ? kDecRows : kRows));
     p.n_rchunks = (int)((T * G + p.rows - 1) / p.rows);
     // Short decode steps of many sequences (more (sequence, kv head) pairs
     // than CUs, at most 4 query rows each): two sequences share a block's 8
@@ -2285,11 +2310,11 @@ static int attn_run(const void *q, int q_dtype, const uint8_t *k_nib, const uint
         const bool qlo = q_dtype == OMNI_F32;
         hipStream_t st = as_stream(stream);
         if (with_qjl) {
-            if (qlo) hipLaunchKernelGGL((attn_prefill32_kernel<true, 1, true>), grid, block, 0, st, a);
-            else hipLaunchKernelGGL((attn_prefill32_kernel<true, 2, false>), grid, block, 0, st, a);
+            if (qlo) hipLaunchKernelGGL((attn_prefill32_kernel<true, 2, true>), grid, block, 0, st, a);
+            else hipLaunchKernelGGL((attn_prefill32_kernel<true, kP32Ncb, false>), grid, block, 0, st, a);
         } else {
-            if (qlo) hipLaunchKernelGGL((attn_prefill32_kernel<false, 1, true>), grid, block, 0, st, a);
-            else hipLaunchKernelGGL((attn_prefill32_kernel<false, 2, false>), grid, block, 0, st, a);
+            if (qlo) hipLaunchKernelGGL((attn_prefill32_kernel<false, 2, true>), grid, block, 0, st, a);
+            else hipLaunchKernelGGL((attn_prefill32_kernel<false, kP32Ncb, false>), grid, block, 0, st, a);
         }
     } else if (p.dec128) {
         hipStream_t st = as_stream(stream);

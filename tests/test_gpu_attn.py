@@ -254,6 +254,20 @@ def test_prefill_d32_rotate_q_and_extreme_rows(device):
     _assert_close(got, want, "prefill d32 extreme rows")
 
 
+@pytest.mark.parametrize("scale", [-0.3, 0.0])
+def test_prefill_d32_negative_and_zero_scale(device, scale):
+    """The head_dim-32 prefill kernel folds the score scale's sign into the
+    query rows; a zero scale is a uniform softmax over the visible keys."""
+    B, Hq, Hkv, T, S, uid = 1, 16, 4, 40, 300, 4
+    kn, kq, kr, vn, cb, P = _proj32_cache(B, Hkv, S, seed=97, uid=uid)
+    q = (_data.query((B, Hq, T, 128), seed=98, dtype=torch.float32) @ P).to(torch.bfloat16)
+    off = S - T
+    got = _run(device, q, kn, kq, kr, vn, cb, uid, scale=scale, causal_offset=off)
+    want = restate.fused_attn_python(q.float(), kn, kq, kr, vn, cb, uid, scale, True, mask=_causal_mask(T, S, off))
+    assert torch.isfinite(got).all()
+    _assert_close(got, want, f"prefill d32 scale {scale}")
+
+
 def test_attn_shared_codebook(device):
     kn, kq, kr, vn, cb = _cache(1, 2, 70, seed=24, user_id=0)
     cb1 = cb[0]
