@@ -1392,6 +1392,9 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
     {
         const bool use_flip = a.rotate_q && a.sign_flip;
         const bool flip_lo = use_flip && a.sign_flip[lane] < 0, flip_hi = use_flip && a.sign_flip[64 + lane] < 0;
+        // the score scale's sign goes into the staged rows (exact), so every
+        // row's score scale is >= 0 and the exponent takes it in an fma
+        const float ssign = a.qscale < 0.0f ? -1.0f : 1.0f;
         for (int rr = 0; rr < RW; ++rr) {
             const int rho = row0 + rr;
             const bool ok = rho < nrows_total;
@@ -1414,16 +1417,17 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
             int ex = 0;
             if (m > 0.0f && m < INFINITY) { frexpf(m, &ex); }
             const float sr = ldexpf(1.0f, 15 - imax(ex, -100));   // m * sr in [2^14, 2^15) unless m < 2^-101
-            const uint16_t l16 = f32_to_f16_rne(lo * sr), h16 = f32_to_f16_rne(hi * sr);
+            const float los = ssign * lo * sr, his = ssign * hi * sr;
+            const uint16_t l16 = f32_to_f16_rne(los), h16 = f32_to_f16_rne(his);
             reinterpret_cast<uint16_t *>(stage)[rr * D + lane] = l16;
             reinterpret_cast<uint16_t *>(stage)[rr * D + 64 + lane] = h16;
             if constexpr (QLO) {
                 // second plane: fp16 remainder of the scaled f32 row
                 uint16_t *lop = reinterpret_cast<uint16_t *>(stage) + 16 * D;
-                lop[rr * D + lane] = f32_to_f16_rne(lo * sr - f16_to_f32(l16));
-                lop[rr * D + 64 + lane] = f32_to_f16_rne(hi * sr - f16_to_f32(h16));
+                lop[rr * D + lane] = f32_to_f16_rne(los - f16_to_f32(l16));
+                lop[rr * D + 64 + lane] = f32_to_f16_rne(his - f16_to_f32(h16));
             }
-            if (lane == 0) qsr_l[rr] = a.qscale / sr;
+            if (lane == 0) qsr_l[rr] = fabsf(a.qscale) / sr;
         }
     }
     __syncthreads();
@@ -1527,6 +1531,20 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
             bgl[c][s] = as_half8(wl[0], wl[1], wl[2], wl[3]);
         }
     }
+    // the QJL B operands go back to the stage area as lane-linear images and
+    // are read there every tile: held in registers they push the loop past
+    // the register file
+    {
+        uint4 *img = reinterpret_cast<uint4 *>(stage);
+#pragma unroll
+        for (int c = 0; c < NCB; ++c)
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                img[((c * 2 + s) * 2) * 64 + lane] = __builtin_bit_cast(uint4, bgq[c][s]);
+                img[((c * 2 + s) * 2 + 1) * 64 + lane] = __builtin_bit_cast(uint4, bgl[c][s]);
+            }
+    }
+    const uint32_t qimg_off = (uint32_t)(stage - smem) + (uint32_t)lane * 16u;
     __syncthreads();   // byte LUT complete
 
     // ── key range of this wave: causal limits of its rows ─────────────────
@@ -1568,13 +1586,15 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
     const unsigned char *lut = smem + kLutOff;
 
     float4_t oacc[NCB][8], lacc[NCB];
+    // running maximum (scaled, log2 domain) from -FLT_MAX: it serves as the
+    // exponent offset as is (the first finite maximum replaces it)
     float m_run[NCB];
 #pragma unroll
     for (int c = 0; c < NCB; ++c) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) oacc[c][k] = float4_t{0.f, 0.f, 0.f, 0.f};
         lacc[c] = float4_t{0.f, 0.f, 0.f, 0.f};
-        m_run[c] = -INFINITY;
+        m_run[c] = -__FLT_MAX__;
     }
 
     auto tile_step = [&](TileRaw &R, const int tt) {
@@ -1603,14 +1623,20 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
             }
             if (QJL) {
                 // signs . (G q as fp16 hi + fp16 remainder), then + norm * that
-                // (norm of token 4g + i: a quad broadcast, fp32)
+                // (norm of token 4g + i: a quad broadcast, fp32); the B images
+                // are read from the stage area (the opaque offset keeps the
+                // reads in the loop)
+                uint32_t qo = qimg_off;
+                asm volatile("" : "+v"(qo));
 #pragma unroll
                 for (int s = 0; s < 2; ++s) {
                     const half8_t s8 = sign_halves(smem, s ? R.sg[u].y : R.sg[u].x, 8u * g, slane);
 #pragma unroll
                     for (int c = 0; c < NCB; ++c) {
-                        qacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(s8, bgq[c][s], qacc[c], 0, 0, 0);
-                        qacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(s8, bgl[c][s], qacc[c], 0, 0, 0);
+                        const uint4 vq = *reinterpret_cast<const uint4 *>(smem + qo + ((c * 2 + s) * 2) * 1024);
+                        const uint4 vl = *reinterpret_cast<const uint4 *>(smem + qo + ((c * 2 + s) * 2 + 1) * 1024);
+                        qacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(s8, __builtin_bit_cast(half8_t, vq), qacc[c], 0, 0, 0);
+                        qacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(s8, __builtin_bit_cast(half8_t, vl), qacc[c], 0, 0, 0);
                     }
                 }
 #pragma unroll
@@ -1624,36 +1650,52 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
         half8_t pb[NCB][2];
 #pragma unroll
         for (int c = 0; c < NCB; ++c) {
+            // raw scores; the row scale qsr >= 0 enters each exponent's fma
             float sc[8];
 #pragma unroll
             for (int u = 0; u < 2; ++u)
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    sc[4 * u + i] = acc[c][u][i] * qsr[c];
+                for (int i = 0; i < 4; ++i) sc[4 * u + i] = acc[c][u][i];
+            uint32_t dead = 0u;
             if (!full) {
 #pragma unroll
                 for (int u = 0; u < 2; ++u)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int tn = tt + 16 * u + 4 * g + i;
-                        if (tn >= s_end || tn > lim[c]) sc[4 * u + i] = -INFINITY;
+                        if (tn >= s_end || tn > lim[c]) {
+                            sc[4 * u + i] = -INFINITY;
+                            dead |= 1u << (4 * u + i);
+                        }
                     }
             }
-            float mt = vmax3(vmax3(sc[0], sc[1], sc[2]), vmax3(sc[3], sc[4], sc[5]), vmax2(sc[6], sc[7]));
-            mt = max_over_groups(mt);
-            const bool need = mt > m_run[c] + 8.0f;
-            if (__builtin_amdgcn_ballot_w64(need)) {
+            // the scaled maximum of a row is the scale times its raw maximum
+            // (rounding is monotonic and qsr >= 0); m_run is the same in the
+            // four lane groups of a row, so each lane tests its own maximum
+            // and the cross-group maximum is formed only when a lane rescales
+            const float mr = vmax3(vmax3(sc[0], sc[1], sc[2]), vmax3(sc[3], sc[4], sc[5]), vmax2(sc[6], sc[7]));
+            float mt = mr == -INFINITY ? -INFINITY : mr * qsr[c];
+            if (__builtin_amdgcn_ballot_w64(mt > m_run[c] + 8.0f)) {
+                mt = max_over_groups(mt);
+                const bool need = mt > m_run[c] + 8.0f;
                 const float f = need ? __builtin_amdgcn_exp2f(m_run[c] - mt) : 1.0f;
 #pragma unroll
                 for (int k = 0; k < 8; ++k) oacc[c][k] *= f;
                 lacc[c] *= f;
                 m_run[c] = need ? mt : m_run[c];
             }
-            const float m_use = (m_run[c] == -INFINITY) ? 0.0f : m_run[c];
+            const float nm = -m_run[c];
+            float ex[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) ex[k] = __builtin_fmaf(sc[k], qsr[c], nm);
+            if (!full) {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) ex[k] = (dead >> k) & 1u ? -INFINITY : ex[k];
+            }
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
-                const uint32_t p01 = cvt_pk_h2(__builtin_amdgcn_exp2f(sc[4 * u] - m_use), __builtin_amdgcn_exp2f(sc[4 * u + 1] - m_use));
-                const uint32_t p23 = cvt_pk_h2(__builtin_amdgcn_exp2f(sc[4 * u + 2] - m_use), __builtin_amdgcn_exp2f(sc[4 * u + 3] - m_use));
+                const uint32_t p01 = cvt_pk_h2(__builtin_amdgcn_exp2f(ex[4 * u]), __builtin_amdgcn_exp2f(ex[4 * u + 1]));
+                const uint32_t p23 = cvt_pk_h2(__builtin_amdgcn_exp2f(ex[4 * u + 2]), __builtin_amdgcn_exp2f(ex[4 * u + 3]));
                 pb[c][u] = as_half8(p01, p01, p23, p23);
                 lacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb[c][u], lacc[c], 0, 0, 0);
             }
