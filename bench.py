@@ -18,7 +18,7 @@ C3's byte count (the device's achievable read rate, for comparison with
 `value`); the reference's CPU path (the oracle restatement) timed on a
 bounded C3 sample on this host.
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 5]
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--only c3,c2,c2pool,c4,c5,c5d32,calib] [--no-cpu]
 Prints one JSON line on stdout; progress goes to stderr.
 """
 from __future__ import annotations
@@ -44,9 +44,9 @@ BYTES_PER_TOKEN_HEAD = 64 + 8 + 4 + 64     # K nibbles + K signs + K norm (f32) 
 # (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch) over this script, each
 # scaled by what the counter reads for the 256 MiB calibration copy below
 # (FETCH_SIZE reads half the copied bytes -> x2.0; WRITE_SIZE reads them
-# exactly -> x1.0).  Recorded in profiles/attn_decode128_c3.md; re-measure
+# exactly -> x1.0).  Recorded in profiles/bench_driver_c3.md; re-measure
 # after any change to the decode kernel.
-C3_TRAFFIC = {"fetch_kib": 143655.5, "fetch_scale": 2.0, "write_kib": 512.0, "write_scale": 1.0}
+C3_TRAFFIC = {"fetch_kib": 143651.0, "fetch_scale": 2.0, "write_kib": 512.0, "write_scale": 1.0}
 
 
 def log(msg: str) -> None:
