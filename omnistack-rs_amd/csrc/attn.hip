@@ -27,6 +27,7 @@
 
 #include <atomic>
 #include <mutex>
+#include <type_traits>
 
 #include "omni_common.h"
 
@@ -1019,9 +1020,16 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
             int ex = 0;
             if (m > 0.0f && m < INFINITY) frexpf(m, &ex);
             const float sr = ldexpf(1.0f, 15 - imax(ex, -100));     // 2^k stays finite for tiny rows
-            qs[wave * D + lane] = row_ok ? lo * sr : 0.0f;
-            qs[wave * D + 64 + lane] = row_ok ? hi * sr : 0.0f;
-            if (lane == 0) reinterpret_cast<float *>(smem + kDecCscOff)[wave] = a.qscale / sr;
+            // the score scale's sign goes into the staged row (exact), so the
+            // row's factor |scale| log2(e) / 2^k >= 0 maps raw scores
+            // monotonically.  A factor below 2^-126 (zero included) is raised
+            // to it: raw scores stay below 2^40, so no exponent moves by more
+            // than 2^-86, and a masked key's -inf times the factor stays -inf.
+            const float ssr = a.qscale < 0.0f ? -sr : sr;
+            qs[wave * D + lane] = row_ok ? lo * ssr : 0.0f;
+            qs[wave * D + 64 + lane] = row_ok ? hi * ssr : 0.0f;
+            const float cf = fabsf(a.qscale) / sr;
+            if (lane == 0) reinterpret_cast<float *>(smem + kDecCscOff)[wave] = cf < 0x1p-126f ? 0x1p-126f : cf;
         }
         // MFMA operand images of this row (read back by the same wave):
         //   lanes 0-31, quad j = dims 4j..4j+3 of 2^k q: B slots
@@ -1145,6 +1153,12 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     // still gives exp2(-inf - m) = 0, and the first finite maximum replaces
     // it (scaling the empty accumulators by exp2(-FLT_MAX - mt) = 0)
     float m_run = -__FLT_MAX__;
+    // Exponents are fma(raw, csc, -m_run): exact products against a rounded
+    // maximum, which keeps relative weights exact but puts an error of up to
+    // half an ulp of m_run on every exponent.  Once any row's |m_run| reaches
+    // 2^13 (that error would pass 2^-11) the wave rounds each logit first,
+    // as the reference does (wave-uniform, set at most once).
+    bool round_first = false;
 
     // One 32-token tile: scores, online softmax, PV.
     auto tile_step = [&](TileRaw &R, const int tt, const int tseq) {
@@ -1176,8 +1190,9 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
                 // nor the output.
                 float v = acc[i];
                 if (QJL) v = __builtin_fmaf(dpp_quad_bcast(R.nr[u], i), qacc[i], v);
-                // columns n and n + 8 (hi and lo parts of row n) both get the sum
-                sc[4 * u + i] = (v + __uint_as_float(dpp_row_ror8(__float_as_uint(v)))) * csc;
+                // columns n and n + 8 (hi and lo parts of row n) both get the
+                // raw sum; the row's factor csc >= 0 enters each exponent's fma
+                sc[4 * u + i] = v + __uint_as_float(dpp_row_ror8(__float_as_uint(v)));
             }
         }
         if (!full) {
@@ -1190,12 +1205,15 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
                 }
         }
 
-        // online softmax (exp2 domain), lazy rescale.  Logits are rounded
-        // before the max is taken, so every exponent below is <= 8 exactly.
-        // m_run is the same in the four lane groups of a row (it only ever
-        // takes a cross-group maximum), so each lane tests its own 8 scores
-        // and the cross-group maximum is formed only when some lane rescales.
-        float mt = vmax3(vmax3(sc[0], sc[1], sc[2]), vmax3(sc[3], sc[4], sc[5]), vmax2(sc[6], sc[7]));
+        // online softmax (exp2 domain), lazy rescale.  The scaled maximum of
+        // the lane's scores is csc times their raw maximum (rounding is
+        // monotonic and csc >= 0), so every exponent below is at most 8 plus
+        // the rounding of one product.  m_run is the same in the four lane
+        // groups of a row (it only ever takes a cross-group maximum), so each
+        // lane tests its own maximum and the cross-group maximum is formed
+        // only when some lane rescales.
+        const float mr = vmax3(vmax3(sc[0], sc[1], sc[2]), vmax3(sc[3], sc[4], sc[5]), vmax2(sc[6], sc[7]));
+        float mt = mr == -INFINITY ? -INFINITY : mr * csc;
         if (__builtin_amdgcn_ballot_w64(mt > m_run + 8.0f)) {
             mt = max_over_groups(mt);
             const bool need = mt > m_run + 8.0f;
@@ -1204,16 +1222,26 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
             for (int k = 0; k < 8; ++k) oacc[k] *= f;
             lacc_sum *= f;
             m_run = need ? mt : m_run;
+            round_first = round_first || __builtin_amdgcn_ballot_w64(fabsf(m_run) >= 8192.0f && m_run > -__FLT_MAX__);
         }
-        const float m_use = m_run;
+        const float nm = -m_run;
         // lanes n and n + 8 hold the same scores: columns 0-7 exponentiate the
         // tile's first 16 tokens, columns 8-15 the last 16, and the halves
         // trade places by a row rotation (B columns 8-15 feed output columns
-        // that are never read, so what they hold does not matter)
-        const float e0 = lo_col ? sc[4] : sc[0], e1 = lo_col ? sc[5] : sc[1];
-        const float e2 = lo_col ? sc[6] : sc[2], e3 = lo_col ? sc[7] : sc[3];
-        const uint32_t my01 = cvt_pk_h2(__builtin_amdgcn_exp2f(e0 - m_use), __builtin_amdgcn_exp2f(e1 - m_use));
-        const uint32_t my23 = cvt_pk_h2(__builtin_amdgcn_exp2f(e2 - m_use), __builtin_amdgcn_exp2f(e3 - m_use));
+        // that are never read, so what they hold does not matter).  csc >=
+        // 2^-126, so masked keys give exp2(-inf) = 0.
+        float ex[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) ex[k] = lo_col ? sc[4 + k] : sc[k];
+        if (round_first) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) ex[k] = ex[k] * csc;
+        }
+        const float cm = round_first ? 1.0f : csc;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) ex[k] = __builtin_fmaf(ex[k], cm, nm);
+        const uint32_t my01 = cvt_pk_h2(__builtin_amdgcn_exp2f(ex[0]), __builtin_amdgcn_exp2f(ex[1]));
+        const uint32_t my23 = cvt_pk_h2(__builtin_amdgcn_exp2f(ex[2]), __builtin_amdgcn_exp2f(ex[3]));
         const uint32_t ot01 = dpp_row_ror8(my01), ot23 = dpp_row_ror8(my23);
         half8_t pb[2];
         pb[0] = as_half8(my01, my01, my23, my23);
@@ -1293,34 +1321,53 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     float *ob = reinterpret_cast<float *>(smem);                     // [nw][kDecRows][kObStride]
     float *wm = reinterpret_cast<float *>(smem + kDecSlabBytes);     // [nw][kDecRows] running max
     float *wl = wm + kDecWaves * kDecRows;                           // [nw][kDecRows] denominators
-    if (!lo_col) {
-        if (g == 0) {
-            wm[wave * kDecRows + n] = m_run;
-            wl[wave * kDecRows + n] = lacc_sum[0];
+    // Each wave's first tile is its own index, so waves at or past the tile
+    // count claimed nothing: only the first min(nw, ntiles) slabs (at least
+    // one, so an empty split still merges one empty state) hold data.
+    const int nw_act = ntiles < 1 ? 1 : (ntiles < nw ? ntiles : nw);
+    {
+        // lane coordinates recomputed here (opaque), so no address of this
+        // step is kept live across the main loop
+        int le = lane;
+        asm volatile("" : "+v"(le));
+        const int ne = le & 15, ge = le >> 4;
+        if (ne < kDecRows && wave < nw_act) {
+            if (ge == 0) {
+                wm[wave * kDecRows + ne] = m_run;
+                wl[wave * kDecRows + ne] = lacc_sum[0];
+            }
+            float *dst = ob + (wave * kDecRows + ne) * kObStride;
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) dst[8 * (4 * ge + i) + k] = oacc[k][i];
         }
-        float *dst = ob + (wave * kDecRows + n) * kObStride;
-#pragma unroll
-        for (int k = 0; k < 8; ++k)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) dst[8 * (4 * g + i) + k] = oacc[k][i];
     }
     __syncthreads();
     const int64_t unit = (b * a.Hkv + hk) * a.n_rchunks + rc;
-    for (int s = tid; s < kDecRows * D; s += blockDim.x) {
-        const int rr = s / D, d = s % D;
-        if (!row_valid(rr)) continue;
-        const int rr_rho = row_rho(rr);
-        const int64_t rr_b = b + row_seq(rr);
-        float rmx = -INFINITY;
-        for (int w = 0; w < nw; ++w) rmx = fmaxf(rmx, wm[w * kDecRows + rr]);
+    // (max, denominator, output element) of row rr, dim d over the first
+    // `cnt` slabs in wave order; a compile-time count unrolls the loops
+    auto merge = [&](auto cnt, int rr, int d, float &rmx, float &lsum, float &osum) {
+        rmx = -INFINITY;
+        for (int w = 0; w < cnt; ++w) rmx = fmaxf(rmx, wm[w * kDecRows + rr]);
         const float rmu = (rmx == -INFINITY) ? 0.0f : rmx;
-        float lsum = 0.0f, osum = 0.0f;
-        for (int w = 0; w < nw; ++w) {
+        lsum = 0.0f;
+        osum = 0.0f;
+        for (int w = 0; w < cnt; ++w) {
             // merge weights lie in [0, 1]; the hardware exp2 is within 1 ulp
             const float f = __builtin_amdgcn_exp2f(wm[w * kDecRows + rr] - rmu);
             lsum = __builtin_fmaf(f, wl[w * kDecRows + rr], lsum);
             osum = __builtin_fmaf(f, ob[(w * kDecRows + rr) * kObStride + d], osum);
         }
+    };
+    for (int s = tid; s < kDecRows * D; s += blockDim.x) {
+        const int rr = s / D, d = s % D;
+        if (!row_valid(rr)) continue;
+        const int rr_rho = row_rho(rr);
+        const int64_t rr_b = b + row_seq(rr);
+        float rmx, lsum, osum;
+        if (nw_act == nw) merge(std::integral_constant<int, nw>{}, rr, d, rmx, lsum, osum);
+        else merge(nw_act, rr, d, rmx, lsum, osum);
         if (a.seq_index != nullptr) {
             bool bad;
             (void)cache_seq(a, rr_b, bad);
@@ -1596,6 +1643,10 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
         lacc[c] = float4_t{0.f, 0.f, 0.f, 0.f};
         m_run[c] = -__FLT_MAX__;
     }
+    // exponents are fma(raw, qsr, -m_run): exact products against a rounded
+    // maximum, so each carries up to half an ulp of m_run; once any row's
+    // |m_run| reaches 2^13 the wave rounds each logit first (wave-uniform)
+    bool round_first = false;
 
     auto tile_step = [&](TileRaw &R, const int tt) {
         const bool full = tt + kDecTile <= full_end;
@@ -1683,11 +1734,18 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
                 for (int k = 0; k < 8; ++k) oacc[c][k] *= f;
                 lacc[c] *= f;
                 m_run[c] = need ? mt : m_run[c];
+                round_first = round_first ||
+                              __builtin_amdgcn_ballot_w64(fabsf(m_run[c]) >= 8192.0f && m_run[c] > -__FLT_MAX__);
             }
             const float nm = -m_run[c];
+            if (round_first) {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) sc[k] = sc[k] * qsr[c];
+            }
+            const float qm = round_first ? 1.0f : qsr[c];
             float ex[8];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) ex[k] = __builtin_fmaf(sc[k], qsr[c], nm);
+            for (int k = 0; k < 8; ++k) ex[k] = __builtin_fmaf(sc[k], qm, nm);
             if (!full) {
 #pragma unroll
                 for (int k = 0; k < 8; ++k) ex[k] = (dead >> k) & 1u ? -INFINITY : ex[k];
@@ -1747,9 +1805,14 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
 
     // ── rows out (or split partials) ──────────────────────────────────────
     const int64_t unit = (b * a.Hkv + hk) * a.n_rchunks + rc;
+    // lane coordinates recomputed here (opaque), so no address of this step
+    // is kept live across the main loop
+    int le = lane;
+    asm volatile("" : "+v"(le));
+    const int ne = le & 15, ge = le >> 4;
 #pragma unroll
     for (int c = 0; c < NCB; ++c) {
-        const int rho = row0 + 16 * c + n;
+        const int rho = row0 + 16 * c + ne;
         if (!rowok[c]) continue;
         const float l = seq_bad ? __builtin_nanf("") : lacc[c][0];
         if (a.splits == 1) {
@@ -1758,15 +1821,15 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
 #pragma unroll
             for (int k = 0; k < 8; ++k)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) o[8 * (4 * g + i) + k] = oacc[c][k][i] / l;
+                for (int i = 0; i < 4; ++i) o[8 * (4 * ge + i) + k] = oacc[c][k][i] / l;
         } else {
-            const int rr = wave * RW + 16 * c + n;
+            const int rr = wave * RW + 16 * c + ne;
             float *wp = a.ws + ((unit * a.splits + split) * a.rows + rr) * (D + 2);
 #pragma unroll
             for (int k = 0; k < 8; ++k)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) wp[8 * (4 * g + i) + k] = oacc[c][k][i];
-            if (g == 0) { wp[D] = m_run[c]; wp[D + 1] = l; }
+                for (int i = 0; i < 4; ++i) wp[8 * (4 * ge + i) + k] = oacc[c][k][i];
+            if (ge == 0) { wp[D] = m_run[c]; wp[D + 1] = l; }
         }
     }
 }
@@ -2012,6 +2075,10 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
         lacc[c] = float4_t{0.f, 0.f, 0.f, 0.f};
         m_run[c] = -__FLT_MAX__;
     }
+    // exponents are fma(raw, qsr, -m_run): exact products against a rounded
+    // maximum, so each carries up to half an ulp of m_run; once any row's
+    // |m_run| reaches 2^13 the wave rounds each logit first (wave-uniform)
+    bool round_first = false;
 
     auto tile_step = [&](TileRaw32 &R, const int tt) {
         const bool full = tt + kDecTile <= full_end;
@@ -2078,11 +2145,18 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
                 oacc[c][1] *= f;
                 lacc[c] *= f;
                 m_run[c] = need ? mt : m_run[c];
+                round_first = round_first ||
+                              __builtin_amdgcn_ballot_w64(fabsf(m_run[c]) >= 8192.0f && m_run[c] > -__FLT_MAX__);
             }
             const float nm = -m_run[c];
+            if (round_first) {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) sc[k] = sc[k] * qsr[c];
+            }
+            const float qm = round_first ? 1.0f : qsr[c];
             float ex[8];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) ex[k] = __builtin_fmaf(sc[k], qsr[c], nm);
+            for (int k = 0; k < 8; ++k) ex[k] = __builtin_fmaf(sc[k], qm, nm);
             if (!full) {
 #pragma unroll
                 for (int k = 0; k < 8; ++k) ex[k] = (dead >> k) & 1u ? -INFINITY : ex[k];

@@ -162,14 +162,15 @@ __global__ __launch_bounds__(kRowsPerBlock) void encode_kernel(
         v[d] = v[d] - cval;  // residual e_d (fp32), quantize.py:580
     }
 
-    // ||e||_2: fp32 squares (as the reference's fp32 norm forms them) summed
-    // in fp64 and rounded once; a sum beyond the fp32 range is +inf, where the
+    // ||e||_2: the exact squares (fp32 x fp32 fits fp64) summed in fp64 and
+    // rounded once; a sum beyond the fp32 range is +inf, where the
     // reference's fp32 accumulation overflows.
     double ss = 0.0;
     float abs_sum = 0.0f;
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-        ss += (double)__fmul_rn(v[d], v[d]);
+        const double ed = (double)v[d];
+        ss = __builtin_fma(ed, ed, ss);
         abs_sum += fabsf(v[d]);
     }
     const float nrm = ss > 3.4028234663852886e38 ? INFINITY : (float)sqrt(ss);
@@ -251,9 +252,10 @@ __device__ __forceinline__ uint32_t cvt_pk_f16(float x, float y) {
 //     16-bit pattern, built exactly (brute-force first-index argmin with the
 //     NaN rule) by code_table_kernel into the caller's workspace.
 //   * QJL projections P = E G^T on v_mfma_f32_16x16x32_bf16: each residual
-//     is split exactly into three truncated bf16 parts (8 + 8 + 8 bits), G is
-//     exactly +-1, so the only error is fp32 accumulation, bounded by
-//     1024 * 2^-24 * sum|e| (+ 2^-100 for flushed denormals).  Signs outside
+//     is split into two round-to-nearest bf16 parts (the dropped remainder is
+//     below 2^-16 |e|), G is exactly +-1, so the products are exact and the
+//     error (fp32 accumulation plus the remainder) is bounded by
+//     1312 * 2^-24 * sum|e| (+ 2^-100 for flushed denormals).  Signs outside
 //     the bound are certain; the rare rest are recomputed in fp64 with
 //     compensated sums.  Rows with a non-finite residual take the
 //     order-free sign of the reference's fp32 sum (NaN if it meets NaN or
@@ -448,26 +450,32 @@ __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
     const float *cent = reinterpret_cast<const float *>(smem + kEncCentOff);
     const uint32_t *gbits = reinterpret_cast<const uint32_t *>(smem + kEncGbitsOff);
 
-    for (int64_t v0 = v_begin + 16 * wave; v0 < v_end; v0 += 16 * kEncWaves) {
-        // row of lane n: virtual v = v0 + n (clamped) -> (b, t) -> memory row
-        const int64_t b0 = v0 / a.T;                         // uniform
-        int64_t t = (v0 - b0 * a.T) + (v0 + n < v_end ? n : (v_end - 1 - v0));
+    // row of lane n in the 16-row group at virtual row v (< v_end): v + n
+    // (clamped) -> (b, t) -> memory row
+    auto group_row = [&](int64_t v) {
+        const int64_t b0 = v / a.T;                          // uniform
+        int64_t t = (v - b0 * a.T) + (v + n < v_end ? n : (v_end - 1 - v));
         int64_t bq = b0;
         while (t >= a.T) { t -= a.T; ++bq; }                 // at most 16 / T + 1 steps
-        const int64_t mrow = (bq * a.H + h) * a.T + t;
+        return (bq * a.H + h) * a.T + t;
+    };
+    auto load_group = [&](uint4 (&w)[4], int64_t row) {
+        const uint4 *src = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(a.x) + row * 128);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) w[s] = src[4 * s + g];
+    };
+    // One 16-row group: w4 holds lane (n, g)'s four 16-byte chunks of row
+    // mrow (virtual row v0 + n).
+    auto encode_group = [&](const uint4 (&w4)[4], const int64_t mrow, const int64_t v0) {
         const bool store = v0 + n < v_end && g == 0;
 
-        // load (8 x 16-bit per chunk), flip signs on the raw words, widen
+        // flip signs on the raw words (8 x 16-bit per chunk), widen
         float x[4][8];
         uint32_t nib[4];
         double ss = 0.0;
         float as = 0.0f;
         {
-            const uint4 *src = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(a.x) + mrow * 128);
             const uint4 *fmk = reinterpret_cast<const uint4 *>(smem + kEncFlipOff) + lane * 4;
-            uint4 w4[4];
-#pragma unroll
-            for (int s = 0; s < 4; ++s) w4[s] = src[4 * s + g];
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
                 const uint4 f = ROT ? fmk[s] : make_uint4(0u, 0u, 0u, 0u);
@@ -563,69 +571,84 @@ __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
         for (int s = 0; s < 4; ++s)
 #pragma unroll
             for (int i = 0; i < 8; ++i) cv[s][i] = cent[vb[s][i]];
-        // residuals, norm and |e| partial sums
+        // residuals, norm (fp64 sum of the exact squares) and |e| partial sums
 #pragma unroll
         for (int s = 0; s < 4; ++s)
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const float e = x[s][i] - cv[s][i];
                 x[s][i] = e;
-                ss += (double)__fmul_rn(e, e);
+                const double ed = (double)e;
+                ss = __builtin_fma(ed, ed, ss);
                 as += fabsf(e);
             }
         ss = xlane_sum_f64<16>(ss);
         ss = xlane_sum_f64<32>(ss);
         as = xlane_sum_f32(as);
 
-        // projections: P^T = G . E^T on MFMA, three exact bf16 parts of E
+        // projections: P^T = G . E^T on MFMA with each residual as two
+        // round-to-nearest bf16 parts, e = h + m + l: h = bf16(e), m =
+        // bf16(e - h) (e - h is exact), |l| <= 2^-16 |e|.  G is exactly +-1,
+        // so the products are exact and the MFMA sum of G (h + m) is within
+        // 1024 * 2^-24 * sum(|h| + |m|) <= 1032.1 * 2^-24 * sum|e| of its exact
+        // value (fp32 accumulation of 256 terms in any order, rounding to
+        // nearest or toward zero); sum|l| adds 256 * 2^-24 * sum|e|, and the
+        // fp32 sum `as` is within a relative 127 * 2^-24 of sum|e|:
+        // 1312 * 2^-24 * as bounds the total.  Rows with sum|e| >= 2^127
+        // (where a part could round to infinity) take the exact path below.
         float4_t acc[4];
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb) acc[cb] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            uint32_t ph[4], pm[4], pl[4];
+            uint32_t ph[4], pm[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
+                typedef __bf16 bf2_t __attribute__((ext_vector_type(2)));
+                typedef float f2_t __attribute__((ext_vector_type(2)));
                 const float e0 = x[s][2 * j], e1 = x[s][2 * j + 1];
-                const float r0 = e0 - __uint_as_float(__float_as_uint(e0) & 0xffff0000u);
-                const float r1 = e1 - __uint_as_float(__float_as_uint(e1) & 0xffff0000u);
-                const float q0 = r0 - __uint_as_float(__float_as_uint(r0) & 0xffff0000u);
-                const float q1 = r1 - __uint_as_float(__float_as_uint(r1) & 0xffff0000u);
-                ph[j] = __builtin_amdgcn_perm(__float_as_uint(e1), __float_as_uint(e0), 0x07060302u);
-                pm[j] = __builtin_amdgcn_perm(__float_as_uint(r1), __float_as_uint(r0), 0x07060302u);
-                pl[j] = __builtin_amdgcn_perm(__float_as_uint(q1), __float_as_uint(q0), 0x07060302u);
+                const uint32_t hp = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2_t){e0, e1}, bf2_t));
+                const float r0 = e0 - __uint_as_float(hp << 16);
+                const float r1 = e1 - __uint_as_float(hp & 0xffff0000u);
+                ph[j] = hp;
+                pm[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2_t){r0, r1}, bf2_t));
             }
             const bf16x8_t bh = __builtin_bit_cast(bf16x8_t, make_uint4(ph[0], ph[1], ph[2], ph[3]));
             const bf16x8_t bm = __builtin_bit_cast(bf16x8_t, make_uint4(pm[0], pm[1], pm[2], pm[3]));
-            const bf16x8_t bl = __builtin_bit_cast(bf16x8_t, make_uint4(pl[0], pl[1], pl[2], pl[3]));
 #pragma unroll
             for (int cb = 0; cb < 4; ++cb) {
                 const uint4 gv = reinterpret_cast<const uint4 *>(smem + kEncGimgOff)[(cb * 4 + s) * 64 + lane];
                 const bf16x8_t ga = __builtin_bit_cast(bf16x8_t, gv);
                 acc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ga, bh, acc[cb], 0, 0, 0);
                 acc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ga, bm, acc[cb], 0, 0, 0);
-                acc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ga, bl, acc[cb], 0, 0, 0);
             }
         }
 
-        // signs: lane (n, g) holds P[n][16 cb + 4 g + i]
-        const bool finite_row = isfinite(as);
-        const float bound = as * 6.103515625e-05f + 7.888609052210118e-31f;   // 1024 * 2^-24, 2^-100
-        uint32_t slo = 0u, shi = 0u, unc = 0u;
+        // signs: lane (n, g) holds P[n][16 cb + 4 g + i]; cb's four bits go
+        // to bits 16 (cb & 1) + 4 g .. + 3 of word cb / 2
+        const bool finite_row = as < 0x1p127f;                 // false for inf / NaN
+        const float bound = as * 7.82012939453125e-05f + 7.888609052210118e-31f;   // 1312 * 2^-24, 2^-100
+        uint32_t slo = 0u, shi = 0u;
+        float amin = INFINITY;
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t bit = acc[cb][i] >= 0.0f ? 1u : 0u;
-                const int pos = 16 * (cb & 1) + 4 * g + i;
-                if (cb < 2) slo |= bit << pos; else shi |= bit << pos;
-                if (finite_row && !(fabsf(acc[cb][i]) > bound)) unc |= 1u << (4 * cb + i);
-            }
+        for (int cb = 0; cb < 4; ++cb) {
+            const uint32_t nb = (acc[cb][0] >= 0.0f ? 1u : 0u) | (acc[cb][1] >= 0.0f ? 2u : 0u) |
+                                (acc[cb][2] >= 0.0f ? 4u : 0u) | (acc[cb][3] >= 0.0f ? 8u : 0u);
+            const uint32_t w = nb << (16 * (cb & 1) + 4 * g);
+            if (cb < 2) slo |= w; else shi |= w;
+            amin = fminf(amin, fminf(fminf(fabsf(acc[cb][0]), fabsf(acc[cb][1])), fminf(fabsf(acc[cb][2]), fabsf(acc[cb][3]))));
+        }
         // rare: uncertain signs of finite rows (recomputed exactly: the 4
         // lanes of the row each sum their 32 elements, then combine) and
-        // rows whose residual is not finite (or whose |e| sum overflows)
+        // rows whose residual is not finite (or whose |e| sum reaches 2^127)
         const bool nf = !finite_row && v0 + n < v_end;
-        if (__builtin_amdgcn_ballot_w64(unc != 0u || nf)) {
+        if (__builtin_amdgcn_ballot_w64((finite_row && !(amin > bound)) || nf)) {
+            uint32_t unc = 0u;
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (finite_row && !(fabsf(acc[cb][i]) > bound)) unc |= 1u << (4 * cb + i);
             // one residual row at a time goes through this wave's LDS row
             float *st = reinterpret_cast<float *>(smem + kEncStageOff) + wave * 128;
             int staged = -1;
@@ -697,6 +720,29 @@ __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
             reinterpret_cast<uint2 *>(a.qjl + mrow * 8)[0] = make_uint2(slo, shi);
             a.norms[mrow] = ss > 3.4028234663852886e38 ? INFINITY : (float)sqrt(ss);
         }
+    };
+
+    // Groups v0, v0 + 16 nw, ... through a two-slot ring: the next group's
+    // rows are requested before the current one is encoded (past the last
+    // group, the current group's rows again, so every load is unconditional
+    // and the compiler waits only for the slot it consumes).
+    constexpr int64_t kStep = 16 * kEncWaves;
+    int64_t v0 = v_begin + 16 * wave;
+    if (v0 >= v_end) return;                                 // no barrier follows
+    uint4 ring0[4], ring1[4];
+    int64_t row0 = group_row(v0), row1;
+    load_group(ring0, row0);
+    for (;;) {
+        row1 = v0 + kStep < v_end ? group_row(v0 + kStep) : row0;
+        load_group(ring1, row1);
+        encode_group(ring0, row0, v0);
+        v0 += kStep;
+        if (v0 >= v_end) break;
+        row0 = v0 + kStep < v_end ? group_row(v0 + kStep) : row1;
+        load_group(ring0, row0);
+        encode_group(ring1, row1, v0);
+        v0 += kStep;
+        if (v0 >= v_end) break;
     }
 }
 

@@ -247,6 +247,7 @@ def test_prefill_d32_rotate_q_and_extreme_rows(device):
     q2 = q.float() * 200.0
     q2[0, 0] *= 3e5
     q2[1, 1] *= 1e-9
+    q2[1, 2] *= 1e28
     q2 = q2.to(torch.bfloat16)
     got = _run(device, q2, kn, kq, kr, vn, cb, uid, scale=0.1)
     want = restate.fused_attn_python(q2.float(), kn, kq, kr, vn, cb, uid, 0.1, True)
@@ -529,13 +530,19 @@ def test_prefill_extreme_q_no_overflow(device, dtype):
 
 
 def test_prefill_large_and_tiny_query_rows(device):
-    """Per-row power-of-two scaling keeps bf16 rows far outside fp16 range exact."""
+    """Per-row power-of-two scaling keeps bf16 rows far outside fp16 range exact;
+    rows whose logits pass 2^13 (log2 units) switch the exponents to rounded
+    logits, so huge rows (x 1e30) stay finite."""
     B, Hq, Hkv, T, S, uid = 1, 8, 2, 16, 300, 2
     kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=23, user_id=uid)
     q = _data.query((B, Hq, T, 128), seed=24, dtype=torch.float32)
     q[0, 0] *= 3e5           # beyond fp16 max
     q[0, 1] *= 1e-7          # fp16 subnormal range
+    q[0, 2] *= 1e30
+    q[0, 3] *= 1e-36         # f32 near its smallest normal
     q = q.to(torch.bfloat16)
-    got = _run(device, q, kn, kq, kr, vn, cb, uid, scale=1e-6)
-    want = restate.fused_attn_python(q.float(), kn, kq, kr, vn, cb, uid, 1e-6, True)
-    _assert_close(got, want, "prefill extreme rows")
+    for scale in (1e-6, 1 / math.sqrt(128)):
+        got = _run(device, q, kn, kq, kr, vn, cb, uid, scale=scale)
+        want = restate.fused_attn_python(q.float(), kn, kq, kr, vn, cb, uid, scale, True)
+        assert torch.isfinite(got).all()
+        _assert_close(got, want, f"prefill extreme rows scale {scale:.3g}")
