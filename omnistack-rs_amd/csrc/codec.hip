@@ -571,17 +571,22 @@ __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
         for (int s = 0; s < 4; ++s)
 #pragma unroll
             for (int i = 0; i < 8; ++i) cv[s][i] = cent[vb[s][i]];
-        // residuals, norm (fp64 sum of the exact squares) and |e| partial sums
+        // residuals, norm (fp64 sum of the exact squares) and |e| partial
+        // sums, one chain per chunk s (four independent dependency chains)
+        double ssp[4] = {0.0, 0.0, 0.0, 0.0};
+        float asp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
+        for (int i = 0; i < 8; ++i)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
+            for (int s = 0; s < 4; ++s) {
                 const float e = x[s][i] - cv[s][i];
                 x[s][i] = e;
                 const double ed = (double)e;
-                ss = __builtin_fma(ed, ed, ss);
-                as += fabsf(e);
+                ssp[s] = __builtin_fma(ed, ed, ssp[s]);
+                asp[s] += fabsf(e);
             }
+        ss = (ssp[0] + ssp[1]) + (ssp[2] + ssp[3]);
+        as = (asp[0] + asp[1]) + (asp[2] + asp[3]);
         ss = xlane_sum_f64<16>(ss);
         ss = xlane_sum_f64<32>(ss);
         as = xlane_sum_f32(as);
