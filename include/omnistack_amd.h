@@ -279,6 +279,36 @@ int omni_attn_serve(const void *q, int q_dtype, const int64_t *cache_index, int6
                     float *out, void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * The serving step over a page-granular cache.  The reference plans a paged
+ * KV cache (MANIFEST.md:211-215; page_size = 16 tokens, config.py:43) but
+ * gathers whole sequences instead (scripts/run_criteo_benchmark.py:553-557);
+ * this is that gather as page lookups inside the decode kernel.
+ * Pools (k_nib, k_qjl, k_norms, v_nib) are shaped like a contiguous cache
+ * with pages as the batch axis: (n_pages, Hkv, page_size, ...).  Sequence b
+ * holds seq_lens[b] tokens; token s sits in page page_table[b * max_pages +
+ * s / page_size] at slot s % page_size.  page_size is a power of two in
+ * [16, 1024]; n_pages * Hkv * page_size < 2^26; head_dim 128 and
+ * T * Hq / Hkv <= 32 query rows per kv head.  causal != 0 lets query token
+ * t see keys <= seq_lens[b] - T + t.  A page id outside [0, n_pages) among a
+ * sequence's pages, or a length outside [0, max_pages * page_size], gives
+ * NaN rows for that sequence and reads nothing out of bounds; a length of 0
+ * gives NaN rows (no keys).  LoRA as omni_attn_serve (lora_a NULL: none).
+ * workspace: omni_attn_paged_workspace_size(...) bytes.
+ */
+size_t omni_attn_paged_workspace_size(int64_t B, int Hq, int Hkv, int64_t T, int64_t max_pages,
+                                      int page_size, int q_dtype);
+int omni_attn_paged(const void *q, int q_dtype,
+                    const uint8_t *k_nib, const uint8_t *k_qjl, const float *k_norms,
+                    const uint8_t *v_nib, int64_t n_pages, int page_size,
+                    const int32_t *page_table, int64_t max_pages, const int32_t *seq_lens,
+                    const void *x, const void *lora_a, const void *lora_b, int w_dtype,
+                    const int32_t *lora_idx, int hidden, int rank, int n_loras, float lora_alpha,
+                    const float *codebooks, int per_head_codebook, const uint32_t *g_bits,
+                    int64_t B, int Hq, int Hkv, int64_t T, int head_dim,
+                    float scale, int with_qjl, int causal, int rotate_q, const int8_t *sign_flip,
+                    float *out, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
  * Measurement helper with no counterpart in the reference: streams `bytes`
  * (a multiple of 16, 16-byte aligned device buffer) once with n_partials
  * blocks and writes one XOR fold per block to partials[0 .. n_partials),

@@ -68,12 +68,20 @@ struct AttnArgs {
     int lora_w_dtype, lora_hidden, lora_rank, lora_n;
     float lora_alpha;
     int rows;                  // query rows per block (16: generic kernel, 8: D=128 decode kernel)
+    // paged cache (D=128 decode kernel): pool arrays shaped like a contiguous
+    // cache with (n_pages, Hkv, page_size); sequence b holds seq_lens[b]
+    // tokens in pages page_table[b * max_pages + j] (S = max_pages * page_size)
+    const int32_t *page_table;
+    const int32_t *seq_lens;
+    int64_t max_pages, n_pages;
+    int page_size, page_shift;  // page_size = 2^page_shift >= 16
     float qscale;              // scale * log2(e)
     float alpha_c;             // fp32 sqrt(2/pi)/D (the row scale multiplies the whole score)
     float wht_scale;
 };
 
 __device__ __forceinline__ int64_t imin64(int64_t x, int64_t y) { return x < y ? x : y; }
+__device__ __forceinline__ int64_t imax64(int64_t x, int64_t y) { return x > y ? x : y; }
 
 // Cache sequence read for batch entry b (wave-uniform).  Negative indices
 // count from the end of the pool, as tensor indexing does; an index outside
@@ -666,6 +674,28 @@ __device__ __forceinline__ void tile_load(TileRaw &R, const DecBufs &P, const De
         R.v[i] = __builtin_amdgcn_raw_buffer_load_b32(P.vn, vv + 64u * (16 * (i / 4) + (i % 4)), 0, 0);
 }
 
+// The same tile from a paged pool: half u (16 tokens) starts at pool row
+// rb[u] = (page * Hkv + hk) * page_size + slot; a half never crosses a page
+// (page sizes are multiples of 16 and tiles start at multiples of 32).  The
+// row offset goes into the per-lane offset, so the descriptor's range check
+// (the whole pool) covers it.
+template <bool QJL>
+__device__ __forceinline__ void tile_load_paged(TileRaw &R, const DecBufs &P, const DecOffsets &O, const uint32_t (&rb)[2]) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const u32x4_t kv4 = __builtin_amdgcn_raw_buffer_load_b128(P.kn, O.k + rb[u] * 64u, 0, 0);
+        R.k[u] = make_uint4(kv4.x, kv4.y, kv4.z, kv4.w);
+        if (QJL) {
+            const u32x2_t sv = __builtin_amdgcn_raw_buffer_load_b64(P.kq, O.sg + rb[u] * 8u, 0, 0);
+            R.sg[u] = make_uint2(sv.x, sv.y);
+            R.nr[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(P.kr, O.nr + rb[u] * 4u, 0, 0));
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        R.v[i] = __builtin_amdgcn_raw_buffer_load_b32(P.vn, O.v + rb[i / 4] * 64u + 64u * (i % 4), 0, 0);
+}
+
 __device__ __forceinline__ uint32_t cvt_pk_h2(float x, float y) {
     typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
     typedef float f2_t __attribute__((ext_vector_type(2)));
@@ -852,9 +882,10 @@ __device__ __forceinline__ int claim_issue(int *cnt, int lane) {
 }
 __device__ __forceinline__ int claim_value(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
-template <bool QJL, int PF, int SPB, bool LORA>
+template <bool QJL, int PF, int SPB, bool LORA, bool PAGED>
 __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs a) {
     static_assert(SPB == 1 || SPB == 2, "one or two sequences per block");
+    static_assert(!PAGED || SPB == 1, "a paged cache takes one sequence per block");
     constexpr int D = 128, QD = 64;
     constexpr int nw = kDecWaves;
     __shared__ __attribute__((aligned(16))) unsigned char smem[kDecLdsBytes];
@@ -888,8 +919,30 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
 
     // ── cache stream descriptors ──────────────────────────────────────
     const int s_begin = split * (int)a.split_len;
-    const int s_end = (int)imin64(a.S, (int64_t)s_begin + a.split_len);
+    // paged: this sequence's length; one outside [0, capacity] reads nothing
+    // and its rows come out NaN
+    int seq_len = (int)a.S;
+    bool len_bad = false;
+    if constexpr (PAGED) {
+        const int32_t L = a.seq_lens[b32];
+        len_bad = L < 0 || (int64_t)L > a.S;
+        seq_len = len_bad ? 0 : L;
+    }
+    const int s_end = imax(s_begin, (int)imin64(seq_len, (int64_t)s_begin + a.split_len));
     auto stream_bufs = [&](int64_t bb) {
+        if constexpr (PAGED) {
+            // the whole pool (its row count times 64 fits 32 bits: the host checks)
+            (void)bb;
+            const uint32_t rows = (uint32_t)(a.n_pages * a.Hkv * a.page_size);
+            DecBufs Q;
+            Q.kn = __builtin_amdgcn_make_buffer_rsrc((void *)a.k_nib, (short)0, rows * 64u, kBufWord3);
+            Q.vn = __builtin_amdgcn_make_buffer_rsrc((void *)a.v_nib, (short)0, rows * 64u, kBufWord3);
+            Q.kq = __builtin_amdgcn_make_buffer_rsrc((void *)(QJL ? a.k_qjl : a.k_nib), (short)0, QJL ? rows * 8u : 0u,
+                                                     kBufWord3);
+            Q.kr = __builtin_amdgcn_make_buffer_rsrc((void *)(QJL ? a.k_norms : (const float *)a.k_nib), (short)0,
+                                                     QJL ? rows * 4u : 0u, kBufWord3);
+            return Q;
+        }
         bool bad_unused;
         const int64_t kv_base = (cache_seq(a, bb, bad_unused) * a.Hkv + hk) * a.S;
         DecBufs Q;
@@ -911,6 +964,27 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     OFS.sg = (uint32_t)n * 8u;
     OFS.nr = 16u * g + 4u * (n & 3);      // norm of token 4g + n % 4 (of each 16-token half)
     OFS.v = 256u * g + 4u * n;
+
+    // Paged cache: pool rows of the two 16-token halves of the tile at token
+    // t (wave-uniform scalar loads of the page table).  A page id outside the
+    // pool reads page 0 and, for a half that holds tokens of the sequence,
+    // marks this wave's state bad (the sequence's rows come out NaN); past
+    // the table's width (tiles past the end) the last entry is read.
+    bool page_bad = false;
+    const int32_t *pt_row = PAGED ? a.page_table + b * a.max_pages : nullptr;
+    const int pj_max = PAGED ? (int)a.max_pages - 1 : 0;
+    const uint32_t pg_stride = PAGED ? (uint32_t)(a.Hkv * a.page_size) : 0u;   // pool rows per page
+    const uint32_t hk_rows = PAGED ? (uint32_t)(hk * a.page_size) : 0u;
+    auto half_rows = [&](int t, uint32_t (&rb)[2]) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int th = t + 16 * u;
+            const int32_t id = pt_row[imin(th >> a.page_shift, pj_max)];
+            const bool ok = id >= 0 && (int64_t)id < a.n_pages;
+            page_bad = page_bad || (!ok && th < s_end);
+            rb[u] = (ok ? (uint32_t)id : 0u) * pg_stride + hk_rows + ((uint32_t)th & (uint32_t)(a.page_size - 1));
+        }
+    };
 
     // ── prologue loads: branch-free buffer loads (an absent input gets a
     //    zero-size descriptor and reads 0), issued before the cache
@@ -961,8 +1035,16 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     // claim index i -> (sequence, token offset); i >= ntiles is past the end
     auto tile_seq = [&](int i) { return (nseq > 1 && i >= tps) ? 1 : 0; };
     auto tile_tok = [&](int i) { return s_begin + (i - tile_seq(i) * tps) * kDecTile; };
-    tile_load<QJL>(ring[0], tile_seq(wave) ? P1 : P, OFS, tile_tok(wave));
-    tile_load<QJL>(ring[1], tile_seq(wave + nw) ? P1 : P, OFS, tile_tok(wave + nw));
+    if constexpr (PAGED) {
+        uint32_t rb0[2], rb1[2];
+        half_rows(tile_tok(wave), rb0);
+        half_rows(tile_tok(wave + nw), rb1);
+        tile_load_paged<QJL>(ring[0], P, OFS, rb0);
+        tile_load_paged<QJL>(ring[1], P, OFS, rb1);
+    } else {
+        tile_load<QJL>(ring[0], tile_seq(wave) ? P1 : P, OFS, tile_tok(wave));
+        tile_load<QJL>(ring[1], tile_seq(wave + nw) ? P1 : P, OFS, tile_tok(wave + nw));
+    }
 
     // ── centroid lane % 16 as an (fp16 hi, fp16 remainder) pair ────────
     const uint16_t cb_h16 = f32_to_f16_rne(cb_mine);
@@ -1129,13 +1211,16 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     }
     const int rho_n = row_rho(rn);
     const int seq_n = row_seq(rn);             // this column's sequence
-    const int64_t key_limit64 = (a.causal_offset >= 0 && row_valid(rn)) ? a.causal_offset + div_small(rho_n, a.g_magic)
-                                                                       : INT64_MAX;
+    // causal: query token t sees keys <= coff + t (a paged cache aligns the
+    // last query token with the sequence's last key: coff = length - T)
+    const bool causal = a.causal_offset >= 0;
+    const int64_t coff = PAGED ? (int64_t)seq_len - a.T : a.causal_offset;
+    const int64_t key_limit64 = (causal && row_valid(rn)) ? coff + div_small(rho_n, a.g_magic) : INT64_MAX;
 
     // ── main loop ─────────────────────────────────────────────────────
-    const int key_limit = (int)imin64(key_limit64, (int64_t)0x7fffffff);
+    const int key_limit = (int)imax64(imin64(key_limit64, (int64_t)0x7fffffff), -1);
     // tiles ending at or below min(s_end, first masked key of any row) need no masks
-    const int64_t min_limit64 = (a.causal_offset >= 0) ? a.causal_offset + div_small(rc * kDecRows, a.g_magic) : INT64_MAX;
+    const int64_t min_limit64 = causal ? coff + div_small(rc * kDecRows, a.g_magic) : INT64_MAX;
     // two sequences per block: every tile masks the other sequence's columns
     const int full_end = nseq > 1 ? s_begin : (int)imin64((int64_t)s_end, min_limit64 + 1);
     const uint32_t laneoff = (uint32_t)(lane & 31) * 8u;
@@ -1290,7 +1375,42 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     if (i_cur < ntiles) {
         tile_step(ring[0], tile_tok(i_cur), tile_seq(i_cur));
         const int i_pre = wave + nw;
-        if (i_pre < ntiles) {
+        if (i_pre < ntiles && PAGED) {
+            // paged: a claimed tile's page rows are read (and waited for)
+            // before the next claim is issued, so that wait does not also
+            // wait for the claim's atomic
+            uint32_t rb[2];
+            auto next_rows = [&](int i) {
+                half_rows(tile_tok(i), rb);
+                asm volatile("" ::"s"(rb[0]), "s"(rb[1]));
+                __builtin_amdgcn_sched_barrier(0);
+            };
+            i_cur = claim_value(c_raw);
+            next_rows(i_cur);
+            c_raw = claim_issue(tile_cnt, lane);
+            __builtin_amdgcn_sched_barrier(0);
+            tile_load_paged<QJL>(ring[0], P, OFS, rb);
+            __builtin_amdgcn_sched_barrier(0);
+            tile_step(ring[1], tile_tok(i_pre), 0);
+            for (;;) {
+                if (i_cur >= ntiles) break;
+                const int i_nxt = claim_value(c_raw);
+                next_rows(i_nxt);
+                c_raw = claim_issue(tile_cnt, lane);
+                __builtin_amdgcn_sched_barrier(0);
+                tile_load_paged<QJL>(ring[1], P, OFS, rb);
+                __builtin_amdgcn_sched_barrier(0);
+                tile_step(ring[0], tile_tok(i_cur), 0);
+                if (i_nxt >= ntiles) break;
+                i_cur = claim_value(c_raw);
+                next_rows(i_cur);
+                c_raw = claim_issue(tile_cnt, lane);
+                __builtin_amdgcn_sched_barrier(0);
+                tile_load_paged<QJL>(ring[0], P, OFS, rb);
+                __builtin_amdgcn_sched_barrier(0);
+                tile_step(ring[1], tile_tok(i_nxt), 0);
+            }
+        } else if (i_pre < ntiles) {
             i_cur = claim_value(c_raw);
             c_raw = claim_issue(tile_cnt, lane);
             __builtin_amdgcn_sched_barrier(0);
@@ -1334,7 +1454,8 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
         if (ne < kDecRows && wave < nw_act) {
             if (ge == 0) {
                 wm[wave * kDecRows + ne] = m_run;
-                wl[wave * kDecRows + ne] = lacc_sum[0];
+                // a page outside the pool poisons the sequence's denominator
+                wl[wave * kDecRows + ne] = page_bad ? __builtin_nanf("") : lacc_sum[0];
             }
             float *dst = ob + (wave * kDecRows + ne) * kObStride;
 #pragma unroll
@@ -1373,6 +1494,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
             (void)cache_seq(a, rr_b, bad);
             if (bad) lsum = __builtin_nanf("");
         }
+        if (len_bad) lsum = __builtin_nanf("");
         if (a.splits == 1) {
             const int t = div_small(rr_rho, a.g_magic);
             const int hq = hk * a.G + (rr_rho - t * a.G);
@@ -2264,7 +2386,7 @@ static int device_cus() {
 
 static int64_t clamp64(int64_t v, int64_t lo, int64_t hi) { return v < lo ? lo : (v > hi ? hi : v); }
 
-static Plan make_plan(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int D, bool q32) {
+static Plan make_plan(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int D, bool q32, bool paged = false) {
     Plan p;
     const int G = Hq / Hkv;
     const int cus = device_cus();
@@ -2278,7 +2400,7 @@ static Plan make_plan(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int D, b
     // than CUs, at most 4 query rows each): two sequences share a block's 8
     // row slots, halving the blocks (and the per-block prologues) without
     // idling any slot.
-    p.spb = (p.dec128 && T * G <= kDecRows / 2 && B >= 2 && B * (int64_t)Hkv > cus) ? 2 : 1;
+    p.spb = (!paged && p.dec128 && T * G <= kDecRows / 2 && B >= 2 && B * (int64_t)Hkv > cus) ? 2 : 1;
     const int64_t units = ((B + p.spb - 1) / p.spb) * (int64_t)Hkv * p.n_rchunks;
     if (p.prefill || p.prefill32) {
         const int64_t tiles = (S + kDecTile - 1) / kDecTile;
@@ -2337,13 +2459,20 @@ struct LoraSpec {
 
 static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
-template <bool QJL, int SPB>
+template <bool QJL, int SPB, bool PAGED = false>
 static void launch_decode128(bool lora, dim3 grid, dim3 block, hipStream_t s, const AttnArgs &a) {
     if (lora)
-        hipLaunchKernelGGL((attn_decode128_kernel<QJL, kDecPrefetch, SPB, true>), grid, block, 0, s, a);
+        hipLaunchKernelGGL((attn_decode128_kernel<QJL, kDecPrefetch, SPB, true, PAGED>), grid, block, 0, s, a);
     else
-        hipLaunchKernelGGL((attn_decode128_kernel<QJL, kDecPrefetch, SPB, false>), grid, block, 0, s, a);
+        hipLaunchKernelGGL((attn_decode128_kernel<QJL, kDecPrefetch, SPB, false, PAGED>), grid, block, 0, s, a);
 }
+
+// Paged cache of omni_attn_paged.
+struct PagedSpec {
+    const int32_t *page_table, *seq_lens;
+    int64_t max_pages, n_pages;
+    int page_size, page_shift;
+};
 
 static int attn_run(const void *q, int q_dtype, const uint8_t *k_nib, const uint8_t *k_qjl,
                     const float *k_norms, const uint8_t *v_nib, const float *codebooks,
@@ -2351,7 +2480,7 @@ static int attn_run(const void *q, int q_dtype, const uint8_t *k_nib, const uint
                     int64_t T, int64_t S, int head_dim, float scale, int with_qjl,
                     int64_t causal_offset, int rotate_q, const int8_t *sign_flip, float *out,
                     void *workspace, size_t workspace_bytes, void *stream, const LoraSpec *lora,
-                    const int64_t *seq_index, int64_t n_seqs) {
+                    const int64_t *seq_index, int64_t n_seqs, const PagedSpec *paged = nullptr) {
     OMNI_CHECK_ARG(dtype_ok(q_dtype), "omni_attn: bad q dtype %d", q_dtype);
     OMNI_CHECK_ARG(head_dim_ok(head_dim), "omni_attn: head_dim must be 128 or 32, got %d", head_dim);
     OMNI_CHECK_ARG(B >= 0 && Hq > 0 && Hkv > 0 && T >= 0 && S >= 0, "omni_attn: bad shape");
@@ -2364,7 +2493,9 @@ static int attn_run(const void *q, int q_dtype, const uint8_t *k_nib, const uint
     OMNI_CHECK_ARG(S < (int64_t(1) << 25), "omni_attn: S must be < 2^25 tokens per sequence");
     OMNI_CHECK_ARG(T * (Hq / Hkv) < (int64_t(1) << 31), "omni_attn: T * (n_heads / n_kv_heads) must be < 2^31");
     OMNI_CHECK_ARG(seq_index == nullptr || n_seqs >= 1, "omni_attn: a cache index needs a pool of >= 1 sequences");
-    Plan p = make_plan(B, Hq, Hkv, T, S, head_dim, q_dtype == OMNI_F32);
+    Plan p = make_plan(B, Hq, Hkv, T, S, head_dim, q_dtype == OMNI_F32, paged != nullptr);
+    OMNI_CHECK_ARG(paged == nullptr || (head_dim == 128 && p.dec128),
+                   "omni_attn_paged: needs head_dim 128 and T * n_heads / n_kv_heads <= %d query rows", kPrefillMinRows);
     OMNI_CHECK_ARG(Hkv <= 65535 && ((B + p.spb - 1) / p.spb) * p.n_rchunks <= 65535 && p.splits <= 2147483647,
                    "omni_attn: grid too large (batch x row chunks must be <= 65535)");
     // LoRA: fused into the D=128 decode prologue; other kernels read q_eff
@@ -2411,6 +2542,12 @@ static int attn_run(const void *q, int q_dtype, const uint8_t *k_nib, const uint
     a.seq_index = seq_index;
     a.n_seqs = seq_index ? n_seqs : B;
     a.spb = p.spb;
+    a.page_table = paged ? paged->page_table : nullptr;
+    a.seq_lens = paged ? paged->seq_lens : nullptr;
+    a.max_pages = paged ? paged->max_pages : 0;
+    a.n_pages = paged ? paged->n_pages : 0;
+    a.page_size = paged ? paged->page_size : 0;
+    a.page_shift = paged ? paged->page_shift : 0;
     dim3 grid((unsigned)p.splits, (unsigned)Hkv, (unsigned)(((B + p.spb - 1) / p.spb) * p.n_rchunks));
     dim3 block(64 * p.nw);
     if (p.prefill) {
@@ -2432,6 +2569,10 @@ static int attn_run(const void *q, int q_dtype, const uint8_t *k_nib, const uint
             if (qlo) hipLaunchKernelGGL((attn_prefill32_kernel<false, 2, true>), grid, block, 0, st, a);
             else hipLaunchKernelGGL((attn_prefill32_kernel<false, kP32Ncb, false>), grid, block, 0, st, a);
         }
+    } else if (p.dec128 && paged) {
+        hipStream_t st = as_stream(stream);
+        if (with_qjl) launch_decode128<true, 1, true>(lora_fused, grid, block, st, a);
+        else launch_decode128<false, 1, true>(lora_fused, grid, block, st, a);
     } else if (p.dec128) {
         hipStream_t st = as_stream(stream);
         if (with_qjl && p.spb > 1) launch_decode128<true, 2>(lora_fused, grid, block, st, a);
@@ -2518,6 +2659,78 @@ extern "C" int omni_attn_serve(const void *q, int q_dtype, const int64_t *cache_
     return attn_run(q, q_dtype, k_nib, k_qjl, k_norms, v_nib, codebooks, per_head_codebook, g_bits, B, Hq, Hkv, T,
                     S, head_dim, scale, with_qjl, causal_offset, rotate_q, sign_flip, out, workspace,
                     workspace_bytes, stream, &spec, cache_index, n_cache_seqs);
+}
+
+// ── paged cache ──────────────────────────────────────────────────────────
+//
+// Pool arrays are shaped like a contiguous cache with the batch axis as
+// pages: nibbles (n_pages, Hkv, page_size, 64), signs (.., 8), norms
+// (n_pages, Hkv, page_size), V (.., 64).  Sequence b holds seq_lens[b] tokens
+// in pages page_table[b * max_pages + j], j < ceil(len / page_size); entries
+// past that are never read for keys.  D = 128, T * Hq / Hkv <= 32 query rows
+// per kv head (the decode kernel).  causal != 0 aligns query token t with
+// key len - T + t.
+
+static bool paged_args_ok(int64_t B, int Hkv, int64_t n_pages, int page_size, int64_t max_pages, int &shift) {
+    shift = 0;
+    while (shift < 11 && (1 << shift) < page_size) ++shift;
+    if (page_size < 16 || page_size > 1024 || (1 << shift) != page_size) {
+        set_error("omni_attn_paged: page_size must be a power of two in [16, 1024], got %d", page_size);
+        return false;
+    }
+    if (n_pages < 1 || max_pages < 1 || B < 0) {
+        set_error("omni_attn_paged: need n_pages >= 1, max_pages >= 1");
+        return false;
+    }
+    // every byte offset into the pool fits 32 bits
+    if (Hkv < 1 || n_pages * Hkv * (int64_t)page_size >= (int64_t(1) << 26)) {
+        set_error("omni_attn_paged: pool too large (n_pages * n_kv_heads * page_size must be < 2^26 tokens)");
+        return false;
+    }
+    if (max_pages * (int64_t)page_size >= (int64_t(1) << 25)) {
+        set_error("omni_attn_paged: max_pages * page_size must be < 2^25 tokens per sequence");
+        return false;
+    }
+    return true;
+}
+
+extern "C" size_t omni_attn_paged_workspace_size(int64_t B, int Hq, int Hkv, int64_t T, int64_t max_pages,
+                                                 int page_size, int q_dtype) {
+    if (B <= 0 || Hq <= 0 || Hkv <= 0 || T <= 0 || max_pages <= 0 || page_size <= 0 || Hq % Hkv || !dtype_ok(q_dtype))
+        return 0;
+    const Plan p = make_plan(B, Hq, Hkv, T, max_pages * (int64_t)page_size, 128, q_dtype == OMNI_F32, true);
+    // plus room for the gather-apply LoRA fallback's q_eff
+    return align256(p.ws_bytes) + (size_t)B * Hq * T * 128 * (q_dtype == OMNI_F32 ? 4 : 2);
+}
+
+extern "C" int omni_attn_paged(const void *q, int q_dtype, const uint8_t *k_nib, const uint8_t *k_qjl,
+                               const float *k_norms, const uint8_t *v_nib, int64_t n_pages, int page_size,
+                               const int32_t *page_table, int64_t max_pages, const int32_t *seq_lens,
+                               const void *x, const void *lora_a, const void *lora_b, int w_dtype,
+                               const int32_t *lora_idx, int hidden, int rank, int n_loras, float lora_alpha,
+                               const float *codebooks, int per_head_codebook, const uint32_t *g_bits, int64_t B,
+                               int Hq, int Hkv, int64_t T, int head_dim, float scale, int with_qjl, int causal,
+                               int rotate_q, const int8_t *sign_flip, float *out, void *workspace,
+                               size_t workspace_bytes, void *stream) {
+    int shift = 0;
+    if (!paged_args_ok(B, Hkv, n_pages, page_size, max_pages, shift)) return OMNI_EINVAL;
+    if (B > 0 && T > 0) OMNI_CHECK_ARG(page_table && seq_lens, "omni_attn_paged: NULL page table or lengths");
+    const PagedSpec pg{page_table, seq_lens, max_pages, n_pages, page_size, shift};
+    const int64_t S = max_pages * (int64_t)page_size;
+    const int64_t coff = causal ? 0 : -1;
+    if (lora_a == nullptr)
+        return attn_run(q, q_dtype, k_nib, k_qjl, k_norms, v_nib, codebooks, per_head_codebook, g_bits, B, Hq, Hkv,
+                        T, S, head_dim, scale, with_qjl, coff, rotate_q, sign_flip, out, workspace, workspace_bytes,
+                        stream, nullptr, nullptr, 0, &pg);
+    OMNI_CHECK_ARG(dtype_ok(w_dtype), "omni_attn_paged: bad LoRA dtype %d", w_dtype);
+    OMNI_CHECK_ARG(hidden > 0 && rank >= 1 && rank <= 64 && n_loras >= 1,
+                   "omni_attn_paged: need hidden > 0, 1 <= rank <= 64, n_loras >= 1");
+    if (B > 0 && T > 0) OMNI_CHECK_ARG(x && lora_b && lora_idx, "omni_attn_paged: NULL LoRA pointer");
+    OMNI_CHECK_ARG((int64_t)Hq * head_dim <= (int64_t)1 << 30, "omni_attn_paged: n_heads * head_dim too large");
+    const LoraSpec spec{x, lora_a, lora_b, w_dtype, lora_idx, hidden, rank, n_loras, lora_alpha};
+    return attn_run(q, q_dtype, k_nib, k_qjl, k_norms, v_nib, codebooks, per_head_codebook, g_bits, B, Hq, Hkv, T,
+                    S, head_dim, scale, with_qjl, coff, rotate_q, sign_flip, out, workspace, workspace_bytes, stream,
+                    &spec, nullptr, 0, &pg);
 }
 
 // ── allocation-free variant of omni_attn ─────────────────────────────────

@@ -1,0 +1,193 @@
+"""Page-granular compressed KV cache and the attention that reads it.
+
+The reference serves each query by gathering its user's packed cache out of
+a pool (``nibbles[idx]``, scripts/run_criteo_benchmark.py:553-557) and plans
+a paged cache for it (MANIFEST.md:211-215; ``page_size`` = 16 tokens,
+config.py:43) that it does not implement.  Here the pool is a set of pages in
+the reference's packed layout with the batch axis as pages:
+
+    k_nibbles (n_pages, n_kv_heads, page_size, head_dim / 2)  uint8
+    k_qjl     (n_pages, n_kv_heads, page_size, head_dim / 16) uint8
+    k_norms   (n_pages, n_kv_heads, page_size)                float32
+    v_nibbles (n_pages, n_kv_heads, page_size, head_dim / 2)  uint8
+
+A sequence is a list of pages (one row of an int32 page table) and a length;
+token s of sequence b sits in page ``page_table[b, s // page_size]`` at slot
+``s % page_size``.  ``paged_attention`` is one call into libomnistack_amd.so
+(``omni_attn_paged``): the decode kernel reads each 16-token half-tile from
+its page in place, with the same arithmetic as the contiguous ``omni_attn``
+(so a sequence gives the same result whichever pages hold it).
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Sequence
+
+import torch
+
+from .. import _lib
+from ..kernels.hadamard import HEAD_DIM
+from ..kernels.quantize import _check_packed, _prep_codebooks
+
+
+class PagedKVCache:
+    """A pool of fixed-size pages of packed K/V and a free list.
+
+    ``allocate(n_tokens)`` hands out the pages for a sequence of that length,
+    ``free(pages)`` returns them, ``write(pages, ...)`` copies a contiguous
+    packed sequence (the encoder's output for one batch entry) into them,
+    ``page_table(...)`` builds the int32 table ``paged_attention`` reads.
+    """
+
+    def __init__(self, n_pages: int, n_kv_heads: int, page_size: int = 16, head_dim: int = HEAD_DIM,
+                 device="cuda"):
+        if page_size < 16 or page_size > 1024 or page_size & (page_size - 1):
+            raise ValueError(f"page_size must be a power of two in [16, 1024], got {page_size}")
+        if n_pages < 1 or n_kv_heads < 1:
+            raise ValueError("n_pages and n_kv_heads must be >= 1")
+        if head_dim != HEAD_DIM:
+            raise ValueError(f"the paged decode path takes head_dim {HEAD_DIM}, got {head_dim}")
+        self.n_pages, self.n_kv_heads, self.page_size, self.head_dim = n_pages, n_kv_heads, page_size, head_dim
+        dev = torch.device(device)
+        shape = (n_pages, n_kv_heads, page_size)
+        self.k_nibbles = torch.zeros(*shape, head_dim // 2, dtype=torch.uint8, device=dev)
+        self.k_qjl = torch.zeros(*shape, head_dim // 16, dtype=torch.uint8, device=dev)
+        self.k_norms = torch.zeros(*shape, dtype=torch.float32, device=dev)
+        self.v_nibbles = torch.zeros(*shape, head_dim // 2, dtype=torch.uint8, device=dev)
+        self._free = list(range(n_pages - 1, -1, -1))
+
+    @property
+    def device(self) -> torch.device:
+        return self.k_nibbles.device
+
+    def pages_for(self, n_tokens: int) -> int:
+        return (int(n_tokens) + self.page_size - 1) // self.page_size
+
+    def allocate(self, n_tokens: int) -> list[int]:
+        n = self.pages_for(n_tokens)
+        if n > len(self._free):
+            raise RuntimeError(f"out of pages: {n} needed, {len(self._free)} free")
+        return [self._free.pop() for _ in range(n)]
+
+    def free(self, pages: Sequence[int]) -> None:
+        self._free.extend(int(p) for p in reversed(list(pages)))
+
+    def write(self, pages: Sequence[int], k_nibbles: torch.Tensor, k_qjl: torch.Tensor, k_norms: torch.Tensor,
+              v_nibbles: torch.Tensor, start: int = 0) -> None:
+        """Copy one packed sequence, (n_kv_heads, S, ...) as ``encode_kv``
+        returns per batch entry, into ``pages`` from token ``start`` on."""
+        H, ps = self.n_kv_heads, self.page_size
+        if k_nibbles.dim() != 3 or k_nibbles.shape[0] != H:
+            raise ValueError(f"k_nibbles must be ({H}, S, {self.head_dim // 2}), got {tuple(k_nibbles.shape)}")
+        S = k_nibbles.shape[1]
+        if self.pages_for(start + S) > len(pages):
+            raise ValueError(f"{len(pages)} pages hold {len(pages) * ps} tokens, {start + S} needed")
+        tok = torch.arange(start, start + S, device=self.device)
+        pg = torch.as_tensor(list(pages), dtype=torch.int64, device=self.device)[tok // ps]
+        slot = tok % ps
+        for pool, src in ((self.k_nibbles, k_nibbles), (self.k_qjl, k_qjl), (self.k_norms, k_norms),
+                          (self.v_nibbles, v_nibbles)):
+            pool[pg, :, slot] = src.to(device=self.device, dtype=pool.dtype).transpose(0, 1)
+
+    def page_table(self, sequences: Sequence[Sequence[int]], max_pages: Optional[int] = None) -> torch.Tensor:
+        """int32 (len(sequences), max_pages) table; unused entries are -1."""
+        width = max([len(s) for s in sequences] + [1]) if max_pages is None else int(max_pages)
+        t = torch.full((len(sequences), width), -1, dtype=torch.int32)
+        for i, s in enumerate(sequences):
+            if len(s) > width:
+                raise ValueError(f"sequence {i} has {len(s)} pages, the table {width}")
+            t[i, :len(s)] = torch.as_tensor(list(s), dtype=torch.int32)
+        return t.to(self.device)
+
+    @classmethod
+    def from_contiguous(cls, k_nibbles, k_qjl, k_norms, v_nibbles, page_size: int = 16,
+                        seq_lens: Optional[Sequence[int]] = None, spare_pages: int = 0,
+                        generator: Optional[torch.Generator] = None):
+        """Pages for a contiguous packed cache (B, n_kv_heads, S, ...): returns
+        (cache, page_table, seq_lens).  Pages are assigned in a random order
+        (``generator``), so no sequence's pages are contiguous or in order."""
+        B, H, S, nb = k_nibbles.shape
+        lens = [S] * B if seq_lens is None else [int(x) for x in seq_lens]
+        need = sum((L + page_size - 1) // page_size for L in lens)
+        cache = cls(need + spare_pages, H, page_size, 2 * nb, device=k_nibbles.device)
+        order = torch.randperm(cache.n_pages, generator=generator).tolist()
+        cache._free = list(reversed(order))
+        seqs = []
+        for b, L in enumerate(lens):
+            pages = cache.allocate(L)
+            if L:
+                cache.write(pages, k_nibbles[b, :, :L], k_qjl[b, :, :L], k_norms[b, :, :L], v_nibbles[b, :, :L])
+            seqs.append(pages)
+        table = cache.page_table(seqs)
+        return cache, table, torch.as_tensor(lens, dtype=torch.int32, device=k_nibbles.device)
+
+
+def paged_attention(q: torch.Tensor, cache: PagedKVCache, page_table: torch.Tensor, seq_lens: torch.Tensor,
+                    codebooks: torch.Tensor, user_id: int = 0, scale: Optional[float] = None,
+                    with_qjl: bool = True, *, causal: bool = False, rotate_q: bool = False,
+                    sign_flip: Optional[torch.Tensor] = None, x: Optional[torch.Tensor] = None,
+                    lora_a: Optional[torch.Tensor] = None, lora_b: Optional[torch.Tensor] = None,
+                    lora_indices: Optional[torch.Tensor] = None, lora_alpha: float = 1.0,
+                    validate: bool = True) -> torch.Tensor:
+    """``omni_attn`` over a paged cache: query batch entry b attends the
+    first ``seq_lens[b]`` tokens of the sequence in row b of ``page_table``.
+    q (B, n_heads, T, 128) with T * n_heads / n_kv_heads <= 32; ``causal``
+    aligns query token t with key ``seq_lens[b] - T + t``.  Returns float32
+    (B, n_heads, T, 128).  With ``validate``, page ids outside the pool and
+    lengths beyond the table raise on the host (one device-to-host copy);
+    without it such sequences give NaN rows, as does a length of 0."""
+    if q.dim() != 4:
+        raise ValueError(f"q must be (B, n_heads, T, head_dim), got {tuple(q.shape)}")
+    B, Hq, T, D = q.shape
+    H, ps = cache.n_kv_heads, cache.page_size
+    if D != cache.head_dim:
+        raise ValueError(f"q head_dim {D} differs from the cache's {cache.head_dim}")
+    if Hq % H:
+        raise ValueError(f"n_heads={Hq} must be divisible by n_kv_heads={H}")
+    if T * (Hq // H) > 32:
+        raise ValueError(f"paged attention takes T * n_heads / n_kv_heads <= 32 query rows, got {T * (Hq // H)}")
+    if page_table.dim() != 2 or page_table.shape[0] != B:
+        raise ValueError(f"page_table must be ({B}, max_pages), got {tuple(page_table.shape)}")
+    _check_packed(cache.k_nibbles, cache.k_qjl if with_qjl else None, cache.k_norms if with_qjl else None,
+                  "cache.k_nibbles")
+    dev = _lib.require_device(q, cache.k_nibbles, page_table, seq_lens)
+    pt = page_table.to(device=dev, dtype=torch.int32).contiguous()
+    lens = torch.as_tensor(seq_lens).to(device=dev, dtype=torch.int32).reshape(-1).contiguous()
+    if lens.numel() != B:
+        raise ValueError(f"seq_lens must have {B} entries, got {lens.numel()}")
+    max_pages = pt.shape[1]
+    if validate and B > 0:
+        lh, th = lens.cpu(), pt.cpu()
+        if int(lh.min()) < 0 or int(lh.max()) > max_pages * ps:
+            raise ValueError(f"seq_lens must lie in [0, {max_pages * ps}] (the page table's width)")
+        for b in range(B):
+            used = th[b, :(int(lh[b]) + ps - 1) // ps]
+            if used.numel() and (int(used.min()) < 0 or int(used.max()) >= cache.n_pages):
+                raise IndexError(f"sequence {b}: page id out of range for a pool of {cache.n_pages} pages")
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    cb, per_head = _prep_codebooks(codebooks, H, dev)
+    qc = q if q.dtype in _lib.DTYPE_CODE else q.float()
+    qc = qc.contiguous()
+    gb = _lib.g_bits(_lib.head_seeds(user_id, H), D, dev) if with_qjl else None
+    sf = _lib.sign_flip_i8(sign_flip, D, dev) if (rotate_q and sign_flip is not None) else None
+    if x is not None:
+        from ..kernels.fused_attention import _prep_lora
+        xc, ac, bc, wcode, idx, hidden, rank, n_loras, alpha = _prep_lora(q, x, lora_a, lora_b, lora_indices,
+                                                                          lora_alpha, validate)
+    else:
+        xc = ac = bc = idx = None
+        wcode, hidden, rank, n_loras, alpha = 0, 0, 0, 0, 0.0
+    out = torch.empty(B, Hq, T, D, dtype=torch.float32, device=dev)
+    L = _lib.lib()
+    qcode = _lib.dtype_code(qc.dtype)
+    ws_bytes = L.omni_attn_paged_workspace_size(B, Hq, H, T, max_pages, ps, qcode)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if ws_bytes else None
+    _lib.check(L.omni_attn_paged(
+        _lib.ptr(qc), qcode, _lib.ptr(cache.k_nibbles), _lib.ptr(cache.k_qjl if with_qjl else None),
+        _lib.ptr(cache.k_norms if with_qjl else None), _lib.ptr(cache.v_nibbles), cache.n_pages, ps,
+        _lib.ptr(pt), max_pages, _lib.ptr(lens),
+        _lib.ptr(xc), _lib.ptr(ac), _lib.ptr(bc), wcode, _lib.ptr(idx), hidden, rank, n_loras, alpha,
+        _lib.ptr(cb), per_head, _lib.ptr(gb), B, Hq, H, T, D, float(scale), int(with_qjl), int(causal),
+        int(rotate_q), _lib.ptr(sf), _lib.ptr(out), _lib.ptr(ws), ws_bytes, _lib.stream_of(dev)))
+    return out

@@ -1,0 +1,140 @@
+"""GPU parity of the paged cache (omni_attn_paged) against the contiguous
+path and the CPU oracle.
+
+A sequence spread over pages in random order must give exactly what the
+contiguous kernel gives on the same tokens (same kernel arithmetic, only
+the addresses differ), and both must meet the oracle bar (max-abs <= 2e-3,
+mean-abs <= 2e-4).  Ragged lengths, page sizes 16 / 32 / 64, split-K over
+long sequences, causal multi-token queries, LoRA with in-kernel rotation,
+and the error paths (page ids outside the pool, empty sequences) are
+covered.  The reference has no paged cache (it gathers whole sequences,
+scripts/run_criteo_benchmark.py:553-557); its per-sequence semantics are
+those of _fused_attn_python (fused_attention.py:435-466).
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import restate
+from tests import _data
+from tests.test_gpu_attn import _assert_close, _cache, _causal_mask
+
+pytestmark = pytest.mark.gpu
+
+
+def _paged(device, kn, kq, kr, vn, page_size, lens=None, spare=3, seed=0):
+    from omnistack_rs.cache import PagedKVCache
+    g = torch.Generator().manual_seed(seed)
+    return PagedKVCache.from_contiguous(*(t.to(device) for t in (kn, kq, kr, vn)), page_size=page_size,
+                                        seq_lens=lens, spare_pages=spare, generator=g)
+
+
+@pytest.mark.parametrize("page_size", [16, 32, 64])
+@pytest.mark.parametrize("with_qjl", [True, False])
+def test_paged_equals_contiguous(device, page_size, with_qjl):
+    from omnistack_rs.cache import paged_attention
+    from omnistack_rs.kernels.fused_attention import omni_attn
+    B, Hq, Hkv, T, S, uid = 4, 32, 8, 1, 300, 5
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=301, user_id=uid)
+    q = _data.query((B, Hq, T, 128), seed=302)
+    cache, pt, lens = _paged(device, kn, kq, kr, vn, page_size, seed=page_size)
+    got = paged_attention(q.to(device), cache, pt, lens, cb.to(device), user_id=uid, with_qjl=with_qjl)
+    ref = omni_attn(*(t.to(device) for t in (q, kn, kq, kr, vn, cb)), user_id=uid, with_qjl=with_qjl)
+    # 10 tiles per (sequence, kv head): one per wave, so both runs sum in the same order
+    assert torch.equal(got, ref), f"paged differs from contiguous by {(got - ref).abs().max().item():.3e}"
+    want = restate.fused_attn_python(q.float(), kn, kq, kr, vn, cb, uid, 1 / math.sqrt(128), with_qjl)
+    _assert_close(got, want, f"paged ps{page_size} qjl{with_qjl}")
+
+
+@pytest.mark.parametrize("page_size", [16, 64])
+def test_paged_ragged_lengths(device, page_size):
+    from omnistack_rs.cache import paged_attention
+    B, Hq, Hkv, T, S, uid = 6, 16, 4, 1, 520, 9
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=311, user_id=uid)
+    q = _data.query((B, Hq, T, 128), seed=312)
+    lens = [520, 1, 17, 256, 511, 33]
+    cache, pt, lt = _paged(device, kn, kq, kr, vn, page_size, lens=lens, seed=7)
+    got = paged_attention(q.to(device), cache, pt, lt, cb.to(device), user_id=uid).cpu()
+    for b, L in enumerate(lens):
+        sl = slice(b, b + 1)
+        want = restate.fused_attn_python(q[sl].float(), kn[sl, :, :L], kq[sl, :, :L], kr[sl, :, :L],
+                                         vn[sl, :, :L], cb, uid, 1 / math.sqrt(128), True)
+        _assert_close(got[sl], want, f"paged ragged ps{page_size} b{b} len{L}")
+
+
+def test_paged_long_sequence_split_k(device):
+    """One sequence of 6000 tokens over 2 kv heads: many splits per
+    (sequence, kv head), each reading its own run of pages, merged by the
+    combine kernel; tiles are claimed dynamically within each split."""
+    from omnistack_rs.cache import paged_attention
+    B, Hq, Hkv, T, S, uid = 1, 8, 2, 1, 6000, 3
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=321, user_id=uid)
+    q = _data.query((B, Hq, T, 128), seed=322)
+    cache, pt, lt = _paged(device, kn, kq, kr, vn, 16, seed=11)
+    got = paged_attention(q.to(device), cache, pt, lt, cb.to(device), user_id=uid)
+    want = restate.fused_attn_python(q.float(), kn, kq, kr, vn, cb, uid, 1 / math.sqrt(128), True)
+    _assert_close(got, want, "paged split-K 6000 tokens")
+
+
+def test_paged_causal_chunk(device):
+    """T = 4 query tokens per sequence aligned with the end of each sequence
+    (query t sees keys <= len - 4 + t), ragged lengths."""
+    from omnistack_rs.cache import paged_attention
+    B, Hq, Hkv, T, S, uid = 3, 8, 2, 4, 200, 4
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=331, user_id=uid)
+    q = _data.query((B, Hq, T, 128), seed=332)
+    lens = [200, 37, 98]
+    cache, pt, lt = _paged(device, kn, kq, kr, vn, 32, lens=lens, seed=13)
+    got = paged_attention(q.to(device), cache, pt, lt, cb.to(device), user_id=uid, causal=True).cpu()
+    for b, L in enumerate(lens):
+        sl = slice(b, b + 1)
+        want = restate.fused_attn_python(q[sl].float(), kn[sl, :, :L], kq[sl, :, :L], kr[sl, :, :L],
+                                         vn[sl, :, :L], cb, uid, 1 / math.sqrt(128), True,
+                                         mask=_causal_mask(T, L, L - T))
+        _assert_close(got[sl], want, f"paged causal b{b} len{L}")
+
+
+def test_paged_lora_and_rotation_equal_contiguous(device):
+    """The serving step (rank-8 LoRA on q, in-kernel rotation with a sign
+    flip) over pages equals the contiguous call bit for bit."""
+    from omnistack_rs.cache import paged_attention
+    from omnistack_rs.kernels.fused_attention import omni_attn
+    B, Hq, Hkv, T, S, uid, L, R, HID = 8, 32, 8, 1, 50, 2, 16, 8, 128
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=341, user_id=uid)
+    q = _data.query((B, Hq, T, 128), seed=342)
+    la, lb = (t.to(torch.bfloat16) for t in _data.lora_bank(L, R, HID, Hq * 128))   # fused prologue path
+    ids = _data.lora_ids(B, L)
+    xh = _data.query((B, T, HID), seed=343)
+    s = _data.sign_flip(128)
+    cache, pt, lt = _paged(device, kn, kq, kr, vn, 16, seed=17)
+    kw = dict(user_id=uid, rotate_q=True, sign_flip=s.to(device), x=xh.to(device), lora_a=la.to(device),
+              lora_b=lb.to(device), lora_indices=ids.to(device), lora_alpha=0.5)
+    got = paged_attention(q.to(device), cache, pt, lt, cb.to(device), **kw)
+    ref = omni_attn(*(t.to(device) for t in (q, kn, kq, kr, vn, cb)), **kw)
+    assert torch.equal(got, ref), f"paged LoRA differs by {(got - ref).abs().max().item():.3e}"
+
+
+def test_paged_bad_pages_and_empty_sequences(device):
+    """Without host validation a page id outside the pool or a length past
+    the table gives NaN rows for that sequence only, and an empty sequence
+    (no keys) gives NaN rows; with validation the host raises."""
+    from omnistack_rs.cache import paged_attention
+    B, Hq, Hkv, T, S, uid = 4, 8, 2, 1, 64, 6
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=351, user_id=uid)
+    q = _data.query((B, Hq, T, 128), seed=352).to(device)
+    cache, pt, lt = _paged(device, kn, kq, kr, vn, 16, seed=19)
+    ok = paged_attention(q, cache, pt, lt, cb.to(device), user_id=uid)
+    pt_bad = pt.clone()
+    pt_bad[1, 2] = cache.n_pages + 5
+    lt_bad = lt.clone()
+    lt_bad[2] = 0
+    lt_bad[3] = pt.shape[1] * 16 + 1
+    got = paged_attention(q, cache, pt_bad, lt_bad, cb.to(device), user_id=uid, validate=False)
+    assert torch.equal(got[0], ok[0])
+    for b in (1, 2, 3):
+        assert torch.isnan(got[b]).all(), f"sequence {b} should be NaN"
+    with pytest.raises(IndexError):
+        paged_attention(q, cache, pt_bad, lt, cb.to(device), user_id=uid)
+    with pytest.raises(ValueError):
+        paged_attention(q, cache, pt, lt_bad, cb.to(device), user_id=uid)

@@ -131,6 +131,62 @@ def test_attn_serve_host_checks(L):
     assert rc == _lib.OMNI_EINVAL and "NULL LoRA" in _lib.last_error()
 
 
+def test_attn_paged_host_checks(L):
+    from omnistack_rs import _lib
+
+    def call(n_pages=4, ps=16, pt=1, max_pages=2, lens=1, B=1, Hq=4, Hkv=2, T=1, ptr=None):
+        return L.omni_attn_paged(ptr, 2, ptr, ptr, ptr, ptr, n_pages, ps, pt, max_pages, lens,
+                                 None, None, None, 0, None, 0, 0, 0, 0.0,
+                                 ptr, 1, ptr, B, Hq, Hkv, T, 128, 1.0, 1, 0, 0, None, ptr, None, 0, None)
+
+    for ps in (8, 24, 2048):
+        assert call(ps=ps) == _lib.OMNI_EINVAL and "page_size" in _lib.last_error()
+    assert call(n_pages=0) == _lib.OMNI_EINVAL and "n_pages" in _lib.last_error()
+    assert call(n_pages=1 << 22) == _lib.OMNI_EINVAL and "pool too large" in _lib.last_error()
+    assert call(max_pages=1 << 21) == _lib.OMNI_EINVAL and "per sequence" in _lib.last_error()
+    assert call(pt=None) == _lib.OMNI_EINVAL and "page table" in _lib.last_error()
+    # more than 32 query rows per kv head (the decode kernel's limit), checked before any launch
+    assert call(T=9, Hq=8, Hkv=2, ptr=1) == _lib.OMNI_EINVAL and "query rows" in _lib.last_error()
+    assert call(B=0) == 0
+    ws = L.omni_attn_paged_workspace_size(4, 32, 8, 1, 20, 16, 2)
+    assert ws >= 4 * 32 * 128 * 2 and L.omni_attn_paged_workspace_size(0, 32, 8, 1, 20, 16, 2) == 0
+
+
+def test_paged_cache_host_side():
+    """The page allocator and writer (plain torch, any device): every
+    sequence read back through its page-table row equals the contiguous
+    cache it came from, pages are handed out in the generator's order, and
+    bad page sizes are refused."""
+    from omnistack_rs.cache import PagedKVCache
+    B, H, S, ps = 3, 2, 70, 16
+    g = torch.Generator().manual_seed(3)
+    kn = torch.randint(0, 256, (B, H, S, 64), generator=g, dtype=torch.uint8)
+    kq = torch.randint(0, 256, (B, H, S, 8), generator=g, dtype=torch.uint8)
+    kr = torch.rand(B, H, S, generator=g)
+    vn = torch.randint(0, 256, (B, H, S, 64), generator=g, dtype=torch.uint8)
+    lens = [70, 16, 33]
+    cache, pt, lt = PagedKVCache.from_contiguous(kn, kq, kr, vn, page_size=ps, seq_lens=lens, spare_pages=2,
+                                                 generator=torch.Generator().manual_seed(5))
+    assert lt.tolist() == lens and pt.dtype == torch.int32 and pt.shape == (B, 5)
+    used = [p for b in range(B) for p in pt[b].tolist() if p >= 0]
+    assert len(used) == len(set(used)) == 5 + 1 + 3 and cache.n_pages == len(used) + 2
+    for b, L in enumerate(lens):
+        tok = torch.arange(L)
+        pages = pt[b].long()[tok // ps]
+        for pool, src in ((cache.k_nibbles, kn), (cache.k_qjl, kq), (cache.k_norms, kr), (cache.v_nibbles, vn)):
+            assert torch.equal(pool[pages, :, tok % ps].transpose(0, 1), src[b, :, :L])
+    free = len(cache._free)
+    pages = cache.allocate(20)
+    assert len(pages) == 2 and len(cache._free) == free - 2 == 0
+    cache.free(pages)
+    assert len(cache._free) == free
+    with pytest.raises(RuntimeError):
+        cache.allocate(1000)
+    for bad in (8, 24, 2048):
+        with pytest.raises(ValueError):
+            PagedKVCache(4, 2, page_size=bad, device="cpu")
+
+
 def test_lloyd_max_host_checks(L):
     from omnistack_rs import _lib
     assert L.omni_lloyd_max_workspace_size(0, 1, 100) == 0
