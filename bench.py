@@ -18,7 +18,7 @@ C3's byte count (the device's achievable read rate, for comparison with
 `value`); the reference's CPU path (the oracle restatement) timed on a
 bounded C3 sample on this host.
 
-    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--only c3,c2,c2pool,c4,c5,c5d32,calib] [--no-cpu]
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--only c3,c3paged,c2,c2pool,c4,c5,c5d32,calib,dense] [--no-cpu]
 Prints one JSON line on stdout; progress goes to stderr.
 """
 from __future__ import annotations
@@ -303,11 +303,11 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="C3 (and the CPU baseline) only")
     ap.add_argument("--only", default="",
-                    help="comma-separated sections to run (c3, c2, c2pool, c4, c5, c5d32, calib, dense), for profiling one "
+                    help="comma-separated sections to run (c3, c3paged, c2, c2pool, c4, c5, c5d32, calib, dense), for profiling one "
                          "configuration; the JSON line then carries only those sections")
     args = ap.parse_args()
     sections = set(args.only.split(",")) if args.only else (
-        {"c3"} if args.no_extras else {"c3", "c2", "c2pool", "c4", "c5", "c5d32", "calib", "dense"})
+        {"c3"} if args.no_extras else {"c3", "c3paged", "c2", "c2pool", "c4", "c5", "c5d32", "calib", "dense"})
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -424,6 +424,38 @@ def main() -> int:
                          "note": "algorithmic bytes / (HIP-event time of the timed calls / steps), "
                                  "the calls that give `value`"},
         })
+
+    # ── C3 through a paged cache: the same 32 x 8192 tokens in 16-token pages
+    #    (the reference config's page size) assigned in random order ─────
+    if "c3paged" in sections:
+        from omnistack_rs.cache import PagedKVAttention, PagedKVCache
+        log("[bench] C3 paged: 32 x 8192 tokens in 16-token pages, random page order")
+        kn, kq, kr, vn, cb, q, sign = c3_inputs(dev)
+        cache, pt, lens = PagedKVCache.from_contiguous(kn, kq, kr, vn, page_size=16,
+                                                       generator=torch.Generator().manual_seed(47))
+        att_p = PagedKVAttention(cache, cb, n_heads=Hq, batch=C3_SHAPE["B"], max_pages=pt.shape[1], user_id=uid,
+                                 rotate_q=True, sign_flip=sign)
+        ref = PackedKVAttention(kn, kq, kr, vn, cb, n_heads=Hq, user_id=uid, rotate_q=True, sign_flip=sign)
+        # claims are dynamic (256 tiles per split), so the two calls sum in
+        # different orders: compare to the parity bar, not bit for bit
+        diff_p = float((att_p.run(q, pt, lens).clone() - ref.run(q)).abs().max())
+        del kn, kq, kr, vn, ref
+        bytes_p = (C3_SHAPE["B"] * Hkv * C3_SHAPE["S"] * BYTES_PER_TOKEN_HEAD + q.numel() * 2
+                   + C3_SHAPE["B"] * Hq * D * 4 + pt.numel() * 4)
+        step_p = lambda: att_p.run(q, pt, lens)
+        t_pw, t_pe = timed_region(step_p, args.steps, args.warmup, stream)
+        blocks_p = sustained_blocks(step_p, 1000, 50, stream)
+        med_p = statistics.median(blocks_p)
+        result["paged_c3"] = {
+            "GB_s": round(bytes_p / t_pw / 1e9, 1), "us_per_call": round(t_pw * 1e6, 2),
+            "us_per_call_events": round(t_pe * 1e6, 2), "sustained_median_block_us": round(med_p * 1e6, 2),
+            "GB_s_sustained_median": round(bytes_p / med_p / 1e9, 1), "bytes": bytes_p,
+            "max_abs_vs_contiguous": diff_p,
+            "note": "C3 through PagedKVAttention: 16-token pages in random pool order, one page-table "
+                    "row per sequence; timed like C3 (K calls, then 1000 in 50-call blocks)"}
+        log(f"[bench] C3 paged: {t_pw * 1e6:.1f} us/step (wall), sustained median block {med_p * 1e6:.1f} us "
+            f"-> {bytes_p / med_p / 1e9:.0f} GB/s; max-abs vs the contiguous call {diff_p:.2e}")
+        del cache, att_p
 
     # ── extras: C2 serving, C4 encode, C5 prefill ────────────────────────
     if "c2" in sections:

@@ -972,17 +972,16 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     // the table's width (tiles past the end) the last entry is read.
     bool page_bad = false;
     const int32_t *pt_row = PAGED ? a.page_table + b * a.max_pages : nullptr;
-    const int pj_max = PAGED ? (int)a.max_pages - 1 : 0;
-    const uint32_t pg_stride = PAGED ? (uint32_t)(a.Hkv * a.page_size) : 0u;   // pool rows per page
-    const uint32_t hk_rows = PAGED ? (uint32_t)(hk * a.page_size) : 0u;
     auto half_rows = [&](int t, uint32_t (&rb)[2]) {
+        const int sh = a.page_shift;
+        const uint32_t np = (uint32_t)a.n_pages;                  // < 2^26 (host check)
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int th = t + 16 * u;
-            const int32_t id = pt_row[imin(th >> a.page_shift, pj_max)];
-            const bool ok = id >= 0 && (int64_t)id < a.n_pages;
+            const uint32_t id = (uint32_t)pt_row[imin(th >> sh, (int)a.max_pages - 1)];
+            const bool ok = id < np;                                  // negative ids wrap past np
             page_bad = page_bad || (!ok && th < s_end);
-            rb[u] = (ok ? (uint32_t)id : 0u) * pg_stride + hk_rows + ((uint32_t)th & (uint32_t)(a.page_size - 1));
+            rb[u] = (((ok ? id : 0u) * (uint32_t)a.Hkv + (uint32_t)hk) << sh) + ((uint32_t)th & ((1u << sh) - 1u));
         }
     };
 
@@ -1376,9 +1375,9 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
         tile_step(ring[0], tile_tok(i_cur), tile_seq(i_cur));
         const int i_pre = wave + nw;
         if (i_pre < ntiles && PAGED) {
-            // paged: a claimed tile's page rows are read (and waited for)
-            // before the next claim is issued, so that wait does not also
-            // wait for the claim's atomic
+            // paged: a claimed tile's page rows (scalar loads) are read and
+            // waited for before the next claim is issued, so that wait does
+            // not also wait for the claim's atomic
             uint32_t rb[2];
             auto next_rows = [&](int i) {
                 half_rows(tile_tok(i), rb);

@@ -191,3 +191,88 @@ def paged_attention(q: torch.Tensor, cache: PagedKVCache, page_table: torch.Tens
         _lib.ptr(cb), per_head, _lib.ptr(gb), B, Hq, H, T, D, float(scale), int(with_qjl), int(causal),
         int(rotate_q), _lib.ptr(sf), _lib.ptr(out), _lib.ptr(ws), ws_bytes, _lib.stream_of(dev)))
     return out
+
+
+class PagedKVAttention:
+    """Prepared ``paged_attention`` over one page pool (serving loops).
+
+    Converts codebooks, uploads G and allocates the output and workspace
+    once for ``batch`` sequences of ``q_tokens`` query tokens and page
+    tables up to ``max_pages`` wide; ``run(q, page_table, seq_lens)`` then
+    enqueues a single library call on the current stream (no host sync, no
+    allocation: safe to capture in a HIP graph) and returns the reused
+    float32 output.  Page ids and lengths are not checked on the host: a
+    sequence with a page id outside the pool or a bad length gives NaN rows.
+    With a LoRA bank (``lora_a``, ``lora_b``, ``lora_alpha``),
+    ``run(q, page_table, seq_lens, x, lora_indices)`` applies the per-user
+    update of q inside the same call.
+    """
+
+    def __init__(self, cache: PagedKVCache, codebooks: torch.Tensor, n_heads: int, batch: int, max_pages: int,
+                 q_tokens: int = 1, user_id: int = 0, scale: Optional[float] = None, with_qjl: bool = True,
+                 q_dtype: torch.dtype = torch.bfloat16, rotate_q: bool = False,
+                 sign_flip: Optional[torch.Tensor] = None, causal: bool = False,
+                 lora_a: Optional[torch.Tensor] = None, lora_b: Optional[torch.Tensor] = None,
+                 lora_alpha: float = 1.0):
+        H, D = cache.n_kv_heads, cache.head_dim
+        if n_heads % H:
+            raise ValueError(f"n_heads={n_heads} must be divisible by n_kv_heads={H}")
+        if q_tokens * (n_heads // H) > 32:
+            raise ValueError("paged attention takes q_tokens * n_heads / n_kv_heads <= 32 query rows")
+        if q_dtype not in _lib.DTYPE_CODE:
+            raise ValueError(f"q_dtype must be one of {list(_lib.DTYPE_CODE)}")
+        _check_packed(cache.k_nibbles, cache.k_qjl if with_qjl else None, cache.k_norms if with_qjl else None,
+                      "cache.k_nibbles")
+        dev = cache.device
+        self.cache, self.B, self.Hq, self.T, self.max_pages = cache, int(batch), int(n_heads), int(q_tokens), int(max_pages)
+        self.cb, self.per_head = _prep_codebooks(codebooks, H, dev)
+        self.gb = _lib.g_bits(_lib.head_seeds(user_id, H), D, dev) if with_qjl else None
+        self.sf = _lib.sign_flip_i8(sign_flip, D, dev) if (rotate_q and sign_flip is not None) else None
+        self.scale = float(1.0 / math.sqrt(D) if scale is None else scale)
+        self.with_qjl, self.rotate_q, self.causal = int(with_qjl), int(rotate_q), int(causal)
+        self.qcode = _lib.dtype_code(q_dtype)
+        self.q_dtype = q_dtype
+        self.lora = None
+        if lora_a is not None:
+            n_loras, rank, hidden = lora_a.shape
+            wdt = torch.promote_types(lora_a.dtype, lora_b.dtype)
+            if wdt not in _lib.DTYPE_CODE:
+                wdt = torch.float32
+            self.lora = (lora_a.to(device=dev, dtype=wdt).contiguous(), lora_b.to(device=dev, dtype=wdt).contiguous(),
+                         _lib.dtype_code(wdt), wdt, int(hidden), int(rank), int(n_loras), float(lora_alpha))
+        self.out = torch.empty(self.B, n_heads, self.T, D, dtype=torch.float32, device=dev)
+        L = _lib.lib()
+        self.ws_bytes = L.omni_attn_paged_workspace_size(self.B, n_heads, H, self.T, self.max_pages,
+                                                         cache.page_size, self.qcode)
+        self.ws = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device=dev)
+
+    def run(self, q: torch.Tensor, page_table: torch.Tensor, seq_lens: torch.Tensor,
+            x: Optional[torch.Tensor] = None, lora_indices: Optional[torch.Tensor] = None) -> torch.Tensor:
+        c = self.cache
+        if tuple(q.shape) != (self.B, self.Hq, self.T, c.head_dim) or q.dtype != self.q_dtype:
+            raise ValueError(f"q must be {self.q_dtype} {(self.B, self.Hq, self.T, c.head_dim)}")
+        if tuple(page_table.shape) != (self.B, self.max_pages) or page_table.dtype != torch.int32:
+            raise ValueError(f"page_table must be int32 {(self.B, self.max_pages)}")
+        if seq_lens.dtype != torch.int32 or seq_lens.numel() != self.B:
+            raise ValueError(f"seq_lens must be int32 with {self.B} entries")
+        dev = c.device
+        for t in (q, page_table, seq_lens, x, lora_indices):
+            if t is not None and t.device != dev:
+                raise ValueError(f"q, page_table, seq_lens, x and lora_indices must be on {dev}")
+        if self.lora is not None:
+            if x is None or lora_indices is None:
+                raise ValueError("this attention has a LoRA bank: pass x and lora_indices")
+            la, lb, wcode, wdt, hidden, rank, n_loras, alpha = self.lora
+            xc = x if x.dtype == wdt else x.to(wdt)
+            lora = (_lib.ptr(xc.contiguous()), _lib.ptr(la), _lib.ptr(lb), wcode, _lib.ptr(lora_indices),
+                    hidden, rank, n_loras, alpha)
+        else:
+            lora = (None, None, None, 0, None, 0, 0, 0, 0.0)
+        _lib.check(_lib.lib().omni_attn_paged(
+            _lib.ptr(q.contiguous()), self.qcode, _lib.ptr(c.k_nibbles), _lib.ptr(c.k_qjl if self.with_qjl else None),
+            _lib.ptr(c.k_norms if self.with_qjl else None), _lib.ptr(c.v_nibbles), c.n_pages, c.page_size,
+            _lib.ptr(page_table), self.max_pages, _lib.ptr(seq_lens), *lora,
+            _lib.ptr(self.cb), self.per_head, _lib.ptr(self.gb), self.B, self.Hq, c.n_kv_heads, self.T,
+            c.head_dim, self.scale, self.with_qjl, self.causal, self.rotate_q, _lib.ptr(self.sf),
+            _lib.ptr(self.out), _lib.ptr(self.ws), self.ws_bytes, _lib.stream_of(dev)))
+        return self.out

@@ -138,3 +138,35 @@ def test_paged_bad_pages_and_empty_sequences(device):
         paged_attention(q, cache, pt_bad, lt, cb.to(device), user_id=uid)
     with pytest.raises(ValueError):
         paged_attention(q, cache, pt, lt_bad, cb.to(device), user_id=uid)
+
+
+def test_prepared_paged_attention_and_graph_replay(device):
+    """PagedKVAttention.run equals paged_attention bit for bit, and replays
+    of a HIP graph of it (new page tables and lengths written between
+    replays) each equal an eager call on the same inputs."""
+    from omnistack_rs.cache import PagedKVAttention, paged_attention
+    B, Hq, Hkv, T, S, uid = 4, 32, 8, 1, 130, 8
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=361, user_id=uid)
+    cache, pt, lt = _paged(device, kn, kq, kr, vn, 16, seed=23)
+    att = PagedKVAttention(cache, cb.to(device), n_heads=Hq, batch=B, max_pages=pt.shape[1], user_id=uid)
+    q = _data.query((B, Hq, T, 128), seed=362).to(device)
+    got = att.run(q, pt, lt).clone()
+    assert torch.equal(got, paged_attention(q, cache, pt, lt, cb.to(device), user_id=uid))
+    qs, pts, lts = q.clone(), pt.clone(), lt.clone()
+    att.run(qs, pts, lts)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        att.run(qs, pts, lts)
+    for r in range(3):
+        lens = torch.tensor([130 - 17 * r, 1 + r, 64, 129], dtype=torch.int32)
+        q2 = _data.query((B, Hq, T, 128), seed=370 + r).to(device)
+        qs.copy_(q2)
+        lts.copy_(lens.to(device))
+        pts.copy_(pt.flip(0).roll(r, 0))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        replay = att.out.clone()
+        eager = paged_attention(q2, cache, pts.clone(), lts.clone(), cb.to(device), user_id=uid, validate=False)
+        assert torch.equal(replay, eager), f"replay {r} differs"
