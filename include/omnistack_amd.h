@@ -282,14 +282,15 @@ int omni_attn_serve(const void *q, int q_dtype, const int64_t *cache_index, int6
  * The serving step over a page-granular cache.  The reference plans a paged
  * KV cache (MANIFEST.md:211-215; page_size = 16 tokens, config.py:43) but
  * gathers whole sequences instead (scripts/run_criteo_benchmark.py:553-557);
- * this is that gather as page lookups inside the decode kernel.
+ * this is that gather as page lookups inside the attention kernels (decode
+ * for up to 32 query rows per kv head, T * Hq / Hkv; chunked prefill above).
  * Pools (k_nib, k_qjl, k_norms, v_nib) are shaped like a contiguous cache
  * with pages as the batch axis: (n_pages, Hkv, page_size, ...).  Sequence b
  * holds seq_lens[b] tokens; token s sits in page page_table[b * max_pages +
  * s / page_size] at slot s % page_size.  page_size is a power of two in
- * [16, 1024]; n_pages * Hkv * page_size < 2^26; head_dim 128 and
- * T * Hq / Hkv <= 32 query rows per kv head.  causal != 0 lets query token
- * t see keys <= seq_lens[b] - T + t.  A page id outside [0, n_pages) among a
+ * [16, 1024]; n_pages * Hkv * page_size < 2^26; head_dim 128.  causal != 0
+ * lets query token t see keys <= seq_lens[b] - T + t (a row with none is
+ * NaN).  A page id outside [0, n_pages) among a
  * sequence's pages, or a length outside [0, max_pages * page_size], gives
  * NaN rows for that sequence and reads nothing out of bounds; a length of 0
  * gives NaN rows (no keys).  LoRA as omni_attn_serve (lora_a NULL: none).

@@ -696,6 +696,25 @@ __device__ __forceinline__ void tile_load_paged(TileRaw &R, const DecBufs &P, co
         R.v[i] = __builtin_amdgcn_raw_buffer_load_b32(P.vn, O.v + rb[i / 4] * 64u + 64u * (i % 4), 0, 0);
 }
 
+// Paged cache: pool rows of the two 16-token halves of the tile at token t
+// (wave-uniform scalar loads of the page table row `pt_row`).  A page id
+// outside the pool reads page 0 and, for a half that holds tokens of the
+// sequence (below `s_end`), sets `bad` (the sequence's rows come out NaN);
+// past the table's width (tiles past the end) the last entry is read.
+__device__ __forceinline__ void paged_half_rows(const AttnArgs &a, const int32_t *pt_row, int hk, int t, int s_end,
+                                                bool &bad, uint32_t (&rb)[2]) {
+    const int sh = a.page_shift;
+    const uint32_t np = (uint32_t)a.n_pages;                  // < 2^26 (host check)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int th = t + 16 * u;
+        const uint32_t id = (uint32_t)pt_row[imin(th >> sh, (int)a.max_pages - 1)];
+        const bool ok = id < np;                                  // negative ids wrap past np
+        bad = bad || (!ok && th < s_end);
+        rb[u] = (((ok ? id : 0u) * (uint32_t)a.Hkv + (uint32_t)hk) << sh) + ((uint32_t)th & ((1u << sh) - 1u));
+    }
+}
+
 __device__ __forceinline__ uint32_t cvt_pk_h2(float x, float y) {
     typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
     typedef float f2_t __attribute__((ext_vector_type(2)));
@@ -965,25 +984,11 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     OFS.nr = 16u * g + 4u * (n & 3);      // norm of token 4g + n % 4 (of each 16-token half)
     OFS.v = 256u * g + 4u * n;
 
-    // Paged cache: pool rows of the two 16-token halves of the tile at token
-    // t (wave-uniform scalar loads of the page table).  A page id outside the
-    // pool reads page 0 and, for a half that holds tokens of the sequence,
-    // marks this wave's state bad (the sequence's rows come out NaN); past
-    // the table's width (tiles past the end) the last entry is read.
+    // Paged cache: pool rows of a tile's two halves; a page id outside the
+    // pool marks this wave's state bad (the sequence's rows come out NaN)
     bool page_bad = false;
     const int32_t *pt_row = PAGED ? a.page_table + b * a.max_pages : nullptr;
-    auto half_rows = [&](int t, uint32_t (&rb)[2]) {
-        const int sh = a.page_shift;
-        const uint32_t np = (uint32_t)a.n_pages;                  // < 2^26 (host check)
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int th = t + 16 * u;
-            const uint32_t id = (uint32_t)pt_row[imin(th >> sh, (int)a.max_pages - 1)];
-            const bool ok = id < np;                                  // negative ids wrap past np
-            page_bad = page_bad || (!ok && th < s_end);
-            rb[u] = (((ok ? id : 0u) * (uint32_t)a.Hkv + (uint32_t)hk) << sh) + ((uint32_t)th & ((1u << sh) - 1u));
-        }
-    };
+    auto half_rows = [&](int t, uint32_t (&rb)[2]) { paged_half_rows(a, pt_row, hk, t, s_end, page_bad, rb); };
 
     // ── prologue loads: branch-free buffer loads (an absent input gets a
     //    zero-size descriptor and reads 0), issued before the cache
@@ -1527,7 +1532,7 @@ constexpr int kPreStageOff = kPreCbOff + 64;                     // per wave: q 
 constexpr int kPreQsrOff = kPreStageOff + kPreWaves * 32 * 128 * 2;   // per wave: 32 x f32 score scales
 constexpr int kPreLdsBytes = kPreQsrOff + kPreWaves * 32 * 4;
 
-template <bool QJL, int NCB, int PF, bool QLO>
+template <bool QJL, int NCB, int PF, bool QLO, bool PAGED>
 __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArgs a) {
     constexpr int D = 128, QD = 64, RW = 16 * NCB;      // rows per wave
     static_assert(!QLO || NCB == 1, "the f32 remainder plane shares the 32-row stage area");
@@ -1716,38 +1721,73 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
     __syncthreads();   // byte LUT complete
 
     // ── key range of this wave: causal limits of its rows ─────────────────
+    // paged: the sequence's own length (one outside [0, capacity] reads
+    // nothing and its rows come out NaN); a causal chunk ends at that length
+    int64_t seq_len = a.S;
+    bool len_bad = false;
+    if constexpr (PAGED) {
+        const int32_t L = a.seq_lens[b];
+        len_bad = L < 0 || (int64_t)L > a.S;
+        seq_len = len_bad ? 0 : L;
+    }
+    const bool causal = a.causal_offset >= 0;
+    const int64_t coff = PAGED ? seq_len - a.T : a.causal_offset;
     const int s_begin = split * (int)a.split_len;
-    int s_end = (int)imin64(a.S, (int64_t)s_begin + a.split_len);
+    int s_end = (int)imin64(seq_len, (int64_t)s_begin + a.split_len);
     int lim[NCB];
     bool rowok[NCB];
 #pragma unroll
     for (int c = 0; c < NCB; ++c) {
         const int rho = row0 + 16 * c + n;
         rowok[c] = rho < nrows_total;
-        lim[c] = (a.causal_offset >= 0) ? (int)imin64(a.causal_offset + (rowok[c] ? rho : 0) / a.G, 0x7fffffff)
-                                        : 0x7fffffff;
+        lim[c] = causal ? (int)imax64(imin64(coff + (rowok[c] ? rho : 0) / a.G, 0x7fffffff), -1) : 0x7fffffff;
     }
     int full_end = s_end;
-    if (a.causal_offset >= 0) {
+    if (causal) {
         const int rlo = imin(row0, nrows_total - 1), rhi = imin(row0 + RW - 1, nrows_total - 1);
-        const int64_t lo_lim = a.causal_offset + rlo / a.G, hi_lim = a.causal_offset + rhi / a.G;
+        const int64_t lo_lim = coff + rlo / a.G, hi_lim = coff + rhi / a.G;
         full_end = (int)imin64((int64_t)s_end, lo_lim + 1);
         s_end = (int)imin64((int64_t)s_end, hi_lim + 1);
     }
-    bool seq_bad;
-    const int64_t kv_base = (cache_seq(a, b, seq_bad) * a.Hkv + hk) * a.S;
+    s_end = imax(s_end, s_begin);
+    full_end = imax(full_end, s_begin);
+    bool seq_bad = false;
     DecBufs P;
-    P.kn = __builtin_amdgcn_make_buffer_rsrc((void *)(a.k_nib + kv_base * 64), (short)0, s_end * 64, kBufWord3);
-    P.vn = __builtin_amdgcn_make_buffer_rsrc((void *)(a.v_nib + kv_base * 64), (short)0, s_end * 64, kBufWord3);
-    P.kq = __builtin_amdgcn_make_buffer_rsrc((void *)(QJL ? a.k_qjl + kv_base * 8 : a.k_nib), (short)0,
-                                             QJL ? s_end * 8 : 0, kBufWord3);
-    P.kr = __builtin_amdgcn_make_buffer_rsrc((void *)(QJL ? a.k_norms + kv_base : (const float *)a.k_nib), (short)0,
-                                             QJL ? s_end * 4 : 0, kBufWord3);
+    if constexpr (PAGED) {
+        // the whole pool (its row count times 64 fits 32 bits: the host checks)
+        const uint32_t rows = (uint32_t)(a.n_pages * a.Hkv * a.page_size);
+        P.kn = __builtin_amdgcn_make_buffer_rsrc((void *)a.k_nib, (short)0, rows * 64u, kBufWord3);
+        P.vn = __builtin_amdgcn_make_buffer_rsrc((void *)a.v_nib, (short)0, rows * 64u, kBufWord3);
+        P.kq = __builtin_amdgcn_make_buffer_rsrc((void *)(QJL ? a.k_qjl : a.k_nib), (short)0, QJL ? rows * 8u : 0u,
+                                                 kBufWord3);
+        P.kr = __builtin_amdgcn_make_buffer_rsrc((void *)(QJL ? a.k_norms : (const float *)a.k_nib), (short)0,
+                                                 QJL ? rows * 4u : 0u, kBufWord3);
+    } else {
+        const int64_t kv_base = (cache_seq(a, b, seq_bad) * a.Hkv + hk) * a.S;
+        P.kn = __builtin_amdgcn_make_buffer_rsrc((void *)(a.k_nib + kv_base * 64), (short)0, s_end * 64, kBufWord3);
+        P.vn = __builtin_amdgcn_make_buffer_rsrc((void *)(a.v_nib + kv_base * 64), (short)0, s_end * 64, kBufWord3);
+        P.kq = __builtin_amdgcn_make_buffer_rsrc((void *)(QJL ? a.k_qjl + kv_base * 8 : a.k_nib), (short)0,
+                                                 QJL ? s_end * 8 : 0, kBufWord3);
+        P.kr = __builtin_amdgcn_make_buffer_rsrc((void *)(QJL ? a.k_norms + kv_base : (const float *)a.k_nib),
+                                                 (short)0, QJL ? s_end * 4 : 0, kBufWord3);
+    }
     DecOffsets OFS;
     OFS.k = (uint32_t)n * 64u + 16u * g;
     OFS.sg = (uint32_t)n * 8u;
     OFS.nr = 16u * g + 4u * (n & 3);      // norm of token 4g + n % 4 (of each 16-token half)
     OFS.v = 256u * g + 4u * n;
+    bool page_bad = false;
+    const int32_t *pt_row = PAGED ? a.page_table + b * a.max_pages : nullptr;
+    // one tile's loads (paged: from the pool rows of its two halves)
+    auto load_tile = [&](TileRaw &R, int t) {
+        if constexpr (PAGED) {
+            uint32_t rb[2];
+            paged_half_rows(a, pt_row, hk, t, s_end, page_bad, rb);
+            tile_load_paged<QJL>(R, P, OFS, rb);
+        } else {
+            tile_load<QJL>(R, P, OFS, t);
+        }
+    };
     const uint32_t laneoff = (uint32_t)(lane & 31) * 8u;
     const uint32_t slane = (uint32_t)kSlutOff | laneoff;
     const half8_t ones = as_half8(0x3C003C00u, 0u, 0x3C003C00u, 0u);
@@ -1909,13 +1949,13 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
     constexpr int stride = kDecTile;
     TileRaw ring[PF];
 #pragma unroll
-    for (int p = 0; p < PF - 1; ++p) tile_load<QJL>(ring[p], P, OFS, s_begin + p * stride);
+    for (int p = 0; p < PF - 1; ++p) load_tile(ring[p], s_begin + p * stride);
     int tt0 = s_begin;
     for (; tt0 + (PF - 1) * stride < s_end; tt0 += PF * stride) {
 #pragma unroll
         for (int p = 0; p < PF; ++p) {
             __builtin_amdgcn_sched_barrier(0);
-            tile_load<QJL>(ring[(p + PF - 1) % PF], P, OFS, tt0 + (p + PF - 1) * stride);
+            load_tile(ring[(p + PF - 1) % PF], tt0 + (p + PF - 1) * stride);
             __builtin_amdgcn_sched_barrier(0);
             tile_step(ring[p], tt0 + p * stride);
         }
@@ -1935,7 +1975,7 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
     for (int c = 0; c < NCB; ++c) {
         const int rho = row0 + 16 * c + ne;
         if (!rowok[c]) continue;
-        const float l = seq_bad ? __builtin_nanf("") : lacc[c][0];
+        const float l = (seq_bad || page_bad || len_bad) ? __builtin_nanf("") : lacc[c][0];
         if (a.splits == 1) {
             const int t = rho / a.G, hq = hk * a.G + (rho - t * a.G);
             float *o = a.out + ((b * a.Hq + hq) * a.T + t) * D;
@@ -2493,8 +2533,7 @@ static int attn_run(const void *q, int q_dtype, const uint8_t *k_nib, const uint
     OMNI_CHECK_ARG(T * (Hq / Hkv) < (int64_t(1) << 31), "omni_attn: T * (n_heads / n_kv_heads) must be < 2^31");
     OMNI_CHECK_ARG(seq_index == nullptr || n_seqs >= 1, "omni_attn: a cache index needs a pool of >= 1 sequences");
     Plan p = make_plan(B, Hq, Hkv, T, S, head_dim, q_dtype == OMNI_F32, paged != nullptr);
-    OMNI_CHECK_ARG(paged == nullptr || (head_dim == 128 && p.dec128),
-                   "omni_attn_paged: needs head_dim 128 and T * n_heads / n_kv_heads <= %d query rows", kPrefillMinRows);
+    OMNI_CHECK_ARG(paged == nullptr || head_dim == 128, "omni_attn_paged: needs head_dim 128");
     OMNI_CHECK_ARG(Hkv <= 65535 && ((B + p.spb - 1) / p.spb) * p.n_rchunks <= 65535 && p.splits <= 2147483647,
                    "omni_attn: grid too large (batch x row chunks must be <= 65535)");
     // LoRA: fused into the D=128 decode prologue; other kernels read q_eff
@@ -2549,14 +2588,25 @@ static int attn_run(const void *q, int q_dtype, const uint8_t *k_nib, const uint
     a.page_shift = paged ? paged->page_shift : 0;
     dim3 grid((unsigned)p.splits, (unsigned)Hkv, (unsigned)(((B + p.spb - 1) / p.spb) * p.n_rchunks));
     dim3 block(64 * p.nw);
-    if (p.prefill) {
+    if (p.prefill && paged) {
         const bool qlo = q_dtype == OMNI_F32;
+        hipStream_t st = as_stream(stream);
         if (with_qjl) {
-            if (qlo) hipLaunchKernelGGL((attn_prefill128_kernel<true, 1, 2, true>), grid, block, 0, as_stream(stream), a);
-            else hipLaunchKernelGGL((attn_prefill128_kernel<true, kPreNcb, 2, false>), grid, block, 0, as_stream(stream), a);
+            if (qlo) hipLaunchKernelGGL((attn_prefill128_kernel<true, 1, 2, true, true>), grid, block, 0, st, a);
+            else hipLaunchKernelGGL((attn_prefill128_kernel<true, kPreNcb, 2, false, true>), grid, block, 0, st, a);
         } else {
-            if (qlo) hipLaunchKernelGGL((attn_prefill128_kernel<false, 1, 2, true>), grid, block, 0, as_stream(stream), a);
-            else hipLaunchKernelGGL((attn_prefill128_kernel<false, kPreNcb, 2, false>), grid, block, 0, as_stream(stream), a);
+            if (qlo) hipLaunchKernelGGL((attn_prefill128_kernel<false, 1, 2, true, true>), grid, block, 0, st, a);
+            else hipLaunchKernelGGL((attn_prefill128_kernel<false, kPreNcb, 2, false, true>), grid, block, 0, st, a);
+        }
+    } else if (p.prefill) {
+        const bool qlo = q_dtype == OMNI_F32;
+        hipStream_t st = as_stream(stream);
+        if (with_qjl) {
+            if (qlo) hipLaunchKernelGGL((attn_prefill128_kernel<true, 1, 2, true, false>), grid, block, 0, st, a);
+            else hipLaunchKernelGGL((attn_prefill128_kernel<true, kPreNcb, 2, false, false>), grid, block, 0, st, a);
+        } else {
+            if (qlo) hipLaunchKernelGGL((attn_prefill128_kernel<false, 1, 2, true, false>), grid, block, 0, st, a);
+            else hipLaunchKernelGGL((attn_prefill128_kernel<false, kPreNcb, 2, false, false>), grid, block, 0, st, a);
         }
     } else if (p.prefill32) {
         const bool qlo = q_dtype == OMNI_F32;
@@ -2666,9 +2716,9 @@ extern "C" int omni_attn_serve(const void *q, int q_dtype, const int64_t *cache_
 // pages: nibbles (n_pages, Hkv, page_size, 64), signs (.., 8), norms
 // (n_pages, Hkv, page_size), V (.., 64).  Sequence b holds seq_lens[b] tokens
 // in pages page_table[b * max_pages + j], j < ceil(len / page_size); entries
-// past that are never read for keys.  D = 128, T * Hq / Hkv <= 32 query rows
-// per kv head (the decode kernel).  causal != 0 aligns query token t with
-// key len - T + t.
+// past that are never read for keys.  D = 128; up to 32 query rows per kv
+// head (T * Hq / Hkv) run the decode kernel, more the chunked-prefill kernel.
+// causal != 0 aligns query token t with key len - T + t.
 
 static bool paged_args_ok(int64_t B, int Hkv, int64_t n_pages, int page_size, int64_t max_pages, int &shift) {
     shift = 0;

@@ -14,7 +14,8 @@ the reference's packed layout with the batch axis as pages:
 A sequence is a list of pages (one row of an int32 page table) and a length;
 token s of sequence b sits in page ``page_table[b, s // page_size]`` at slot
 ``s % page_size``.  ``paged_attention`` is one call into libomnistack_amd.so
-(``omni_attn_paged``): the decode kernel reads each 16-token half-tile from
+(``omni_attn_paged``): the decode kernel (up to 32 query rows per kv head)
+or the chunked-prefill kernel (more rows) reads each 16-token half-tile from
 its page in place, with the same arithmetic as the contiguous ``omni_attn``
 (so a sequence gives the same result whichever pages hold it).
 """
@@ -131,8 +132,10 @@ def paged_attention(q: torch.Tensor, cache: PagedKVCache, page_table: torch.Tens
                     validate: bool = True) -> torch.Tensor:
     """``omni_attn`` over a paged cache: query batch entry b attends the
     first ``seq_lens[b]`` tokens of the sequence in row b of ``page_table``.
-    q (B, n_heads, T, 128) with T * n_heads / n_kv_heads <= 32; ``causal``
-    aligns query token t with key ``seq_lens[b] - T + t``.  Returns float32
+    q (B, n_heads, T, 128); up to 32 query rows per kv head
+    (T * n_heads / n_kv_heads) run the decode kernel, more the chunked-prefill
+    kernel.  ``causal`` aligns query token t with key ``seq_lens[b] - T + t``
+    (a row with no visible key is NaN, as in the reference).  Returns float32
     (B, n_heads, T, 128).  With ``validate``, page ids outside the pool and
     lengths beyond the table raise on the host (one device-to-host copy);
     without it such sequences give NaN rows, as does a length of 0."""
@@ -144,8 +147,6 @@ def paged_attention(q: torch.Tensor, cache: PagedKVCache, page_table: torch.Tens
         raise ValueError(f"q head_dim {D} differs from the cache's {cache.head_dim}")
     if Hq % H:
         raise ValueError(f"n_heads={Hq} must be divisible by n_kv_heads={H}")
-    if T * (Hq // H) > 32:
-        raise ValueError(f"paged attention takes T * n_heads / n_kv_heads <= 32 query rows, got {T * (Hq // H)}")
     if page_table.dim() != 2 or page_table.shape[0] != B:
         raise ValueError(f"page_table must be ({B}, max_pages), got {tuple(page_table.shape)}")
     _check_packed(cache.k_nibbles, cache.k_qjl if with_qjl else None, cache.k_norms if with_qjl else None,
@@ -217,8 +218,6 @@ class PagedKVAttention:
         H, D = cache.n_kv_heads, cache.head_dim
         if n_heads % H:
             raise ValueError(f"n_heads={n_heads} must be divisible by n_kv_heads={H}")
-        if q_tokens * (n_heads // H) > 32:
-            raise ValueError("paged attention takes q_tokens * n_heads / n_kv_heads <= 32 query rows")
         if q_dtype not in _lib.DTYPE_CODE:
             raise ValueError(f"q_dtype must be one of {list(_lib.DTYPE_CODE)}")
         _check_packed(cache.k_nibbles, cache.k_qjl if with_qjl else None, cache.k_norms if with_qjl else None,

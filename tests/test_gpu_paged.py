@@ -6,8 +6,8 @@ contiguous kernel gives on the same tokens (same kernel arithmetic, only
 the addresses differ), and both must meet the oracle bar (max-abs <= 2e-3,
 mean-abs <= 2e-4).  Ragged lengths, page sizes 16 / 32 / 64, split-K over
 long sequences, causal multi-token queries, LoRA with in-kernel rotation,
-and the error paths (page ids outside the pool, empty sequences) are
-covered.  The reference has no paged cache (it gathers whole sequences,
+chunked prefill over pages (more than 32 query rows per kv head), and the
+error paths (page ids outside the pool, empty sequences) are covered.  The reference has no paged cache (it gathers whole sequences,
 scripts/run_criteo_benchmark.py:553-557); its per-sequence semantics are
 those of _fused_attn_python (fused_attention.py:435-466).
 """
@@ -170,3 +170,69 @@ def test_prepared_paged_attention_and_graph_replay(device):
         replay = att.out.clone()
         eager = paged_attention(q2, cache, pts.clone(), lts.clone(), cb.to(device), user_id=uid, validate=False)
         assert torch.equal(replay, eager), f"replay {r} differs"
+
+
+@pytest.mark.parametrize("page_size", [16, 32])
+@pytest.mark.parametrize("with_qjl", [True, False])
+def test_paged_prefill_equals_contiguous(device, page_size, with_qjl):
+    """A 40-token causal chunk (160 query rows per kv head: the chunked-prefill
+    kernel) over 600 tokens spread over pages equals the contiguous call bit
+    for bit (static tile order, the same split plan) and meets the oracle bar."""
+    from omnistack_rs.cache import paged_attention
+    from omnistack_rs.kernels.fused_attention import omni_attn
+    B, Hq, Hkv, T, S, uid = 2, 32, 8, 40, 600, 7
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=371, user_id=uid)
+    q = _data.query((B, Hq, T, 128), seed=372)
+    cache, pt, lens = _paged(device, kn, kq, kr, vn, page_size, seed=page_size + 1)
+    got = paged_attention(q.to(device), cache, pt, lens, cb.to(device), user_id=uid, with_qjl=with_qjl, causal=True)
+    ref = omni_attn(*(t.to(device) for t in (q, kn, kq, kr, vn, cb)), user_id=uid, with_qjl=with_qjl,
+                    causal_offset=S - T)
+    assert torch.equal(got, ref), f"paged prefill differs from contiguous by {(got - ref).abs().max().item():.3e}"
+    want = restate.fused_attn_python(q.float(), kn, kq, kr, vn, cb, uid, 1 / math.sqrt(128), with_qjl,
+                                     mask=_causal_mask(T, S, S - T))
+    _assert_close(got, want, f"paged prefill ps{page_size} qjl{with_qjl}")
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_paged_prefill_ragged_lengths(device, causal):
+    """24 query tokens x 4 heads per kv head (96 rows) over ragged lengths in
+    64-token pages, split over the capacity; each sequence against the
+    oracle on its own tokens (causal: aligned to its end)."""
+    from omnistack_rs.cache import paged_attention
+    B, Hq, Hkv, T, S, uid = 3, 16, 4, 24, 1100, 9
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=381, user_id=uid)
+    q = _data.query((B, Hq, T, 128), seed=382)
+    lens = [1100, 64, 301]
+    cache, pt, lt = _paged(device, kn, kq, kr, vn, 64, lens=lens, seed=29)
+    got = paged_attention(q.to(device), cache, pt, lt, cb.to(device), user_id=uid, causal=causal).cpu()
+    for b, L in enumerate(lens):
+        sl = slice(b, b + 1)
+        mask = _causal_mask(T, L, L - T) if causal else None
+        want = restate.fused_attn_python(q[sl].float(), kn[sl, :, :L], kq[sl, :, :L], kr[sl, :, :L],
+                                         vn[sl, :, :L], cb, uid, 1 / math.sqrt(128), True, mask=mask)
+        _assert_close(got[sl], want, f"paged prefill causal{causal} b{b} len{L}")
+
+
+def test_paged_prefill_bad_page_and_prepared(device):
+    """Prefill over pages: a page id outside the pool gives NaN rows for that
+    sequence only; the prepared class (with a LoRA bank: the gather-apply
+    update into its workspace) equals paged_attention bit for bit."""
+    from omnistack_rs.cache import PagedKVAttention, paged_attention
+    B, Hq, Hkv, T, S, uid, L, R, HID = 2, 16, 4, 12, 200, 5, 8, 8, 128
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=391, user_id=uid)
+    q = _data.query((B, Hq, T, 128), seed=392).to(device)
+    cache, pt, lt = _paged(device, kn, kq, kr, vn, 16, seed=31)
+    ok = paged_attention(q, cache, pt, lt, cb.to(device), user_id=uid, causal=True)
+    pt_bad = pt.clone()
+    pt_bad[1, 3] = -2
+    got = paged_attention(q, cache, pt_bad, lt, cb.to(device), user_id=uid, causal=True, validate=False)
+    assert torch.equal(got[0], ok[0]) and torch.isnan(got[1]).all()
+    la, lb = (t.to(torch.bfloat16) for t in _data.lora_bank(L, R, HID, Hq * 128))
+    ids = _data.lora_ids(B, L).to(device)
+    xh = _data.query((B, T, HID), seed=393).to(device)
+    att = PagedKVAttention(cache, cb.to(device), n_heads=Hq, batch=B, max_pages=pt.shape[1], q_tokens=T,
+                           user_id=uid, causal=True, lora_a=la.to(device), lora_b=lb.to(device), lora_alpha=0.5)
+    run = att.run(q, pt, lt, xh, ids).clone()
+    want = paged_attention(q, cache, pt, lt, cb.to(device), user_id=uid, causal=True, x=xh,
+                           lora_a=la.to(device), lora_b=lb.to(device), lora_indices=ids, lora_alpha=0.5)
+    assert torch.equal(run, want)

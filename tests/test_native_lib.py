@@ -134,10 +134,10 @@ def test_attn_serve_host_checks(L):
 def test_attn_paged_host_checks(L):
     from omnistack_rs import _lib
 
-    def call(n_pages=4, ps=16, pt=1, max_pages=2, lens=1, B=1, Hq=4, Hkv=2, T=1, ptr=None):
+    def call(n_pages=4, ps=16, pt=1, max_pages=2, lens=1, B=1, Hq=4, Hkv=2, T=1, ptr=None, D=128):
         return L.omni_attn_paged(ptr, 2, ptr, ptr, ptr, ptr, n_pages, ps, pt, max_pages, lens,
                                  None, None, None, 0, None, 0, 0, 0, 0.0,
-                                 ptr, 1, ptr, B, Hq, Hkv, T, 128, 1.0, 1, 0, 0, None, ptr, None, 0, None)
+                                 ptr, 1, ptr, B, Hq, Hkv, T, D, 1.0, 1, 0, 0, None, ptr, None, 0, None)
 
     for ps in (8, 24, 2048):
         assert call(ps=ps) == _lib.OMNI_EINVAL and "page_size" in _lib.last_error()
@@ -145,8 +145,8 @@ def test_attn_paged_host_checks(L):
     assert call(n_pages=1 << 22) == _lib.OMNI_EINVAL and "pool too large" in _lib.last_error()
     assert call(max_pages=1 << 21) == _lib.OMNI_EINVAL and "per sequence" in _lib.last_error()
     assert call(pt=None) == _lib.OMNI_EINVAL and "page table" in _lib.last_error()
-    # more than 32 query rows per kv head (the decode kernel's limit), checked before any launch
-    assert call(T=9, Hq=8, Hkv=2, ptr=1) == _lib.OMNI_EINVAL and "query rows" in _lib.last_error()
+    # head_dim 32 has no paged kernel: refused before any launch
+    assert call(T=9, Hq=8, Hkv=2, ptr=1, D=32) == _lib.OMNI_EINVAL and "head_dim 128" in _lib.last_error()
     assert call(B=0) == 0
     ws = L.omni_attn_paged_workspace_size(4, 32, 8, 1, 20, 16, 2)
     assert ws >= 4 * 32 * 128 * 2 and L.omni_attn_paged_workspace_size(0, 32, 8, 1, 20, 16, 2) == 0
