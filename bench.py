@@ -18,7 +18,7 @@ C3's byte count (the device's achievable read rate, for comparison with
 `value`); the reference's CPU path (the oracle restatement) timed on a
 bounded C3 sample on this host.
 
-    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--only c3,c3paged,c2,c2pool,c4,c5,c5d32,calib,dense] [--no-cpu]
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--only c3,c3paged,c2,c2pool,c4,c5,c5paged,c5d32,calib,dense] [--no-cpu]
 Prints one JSON line on stdout; progress goes to stderr.
 """
 from __future__ import annotations
@@ -303,11 +303,11 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="C3 (and the CPU baseline) only")
     ap.add_argument("--only", default="",
-                    help="comma-separated sections to run (c3, c3paged, c2, c2pool, c4, c5, c5d32, calib, dense), for profiling one "
+                    help="comma-separated sections to run (c3, c3paged, c2, c2pool, c4, c5, c5paged, c5d32, calib, dense), for profiling one "
                          "configuration; the JSON line then carries only those sections")
     args = ap.parse_args()
     sections = set(args.only.split(",")) if args.only else (
-        {"c3"} if args.no_extras else {"c3", "c3paged", "c2", "c2pool", "c4", "c5", "c5d32", "calib", "dense"})
+        {"c3"} if args.no_extras else {"c3", "c3paged", "c2", "c2pool", "c4", "c5", "c5paged", "c5d32", "calib", "dense"})
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -547,6 +547,25 @@ def main() -> int:
                                 "frac_of_fp16_dense_peak": round(tf5 / 2500.0, 4),
                                 "note": "useful flops (QK, PV, QJL correction) over the causally visible keys"}
         log(f"[bench] C5: {t5 * 1e6:.0f} us -> {tf5:.1f} TFLOP/s ({tf5 / 2500:.1%} of fp16 dense MFMA peak)")
+        if "c5paged" in sections:
+            # the same chunk over the same tokens in 16-token pages (random
+            # pool order); the prefill kernel has a static tile order, so the
+            # paged call must equal the contiguous one bit for bit
+            from omnistack_rs.cache import PagedKVAttention, PagedKVCache
+            log("[bench] C5 paged: the same prefill over 16-token pages, random page order")
+            cache5, pt5, lens5 = PagedKVCache.from_contiguous(kn5, kq5, kr5, vn5, page_size=16,
+                                                              generator=torch.Generator().manual_seed(48))
+            att5p = PagedKVAttention(cache5, cb, n_heads=Hq, batch=B5, max_pages=pt5.shape[1], q_tokens=T5,
+                                     user_id=uid, causal=True)
+            eq5 = bool(torch.equal(att5p.run(q5, pt5, lens5), att5.run(q5)))
+            t5p = wall_eager(lambda: att5p.run(q5, pt5, lens5), max(3, args.steps // 10), 1)
+            tf5p = (fl_qkpv + fl_qjl) / t5p / 1e12
+            result["paged_c5"] = {"us_per_call": round(t5p * 1e6, 1), "TFLOP_s": round(tf5p, 2),
+                                  "frac_of_fp16_dense_peak": round(tf5p / 2500.0, 4), "equal_to_contiguous": eq5,
+                                  "note": "C5 through PagedKVAttention (16-token pages in random pool order, "
+                                          "causal chunk aligned to each sequence's end); timed like C5"}
+            log(f"[bench] C5 paged: {t5p * 1e6:.0f} us -> {tf5p:.1f} TFLOP/s; equal to the contiguous call: {eq5}")
+            del cache5, att5p
         del kn5, kq5, kr5, vn5, att5
 
     if "c5d32" in sections:

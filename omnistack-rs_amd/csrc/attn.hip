@@ -701,18 +701,28 @@ __device__ __forceinline__ void tile_load_paged(TileRaw &R, const DecBufs &P, co
 // outside the pool reads page 0 and, for a half that holds tokens of the
 // sequence (below `s_end`), sets `bad` (the sequence's rows come out NaN);
 // past the table's width (tiles past the end) the last entry is read.
-__device__ __forceinline__ void paged_half_rows(const AttnArgs &a, const int32_t *pt_row, int hk, int t, int s_end,
-                                                bool &bad, uint32_t (&rb)[2]) {
+__device__ __forceinline__ void paged_page_ids(const AttnArgs &a, const int32_t *pt_row, int t, int32_t (&id)[2]) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) id[u] = pt_row[imin((t + 16 * u) >> a.page_shift, (int)a.max_pages - 1)];
+}
+__device__ __forceinline__ void paged_rows(const AttnArgs &a, const int32_t (&id)[2], int hk, int t, int s_end,
+                                           bool &bad, uint32_t (&rb)[2]) {
     const int sh = a.page_shift;
     const uint32_t np = (uint32_t)a.n_pages;                  // < 2^26 (host check)
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const int th = t + 16 * u;
-        const uint32_t id = (uint32_t)pt_row[imin(th >> sh, (int)a.max_pages - 1)];
-        const bool ok = id < np;                                  // negative ids wrap past np
+        const bool ok = (uint32_t)id[u] < np;                     // negative ids wrap past np
         bad = bad || (!ok && th < s_end);
-        rb[u] = (((ok ? id : 0u) * (uint32_t)a.Hkv + (uint32_t)hk) << sh) + ((uint32_t)th & ((1u << sh) - 1u));
+        rb[u] = (((ok ? (uint32_t)id[u] : 0u) * (uint32_t)a.Hkv + (uint32_t)hk) << sh) +
+                ((uint32_t)th & ((1u << sh) - 1u));
     }
+}
+__device__ __forceinline__ void paged_half_rows(const AttnArgs &a, const int32_t *pt_row, int hk, int t, int s_end,
+                                                bool &bad, uint32_t (&rb)[2]) {
+    int32_t id[2];
+    paged_page_ids(a, pt_row, t, id);
+    paged_rows(a, id, hk, t, s_end, bad, rb);
 }
 
 __device__ __forceinline__ uint32_t cvt_pk_h2(float x, float y) {
@@ -1778,12 +1788,17 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
     OFS.v = 256u * g + 4u * n;
     bool page_bad = false;
     const int32_t *pt_row = PAGED ? a.page_table + b * a.max_pages : nullptr;
-    // one tile's loads (paged: from the pool rows of its two halves)
+    // one tile's loads (paged: from the pool rows of its two halves; tiles
+    // are loaded in order, so the next tile's page ids are requested here
+    // and waited for only at the next call)
+    int32_t pid[2] = {0, 0};
+    if constexpr (PAGED) paged_page_ids(a, pt_row, s_begin, pid);
     auto load_tile = [&](TileRaw &R, int t) {
         if constexpr (PAGED) {
             uint32_t rb[2];
-            paged_half_rows(a, pt_row, hk, t, s_end, page_bad, rb);
+            paged_rows(a, pid, hk, t, s_end, page_bad, rb);
             tile_load_paged<QJL>(R, P, OFS, rb);
+            paged_page_ids(a, pt_row, t + kDecTile, pid);
         } else {
             tile_load<QJL>(R, P, OFS, t);
         }
