@@ -47,7 +47,7 @@ class PagedKVCache:
         if n_pages < 1 or n_kv_heads < 1:
             raise ValueError("n_pages and n_kv_heads must be >= 1")
         if head_dim != HEAD_DIM:
-            raise ValueError(f"the paged decode path takes head_dim {HEAD_DIM}, got {head_dim}")
+            raise ValueError(f"the paged attention kernels take head_dim {HEAD_DIM}, got {head_dim}")
         self.n_pages, self.n_kv_heads, self.page_size, self.head_dim = n_pages, n_kv_heads, page_size, head_dim
         dev = torch.device(device)
         shape = (n_pages, n_kv_heads, page_size)
@@ -71,7 +71,17 @@ class PagedKVCache:
         return [self._free.pop() for _ in range(n)]
 
     def free(self, pages: Sequence[int]) -> None:
-        self._free.extend(int(p) for p in reversed(list(pages)))
+        """Return pages to the pool; a page that is already free or outside
+        the pool raises (it would otherwise be handed out twice)."""
+        pages = [int(p) for p in pages]
+        free = set(self._free)
+        for p in pages:
+            if not 0 <= p < self.n_pages:
+                raise IndexError(f"page {p} is outside the pool of {self.n_pages} pages")
+            if p in free:
+                raise ValueError(f"page {p} is already free")
+            free.add(p)
+        self._free.extend(reversed(pages))
 
     def write(self, pages: Sequence[int], k_nibbles: torch.Tensor, k_qjl: torch.Tensor, k_norms: torch.Tensor,
               v_nibbles: torch.Tensor, start: int = 0) -> None:
@@ -81,8 +91,14 @@ class PagedKVCache:
         if k_nibbles.dim() != 3 or k_nibbles.shape[0] != H:
             raise ValueError(f"k_nibbles must be ({H}, S, {self.head_dim // 2}), got {tuple(k_nibbles.shape)}")
         S = k_nibbles.shape[1]
+        if start < 0:
+            raise ValueError(f"start must be >= 0, got {start}")
         if self.pages_for(start + S) > len(pages):
             raise ValueError(f"{len(pages)} pages hold {len(pages) * ps} tokens, {start + S} needed")
+        # page ids are checked here: an index outside the pool inside the
+        # device-side copy below would be a device assertion, not an error
+        if any(not 0 <= int(p) < self.n_pages for p in pages):
+            raise IndexError(f"a page id lies outside the pool of {self.n_pages} pages")
         tok = torch.arange(start, start + S, device=self.device)
         pg = torch.as_tensor(list(pages), dtype=torch.int64, device=self.device)[tok // ps]
         slot = tok % ps

@@ -156,7 +156,7 @@ def test_paged_cache_host_side():
     """The page allocator and writer (plain torch, any device): every
     sequence read back through its page-table row equals the contiguous
     cache it came from, pages are handed out in the generator's order, and
-    bad page sizes are refused."""
+    bad page sizes, double frees and page ids outside the pool are refused."""
     from omnistack_rs.cache import PagedKVCache
     B, H, S, ps = 3, 2, 70, 16
     g = torch.Generator().manual_seed(3)
@@ -180,8 +180,16 @@ def test_paged_cache_host_side():
     assert len(pages) == 2 and len(cache._free) == free - 2 == 0
     cache.free(pages)
     assert len(cache._free) == free
+    with pytest.raises(ValueError):
+        cache.free(pages[:1])                      # already free
+    with pytest.raises(IndexError):
+        cache.free([cache.n_pages])
     with pytest.raises(RuntimeError):
         cache.allocate(1000)
+    with pytest.raises(IndexError):                # checked before any device copy
+        cache.write([0, cache.n_pages + 3], kn[0, :, :20], kq[0, :, :20], kr[0, :, :20], vn[0, :, :20])
+    with pytest.raises(ValueError):
+        cache.write([0, 1], kn[0, :, :20], kq[0, :, :20], kr[0, :, :20], vn[0, :, :20], start=-1)
     for bad in (8, 24, 2048):
         with pytest.raises(ValueError):
             PagedKVCache(4, 2, page_size=bad, device="cpu")
