@@ -99,6 +99,34 @@ size_t omni_encode_workspace_size(int64_t B, int H, int64_t T, int head_dim, int
                                   int per_head_codebook);
 
 /*
+ * The encoder with its code tables built once (serving loops that encode
+ * every step's new K and V against a fixed, baked codebook), and K and V of
+ * one step in a single launch.  The reference encodes each tensor with its
+ * own quantize_heads call (omnistack_rs/kernels/quantize.py:542-590; the
+ * bake, scripts/run_criteo_benchmark.py:355-367, calls it for K and for V);
+ * these entry points give the same codes, signs and norms.
+ *   omni_encode_tables_size: bytes of the tables, (per_head_codebook ? H : 1)
+ *     x 64 KB.
+ *   omni_encode_build_tables: writes them for 16-bit inputs (x_dtype bf16 or
+ *     f16) from `codebooks` (as omni_encode); they stay valid while the
+ *     codebooks and the dtype do.
+ *   omni_encode_pair: omni_encode of x0 and, when x1 is not NULL, of x1
+ *     (same dtype and shape, same G and codebooks) into their own outputs.
+ *     16-bit inputs at head_dim 128 with B * T >= 64 read the prebuilt
+ *     `tables` (OMNI_EWORKSPACE when missing or short) in one launch; other
+ *     inputs take the lane-per-row kernel (tables unused, may be NULL).
+ */
+size_t omni_encode_tables_size(int H, int per_head_codebook);
+int omni_encode_build_tables(const float *codebooks, int per_head_codebook, int H, int x_dtype,
+                             uint8_t *tables, size_t tables_bytes, void *stream);
+int omni_encode_pair(const void *x0, const void *x1, int x_dtype, int64_t B, int H, int64_t T,
+                     int head_dim, int rotate, const int8_t *sign_flip,
+                     const float *codebooks, int per_head_codebook, const uint32_t *g_bits,
+                     const uint8_t *tables, size_t tables_bytes,
+                     uint8_t *nibbles0, uint8_t *qjl0, float *norms0,
+                     uint8_t *nibbles1, uint8_t *qjl1, float *norms1, void *stream);
+
+/*
  * Dequantize packed rows to f32 (B, H, T, D):
  *   out = cb_h[code] + (b+- . G_h) * fp32(norm * fp32(sqrt(2/pi)/D))   (with_qjl)
  *   out = cb_h[code]                                                   (otherwise)

@@ -276,13 +276,13 @@ constexpr int kEncLdsBytes = kEncStageOff + kEncWaves * 128 * 4;
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
 struct EncArgs {
-    const void *x;
+    const void *x[2];            // one or two tensors of the same shape (blockIdx.z)
     const uint8_t *table;        // n_tables x 65536
     const float *codebooks;
     const uint32_t *g_bits;
     const int8_t *sign_flip;
-    uint8_t *nibbles, *qjl;
-    float *norms;
+    uint8_t *nibbles[2], *qjl[2];
+    float *norms[2];
     int64_t T, nrows_head, rows_per_block;
     int H, per_head, rotate;
     float scale;
@@ -411,6 +411,11 @@ __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n = lane & 15, g = lane >> 4;
     const int h = blockIdx.y;
+    // tensor blockIdx.z (K or V of one encode_pair call)
+    const void *const xz = a.x[blockIdx.z];
+    uint8_t *const nibz = a.nibbles[blockIdx.z];
+    uint8_t *const qjlz = a.qjl[blockIdx.z];
+    float *const nrmz = a.norms[blockIdx.z];
     const int64_t v_begin = (int64_t)blockIdx.x * a.rows_per_block;
     const int64_t v_end = v_begin + a.rows_per_block < a.nrows_head ? v_begin + a.rows_per_block : a.nrows_head;
 
@@ -460,7 +465,7 @@ __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
         return (bq * a.H + h) * a.T + t;
     };
     auto load_group = [&](uint4 (&w)[4], int64_t row) {
-        const uint4 *src = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(a.x) + row * 128);
+        const uint4 *src = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(xz) + row * 128);
 #pragma unroll
         for (int s = 0; s < 4; ++s) w[s] = src[4 * s + g];
     };
@@ -717,13 +722,13 @@ __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
 
         // stores: nibble dword s of lane (n, g) is bytes 16 s + 4 g .. + 3
         if (v0 + n < v_end) {
-            uint32_t *np = reinterpret_cast<uint32_t *>(a.nibbles + mrow * 64);
+            uint32_t *np = reinterpret_cast<uint32_t *>(nibz + mrow * 64);
 #pragma unroll
             for (int s = 0; s < 4; ++s) np[4 * s + g] = nib[s];
         }
         if (store) {
-            reinterpret_cast<uint2 *>(a.qjl + mrow * 8)[0] = make_uint2(slo, shi);
-            a.norms[mrow] = ss > 3.4028234663852886e38 ? INFINITY : (float)sqrt(ss);
+            reinterpret_cast<uint2 *>(qjlz + mrow * 8)[0] = make_uint2(slo, shi);
+            nrmz[mrow] = ss > 3.4028234663852886e38 ? INFINITY : (float)sqrt(ss);
         }
     };
 
@@ -846,6 +851,75 @@ extern "C" size_t omni_encode_workspace_size(int64_t B, int H, int64_t T, int he
     return (size_t)(per_head_codebook ? H : 1) * kEncTab;
 }
 
+// Value-to-code tables for 16-bit inputs: one 64 KB table per codebook.
+static void launch_code_tables(const float *codebooks, int per_head_codebook, int H, int x_dtype, uint8_t *tables,
+                               hipStream_t st) {
+    const int n_tab = per_head_codebook ? H : 1;
+    if (x_dtype == OMNI_BF16)
+        hipLaunchKernelGGL(code_table_kernel<OMNI_BF16>, dim3(kEncTab / 256, n_tab), dim3(256), 0, st, codebooks,
+                           per_head_codebook, tables);
+    else
+        hipLaunchKernelGGL(code_table_kernel<OMNI_F16>, dim3(kEncTab / 256, n_tab), dim3(256), 0, st, codebooks,
+                           per_head_codebook, tables);
+}
+
+// The wave kernel over nz (1 or 2) tensors of one shape, tables built.
+static int launch_encode128(const void *const xs[2], int nz, int x_dtype, int64_t B, int H, int64_t T, int rotate,
+                            const int8_t *sign_flip, const float *codebooks, int per_head_codebook,
+                            const uint32_t *g_bits, const uint8_t *tables, uint8_t *const nib[2],
+                            uint8_t *const qjl[2], float *const nrm[2], hipStream_t st) {
+    EncArgs a;
+    for (int z = 0; z < 2; ++z) {
+        const int zz = z < nz ? z : 0;
+        a.x[z] = xs[zz]; a.nibbles[z] = nib[zz]; a.qjl[z] = qjl[zz]; a.norms[z] = nrm[zz];
+    }
+    a.table = tables; a.codebooks = codebooks; a.g_bits = g_bits; a.sign_flip = sign_flip;
+    a.T = T; a.nrows_head = B * T; a.H = H; a.per_head = per_head_codebook; a.rotate = rotate;
+    a.scale = inv_sqrt_dim_f32(128);
+    // about one block per CU across the tensors and heads; each block a run
+    // of rows of one head of one tensor
+    int cus = 256;
+    {
+        int dev = 0;
+        hipDeviceProp_t p;
+        if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&p, dev) == hipSuccess && p.multiProcessorCount > 0)
+            cus = p.multiProcessorCount;
+    }
+    const int64_t per_head_blocks = (cus + (int64_t)H * nz - 1) / ((int64_t)H * nz);
+    const int64_t grp = 16 * kEncWaves;
+    int64_t rpb = (a.nrows_head + per_head_blocks - 1) / per_head_blocks;
+    rpb = (rpb + grp - 1) / grp * grp;
+    a.rows_per_block = rpb;
+    const int64_t nx = (a.nrows_head + rpb - 1) / rpb;
+    OMNI_CHECK_ARG(nx <= 2147483647LL, "omni_encode: grid too large");
+    const dim3 eg((unsigned)nx, (unsigned)H, (unsigned)nz), eb(64 * kEncWaves);
+    if (x_dtype == OMNI_BF16) {
+        if (rotate) hipLaunchKernelGGL((encode128_kernel<OMNI_BF16, true>), eg, eb, 0, st, a);
+        else hipLaunchKernelGGL((encode128_kernel<OMNI_BF16, false>), eg, eb, 0, st, a);
+    } else {
+        if (rotate) hipLaunchKernelGGL((encode128_kernel<OMNI_F16, true>), eg, eb, 0, st, a);
+        else hipLaunchKernelGGL((encode128_kernel<OMNI_F16, false>), eg, eb, 0, st, a);
+    }
+    OMNI_CHECK_LAUNCH("omni_encode");
+    return OMNI_OK;
+}
+
+// The lane-per-row kernel (f32 inputs, D = 32, few rows per head).
+static int launch_encode_rows(const void *x, int x_dtype, int64_t B, int H, int64_t T, int head_dim, int rotate,
+                              const int8_t *sign_flip, const float *codebooks, int per_head_codebook,
+                              const uint32_t *g_bits, uint8_t *nibbles, uint8_t *qjl, float *norms, hipStream_t st) {
+    const float s = inv_sqrt_dim_f32(head_dim);
+    dim3 grid((unsigned)((T + kRowsPerBlock - 1) / kRowsPerBlock), (unsigned)H, (unsigned)B);
+    if (head_dim == 128)
+        hipLaunchKernelGGL(encode_kernel<128>, grid, dim3(kRowsPerBlock), 0, st, x, x_dtype, T, H,
+                           rotate, sign_flip, codebooks, per_head_codebook, g_bits, nibbles, qjl, norms, s);
+    else
+        hipLaunchKernelGGL(encode_kernel<32>, grid, dim3(kRowsPerBlock), 0, st, x, x_dtype, T, H,
+                           rotate, sign_flip, codebooks, per_head_codebook, g_bits, nibbles, qjl, norms, s);
+    OMNI_CHECK_LAUNCH("omni_encode");
+    return OMNI_OK;
+}
+
 extern "C" int omni_encode(const void *x, int x_dtype, int64_t B, int H, int64_t T, int head_dim,
                            int rotate, const int8_t *sign_flip, const float *codebooks,
                            int per_head_codebook, const uint32_t *g_bits,
@@ -857,7 +931,6 @@ extern "C" int omni_encode(const void *x, int x_dtype, int64_t B, int H, int64_t
     if (B == 0 || H == 0 || T == 0) return OMNI_OK;
     OMNI_CHECK_ARG(x && codebooks && g_bits && nibbles && qjl && norms, "omni_encode: NULL pointer");
     OMNI_CHECK_ARG(B <= 65535 && H <= 65535, "omni_encode: B and H must be <= 65535");
-    const float s = inv_sqrt_dim_f32(head_dim);
     hipStream_t st = as_stream(stream);
     if (enc_fast(B, T, head_dim, x_dtype)) {
         const size_t need = omni_encode_workspace_size(B, H, T, head_dim, x_dtype, per_head_codebook);
@@ -866,53 +939,71 @@ extern "C" int omni_encode(const void *x, int x_dtype, int64_t B, int H, int64_t
             return OMNI_EWORKSPACE;
         }
         uint8_t *table = reinterpret_cast<uint8_t *>(workspace);
-        const int n_tab = per_head_codebook ? H : 1;
-        if (x_dtype == OMNI_BF16)
-            hipLaunchKernelGGL(code_table_kernel<OMNI_BF16>, dim3(kEncTab / 256, n_tab), dim3(256), 0, st, codebooks,
-                               per_head_codebook, table);
-        else
-            hipLaunchKernelGGL(code_table_kernel<OMNI_F16>, dim3(kEncTab / 256, n_tab), dim3(256), 0, st, codebooks,
-                               per_head_codebook, table);
+        launch_code_tables(codebooks, per_head_codebook, H, x_dtype, table, st);
         OMNI_CHECK_LAUNCH("omni_encode (code table)");
-        EncArgs a;
-        a.x = x; a.table = table; a.codebooks = codebooks; a.g_bits = g_bits;
-        a.sign_flip = sign_flip; a.nibbles = nibbles; a.qjl = qjl; a.norms = norms;
-        a.T = T; a.nrows_head = B * T; a.H = H; a.per_head = per_head_codebook; a.rotate = rotate; a.scale = s;
-        // about one block per CU across the heads; each block a run of rows of one head
-        int cus = 256;
-        {
-            int dev = 0;
-            hipDeviceProp_t p;
-            if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&p, dev) == hipSuccess && p.multiProcessorCount > 0)
-                cus = p.multiProcessorCount;
-        }
-        const int64_t per_head_blocks = (cus + H - 1) / H;
-        const int64_t grp = 16 * kEncWaves;
-        int64_t rpb = (a.nrows_head + per_head_blocks - 1) / per_head_blocks;
-        rpb = (rpb + grp - 1) / grp * grp;
-        a.rows_per_block = rpb;
-        const int64_t nx = (a.nrows_head + rpb - 1) / rpb;
-        OMNI_CHECK_ARG(nx <= 2147483647LL, "omni_encode: grid too large");
-        const dim3 eg((unsigned)nx, (unsigned)H), eb(64 * kEncWaves);
-        if (x_dtype == OMNI_BF16) {
-            if (rotate) hipLaunchKernelGGL((encode128_kernel<OMNI_BF16, true>), eg, eb, 0, st, a);
-            else hipLaunchKernelGGL((encode128_kernel<OMNI_BF16, false>), eg, eb, 0, st, a);
-        } else {
-            if (rotate) hipLaunchKernelGGL((encode128_kernel<OMNI_F16, true>), eg, eb, 0, st, a);
-            else hipLaunchKernelGGL((encode128_kernel<OMNI_F16, false>), eg, eb, 0, st, a);
-        }
-        OMNI_CHECK_LAUNCH("omni_encode");
-        return OMNI_OK;
+        const void *xs[2] = {x, x};
+        uint8_t *nib[2] = {nibbles, nibbles}, *qj[2] = {qjl, qjl};
+        float *nr[2] = {norms, norms};
+        return launch_encode128(xs, 1, x_dtype, B, H, T, rotate, sign_flip, codebooks, per_head_codebook, g_bits,
+                                table, nib, qj, nr, st);
     }
-    dim3 grid((unsigned)((T + kRowsPerBlock - 1) / kRowsPerBlock), (unsigned)H, (unsigned)B);
-    if (head_dim == 128)
-        hipLaunchKernelGGL(encode_kernel<128>, grid, dim3(kRowsPerBlock), 0, st, x, x_dtype, T, H,
-                           rotate, sign_flip, codebooks, per_head_codebook, g_bits, nibbles, qjl, norms, s);
-    else
-        hipLaunchKernelGGL(encode_kernel<32>, grid, dim3(kRowsPerBlock), 0, st, x, x_dtype, T, H,
-                           rotate, sign_flip, codebooks, per_head_codebook, g_bits, nibbles, qjl, norms, s);
-    OMNI_CHECK_LAUNCH("omni_encode");
+    return launch_encode_rows(x, x_dtype, B, H, T, head_dim, rotate, sign_flip, codebooks, per_head_codebook, g_bits,
+                              nibbles, qjl, norms, st);
+}
+
+extern "C" size_t omni_encode_tables_size(int H, int per_head_codebook) {
+    if (H <= 0) return 0;
+    return (size_t)(per_head_codebook ? H : 1) * kEncTab;
+}
+
+extern "C" int omni_encode_build_tables(const float *codebooks, int per_head_codebook, int H, int x_dtype,
+                                        uint8_t *tables, size_t tables_bytes, void *stream) {
+    OMNI_CHECK_ARG(x_dtype == OMNI_BF16 || x_dtype == OMNI_F16,
+                   "omni_encode_build_tables: tables serve 16-bit inputs (dtype %d)", x_dtype);
+    OMNI_CHECK_ARG(H > 0 && H <= 65535, "omni_encode_build_tables: need 1 <= H <= 65535");
+    OMNI_CHECK_ARG(codebooks && tables, "omni_encode_build_tables: NULL pointer");
+    const size_t need = omni_encode_tables_size(H, per_head_codebook);
+    if (tables_bytes < need) {
+        set_error("omni_encode_build_tables: %zu bytes of tables required, %zu given", need, tables_bytes);
+        return OMNI_EWORKSPACE;
+    }
+    launch_code_tables(codebooks, per_head_codebook, H, x_dtype, tables, as_stream(stream));
+    OMNI_CHECK_LAUNCH("omni_encode_build_tables");
     return OMNI_OK;
+}
+
+extern "C" int omni_encode_pair(const void *x0, const void *x1, int x_dtype, int64_t B, int H, int64_t T,
+                                int head_dim, int rotate, const int8_t *sign_flip, const float *codebooks,
+                                int per_head_codebook, const uint32_t *g_bits, const uint8_t *tables,
+                                size_t tables_bytes, uint8_t *nibbles0, uint8_t *qjl0, float *norms0,
+                                uint8_t *nibbles1, uint8_t *qjl1, float *norms1, void *stream) {
+    OMNI_CHECK_ARG(dtype_ok(x_dtype), "omni_encode_pair: bad dtype %d", x_dtype);
+    OMNI_CHECK_ARG(head_dim_ok(head_dim), "omni_encode_pair: head_dim must be 128 or 32, got %d", head_dim);
+    OMNI_CHECK_ARG(B >= 0 && H >= 0 && T >= 0, "omni_encode_pair: negative shape");
+    if (B == 0 || H == 0 || T == 0) return OMNI_OK;
+    const int nz = x1 ? 2 : 1;
+    OMNI_CHECK_ARG(x0 && codebooks && g_bits && nibbles0 && qjl0 && norms0, "omni_encode_pair: NULL pointer");
+    OMNI_CHECK_ARG(nz == 1 || (nibbles1 && qjl1 && norms1), "omni_encode_pair: NULL output for the second tensor");
+    OMNI_CHECK_ARG(B <= 65535 && H <= 65535, "omni_encode_pair: B and H must be <= 65535");
+    hipStream_t st = as_stream(stream);
+    if (enc_fast(B, T, head_dim, x_dtype)) {
+        const size_t need = omni_encode_tables_size(H, per_head_codebook);
+        if (tables == nullptr || tables_bytes < need) {
+            set_error("omni_encode_pair: %zu bytes of code tables required, %zu given", need, tables_bytes);
+            return OMNI_EWORKSPACE;
+        }
+        const void *xs[2] = {x0, x1 ? x1 : x0};
+        uint8_t *nib[2] = {nibbles0, nz > 1 ? nibbles1 : nibbles0}, *qj[2] = {qjl0, nz > 1 ? qjl1 : qjl0};
+        float *nr[2] = {norms0, nz > 1 ? norms1 : norms0};
+        return launch_encode128(xs, nz, x_dtype, B, H, T, rotate, sign_flip, codebooks, per_head_codebook, g_bits,
+                                tables, nib, qj, nr, st);
+    }
+    int rc = launch_encode_rows(x0, x_dtype, B, H, T, head_dim, rotate, sign_flip, codebooks, per_head_codebook,
+                                g_bits, nibbles0, qjl0, norms0, st);
+    if (rc == OMNI_OK && nz > 1)
+        rc = launch_encode_rows(x1, x_dtype, B, H, T, head_dim, rotate, sign_flip, codebooks, per_head_codebook,
+                                g_bits, nibbles1, qjl1, norms1, st);
+    return rc;
 }
 
 extern "C" int omni_dequantize(const uint8_t *nibbles, const uint8_t *qjl, const float *norms,

@@ -31,6 +31,10 @@ SIGNATURES = {
     "omni_encode": (_c_int, [_vp, _c_int, _c_i64, _c_int, _c_i64, _c_int, _c_int, _vp, _vp, _c_int,
                              _vp, _vp, _vp, _vp, _vp, _c_sz, _vp]),
     "omni_encode_workspace_size": (_c_sz, [_c_i64, _c_int, _c_i64, _c_int, _c_int, _c_int]),
+    "omni_encode_tables_size": (_c_sz, [_c_int, _c_int]),
+    "omni_encode_build_tables": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _c_sz, _vp]),
+    "omni_encode_pair": (_c_int, [_vp, _vp, _c_int, _c_i64, _c_int, _c_i64, _c_int, _c_int, _vp, _vp, _c_int,
+                                  _vp, _vp, _c_sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "omni_dequantize": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _vp, _c_i64, _c_int, _c_i64, _c_int,
                                  _c_int, _vp, _vp]),
     "omni_lora_apply": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _c_int, _vp, _c_i64, _c_int, _c_i64,

@@ -148,6 +148,85 @@ def encode_kv(x: torch.Tensor, codebooks: torch.Tensor, user_id: int = 0,
     return _encode(x, codebooks, user_id, rotate=True, sign_flip=sign_flip)
 
 
+class PackedKVEncoder:
+    """Prepared encoder for a fixed codebook: the bake and serving loops that
+    encode every step's new K and V with the same (baked) codebooks.
+
+    Converts the codebooks, uploads G (seeds (user_id % 1024) ^ h) and, for
+    16-bit inputs, builds the 64 KB value-to-code tables once;
+    ``encode(k, v=None, out=None)`` then encodes K, and V when given, in one
+    launch (``omni_encode_pair``), writing into ``out`` when given (no
+    allocation).  Each tensor gets exactly what ``encode_kv`` (``rotate``) or
+    ``quantize_heads`` (not ``rotate``) returns for it (quantize.py:542-590).
+    """
+
+    def __init__(self, codebooks: torch.Tensor, n_kv_heads: int, user_id: int = 0, rotate: bool = True,
+                 sign_flip: Optional[torch.Tensor] = None, dtype: torch.dtype = torch.bfloat16,
+                 head_dim: int = HEAD_DIM, device=None):
+        if head_dim not in (128, 32):
+            raise ValueError(f"head_dim must be {HEAD_DIM} (or 32), got {head_dim}")
+        if dtype not in _lib.DTYPE_CODE:
+            raise ValueError(f"dtype must be one of {list(_lib.DTYPE_CODE)}")
+        dev = torch.device(device) if device is not None else codebooks.device
+        if dev.type != "cuda":
+            raise RuntimeError("PackedKVEncoder runs on HIP devices only; pass codebooks or device= on 'cuda' (ROCm)")
+        H = int(n_kv_heads)
+        self.H, self.D, self.dtype, self.device = H, int(head_dim), dtype, dev
+        self.code = _lib.dtype_code(dtype)
+        self.rotate = int(rotate)
+        self.cb, self.per_head = _prep_codebooks(codebooks, H, dev)
+        self.gb = _lib.g_bits(_lib.head_seeds(user_id, H), self.D, dev)
+        self.sf = _lib.sign_flip_i8(sign_flip, self.D, dev) if (rotate and sign_flip is not None) else None
+        L = _lib.lib()
+        self.tables, self.tables_bytes = None, 0
+        if dtype in (torch.bfloat16, torch.float16) and self.D == 128:
+            self.tables_bytes = L.omni_encode_tables_size(H, self.per_head)
+            self.tables = torch.empty(self.tables_bytes, dtype=torch.uint8, device=dev)
+            _lib.check(L.omni_encode_build_tables(_lib.ptr(self.cb), self.per_head, H, self.code,
+                                                  _lib.ptr(self.tables), self.tables_bytes, _lib.stream_of(dev)))
+
+    def empty_outputs(self, B: int, T: int):
+        """(nibbles, qjl, norms) buffers for a (B, H, T, D) input."""
+        H, D, dev = self.H, self.D, self.device
+        return (torch.empty(B, H, T, D // 2, dtype=torch.uint8, device=dev),
+                torch.empty(B, H, T, D // 16, dtype=torch.uint8, device=dev),
+                torch.empty(B, H, T, dtype=torch.float32, device=dev))
+
+    def encode(self, k: torch.Tensor, v: Optional[torch.Tensor] = None, out=None):
+        """Packed (nibbles, qjl, norms) of k, or a pair of them for (k, v).
+        ``out``: the same structure of preallocated buffers to write into."""
+        if k.dim() != 4 or k.shape[1] != self.H or k.shape[3] != self.D or k.dtype != self.dtype:
+            raise ValueError(f"k must be {self.dtype} (B, {self.H}, T, {self.D}), got {k.dtype} {tuple(k.shape)}")
+        if v is not None and (v.shape != k.shape or v.dtype != k.dtype):
+            raise ValueError(f"v must match k: {k.dtype} {tuple(k.shape)}, got {v.dtype} {tuple(v.shape)}")
+        _lib.require_device(k, v)
+        for t in (k, v):
+            if t is not None and t.device != self.device:
+                raise ValueError(f"inputs must be on {self.device}")
+        B, _, T, _ = k.shape
+        n = 1 if v is None else 2
+        if out is None:
+            outs = [self.empty_outputs(B, T) for _ in range(n)]
+        else:
+            outs = [out] if n == 1 else list(out)
+            for o in outs:
+                want = [(B, self.H, T, self.D // 2), (B, self.H, T, self.D // 16), (B, self.H, T)]
+                dts = [torch.uint8, torch.uint8, torch.float32]
+                if len(o) != 3 or any(tuple(t.shape) != w or t.dtype != d or not t.is_contiguous() or
+                                      t.device != self.device for t, w, d in zip(o, want, dts)):
+                    raise ValueError("out must hold contiguous (nibbles u8, qjl u8, norms f32) buffers "
+                                     f"of shapes {want} on {self.device}")
+        kc = k.contiguous()
+        vc = v.contiguous() if v is not None else None
+        o1 = outs[1] if n == 2 else (None, None, None)
+        _lib.check(_lib.lib().omni_encode_pair(
+            _lib.ptr(kc), _lib.ptr(vc), self.code, B, self.H, T, self.D, self.rotate, _lib.ptr(self.sf),
+            _lib.ptr(self.cb), self.per_head, _lib.ptr(self.gb), _lib.ptr(self.tables), self.tables_bytes,
+            _lib.ptr(outs[0][0]), _lib.ptr(outs[0][1]), _lib.ptr(outs[0][2]),
+            _lib.ptr(o1[0]), _lib.ptr(o1[1]), _lib.ptr(o1[2]), _lib.stream_of(self.device)))
+        return tuple(outs[0]) if n == 1 else (tuple(outs[0]), tuple(outs[1]))
+
+
 def dequantize_heads(nibbles: torch.Tensor, qjl_packed: torch.Tensor, norms: torch.Tensor,
                      codebooks: torch.Tensor, user_id: int = 0, with_qjl: bool = True) -> torch.Tensor:
     """(B, n_heads, T, 128) float32 reconstruction (quantize.py:593-640)."""

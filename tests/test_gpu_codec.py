@@ -129,6 +129,56 @@ def test_encode_c4_full_size(device):
           flush=True)
 
 
+@pytest.mark.parametrize("B,T,dtype,D", [(2, 200, torch.bfloat16, 128), (3, 70, torch.float16, 128),
+                                          (1, 20, torch.bfloat16, 128), (2, 33, torch.float32, 128),
+                                          (2, 40, torch.float32, 32)])
+def test_prepared_encoder_pair_equals_encode_kv(device, B, T, dtype, D):
+    """PackedKVEncoder: K and V in one launch with code tables built once give
+    exactly what two encode_kv calls give (the wave kernel for 16-bit inputs
+    at D = 128 and B * T >= 64, the lane-per-row kernel otherwise), and
+    writing into preallocated outputs changes nothing; rotate=False equals
+    quantize_heads."""
+    from omnistack_rs.kernels.quantize import PackedKVEncoder, encode_kv, quantize_heads
+    H = 4
+    k = _data.kv((B, H, T, D), seed=61, dtype=dtype)
+    v = _data.kv((B, H, T, D), seed=62, dtype=dtype)
+    s = _data.sign_flip(D)
+    cb = (_data.gaussian_codebook(H) * torch.linspace(0.9, 1.2, H).reshape(H, 1)).to(device)
+    enc = PackedKVEncoder(cb, H, user_id=42, sign_flip=s.to(device), dtype=dtype, head_dim=D)
+    kd, vd = k.to(device), v.to(device)
+    got_k, got_v = enc.encode(kd, vd)
+    for got, x in ((got_k, kd), (got_v, vd)):
+        want = encode_kv(x, cb, user_id=42, sign_flip=s.to(device))
+        for g, w in zip(got, want):
+            assert torch.equal(g, w)
+    outs = (enc.empty_outputs(B, T), enc.empty_outputs(B, T))
+    again = enc.encode(kd, vd, out=outs)
+    assert all(torch.equal(g, w) for pair in zip(again, (got_k, got_v)) for g, w in zip(*pair))
+    assert again[0][0].data_ptr() == outs[0][0].data_ptr()
+    single = enc.encode(kd)
+    assert all(torch.equal(g, w) for g, w in zip(single, got_k))
+    plain = PackedKVEncoder(cb, H, user_id=7, rotate=False, dtype=dtype, head_dim=D)
+    for g, w in zip(plain.encode(kd), quantize_heads(kd, cb, user_id=7)):
+        assert torch.equal(g, w)
+
+
+def test_prepared_encoder_c4_pair(device):
+    """The C4 config (16 x 8 x 4096 K and V) through one encode_pair launch:
+    K and V each bit-equal to encode_kv (which the C4 parity test checks
+    against the oracle)."""
+    from omnistack_rs.kernels.quantize import PackedKVEncoder, encode_kv
+    print("[encode] C4 pair 16 x 8 x 4096", flush=True)
+    k = _data.kv((16, 8, 4096, 128), seed=46).to(device)
+    v = _data.kv((16, 8, 4096, 128), seed=47).to(device)
+    s = _data.sign_flip().to(device)
+    cb = (_data.gaussian_codebook(8) * torch.linspace(0.9, 1.2, 8).reshape(8, 1)).to(device)
+    enc = PackedKVEncoder(cb, 8, user_id=42, sign_flip=s)
+    got = enc.encode(k, v)
+    for pair, x in zip(got, (k, v)):
+        want = encode_kv(x, cb, user_id=42, sign_flip=s)
+        assert all(torch.equal(g, w) for g, w in zip(pair, want))
+
+
 def test_encode_head_dim_32(device):
     from omnistack_rs.kernels.quantize import quantize_heads
     x = restate.wht(torch.randn(2, 3, 50, 32, generator=_data.gen(11)))

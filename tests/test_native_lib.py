@@ -195,6 +195,33 @@ def test_paged_cache_host_side():
             PagedKVCache(4, 2, page_size=bad, device="cpu")
 
 
+def test_encode_pair_host_checks(L):
+    """omni_encode_pair / omni_encode_build_tables argument checks (no launch)."""
+    from omnistack_rs import _lib
+    assert L.omni_encode_tables_size(8, 1) == 8 * 65536 and L.omni_encode_tables_size(8, 0) == 65536
+    assert L.omni_encode_tables_size(0, 1) == 0
+    rc = L.omni_encode_build_tables(1, 1, 8, 0, 1, 1 << 20, None)        # f32 input: no tables
+    assert rc == _lib.OMNI_EINVAL and "16-bit" in _lib.last_error()
+    rc = L.omni_encode_build_tables(1, 1, 8, 2, 1, 1000, None)
+    assert rc == _lib.OMNI_EWORKSPACE
+    tail = (1, 1, 1, None, None, None, None)
+    # a second tensor without outputs
+    rc = L.omni_encode_pair(1, 1, 2, 2, 4, 100, 128, 1, None, 1, 1, 1, 1, 1 << 20, 1, 1, 1, None, None, None, None)
+    assert rc == _lib.OMNI_EINVAL and "second tensor" in _lib.last_error()
+    # 16-bit, D = 128, B * T >= 64: prebuilt tables required
+    rc = L.omni_encode_pair(1, None, 2, 2, 4, 100, 128, 1, None, 1, 1, 1, None, 0, *tail)
+    assert rc == _lib.OMNI_EWORKSPACE and "code tables" in _lib.last_error()
+    assert L.omni_encode_pair(None, None, 2, 0, 4, 100, 128, 1, None, None, 1, None, None, 0, *tail) == 0
+
+
+def test_prepared_encoder_refuses_cpu():
+    from omnistack_rs.kernels.quantize import PackedKVEncoder
+    with pytest.raises(RuntimeError):
+        PackedKVEncoder(torch.zeros(4, 16), 4)
+    with pytest.raises(ValueError):
+        PackedKVEncoder(torch.zeros(4, 16), 4, head_dim=64)
+
+
 def test_lloyd_max_host_checks(L):
     from omnistack_rs import _lib
     assert L.omni_lloyd_max_workspace_size(0, 1, 100) == 0
