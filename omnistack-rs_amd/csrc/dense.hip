@@ -204,54 +204,83 @@ __global__ __launch_bounds__(64 * kDnWaves) void dense_attn_kernel(DenseArgs a) 
 }
 
 // Few query rows per (batch, kv head) (decode: T * G <= 16): the NW waves
-// share one group of 16 rows and split every 16 NW-key tile (wave w takes
-// keys 16 w .. 16 w + 15), each keeping its own online-softmax state; the
-// states are merged in LDS at the end (max, then the exp-weighted sums in
-// wave order).
+// share one group of 16 rows and split the keys in 16-key chunks (wave w
+// takes chunks w, w + NW, ...), each keeping its own online-softmax state;
+// the states are merged in LDS at the end (max, then the exp-weighted sums in
+// wave order).  K and V go from HBM straight into MFMA operand registers (no
+// LDS staging, no block barrier per tile), two chunks in flight per wave.
+// Scores: step s's k axis is dims 4 s .. 4 s + 3 (lane group g: dim 4 s + g,
+// the summation order of the LDS-staged kernel this replaced); lane (n, g)
+// loads 16-byte pieces 16 t + 4 g .. of key n and a 4 x 4 transpose across
+// its four lane groups (two permlane swap stages) hands each lane its dims.
+// P V: lane (n, g) holds dims (D/16) n .. + D/16 - 1 of keys 4 s + g, so
+// output column n of MFMA j is dim (D/16) n + j.
 #ifndef OMNI_DN_KS_WAVES
 #define OMNI_DN_KS_WAVES 8
 #endif
 constexpr int kDnKsWaves = OMNI_DN_KS_WAVES;
 
+template <int D>
+struct DnChunk {
+    float k[D / 4];       // key 16 c + n: k[s] = dim 4 s + g (after the transpose)
+    float v[D / 4];       // keys 16 c + 4 s + g (s = 0..3), dims (D/16) n ..: v[s * D/16 + j]
+};
+
+// 4 x 4 transpose across the four 16-lane rows: on entry row r of x[c]
+// holds M[r][c], on exit M[c][r].
+__device__ __forceinline__ void dn_transpose4(float (&x)[4]) {
+    auto swap32 = [](float &a, float &b) {
+        const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+        a = __uint_as_float(t[0]);
+        b = __uint_as_float(t[1]);
+    };
+    auto swap16 = [](float &a, float &b) {
+        const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+        a = __uint_as_float(t[0]);
+        b = __uint_as_float(t[1]);
+    };
+    swap32(x[0], x[2]);
+    swap32(x[1], x[3]);
+    swap16(x[0], x[1]);
+    swap16(x[2], x[3]);
+}
+
 template <int D, int NW>
 __global__ __launch_bounds__(64 * NW) void dense_attn_ks_kernel(DenseArgs a) {
-    constexpr int kDnKsKeys = 16 * NW;
-    constexpr int DP = D + 4;
-    constexpr int kTileF = kDnKsKeys * DP;
-    __shared__ __attribute__((aligned(16))) float ks[kTileF];
-    __shared__ __attribute__((aligned(16))) float vs[kTileF];
+    constexpr int DQ = D / 4, DV = D / 16, DP = D + 4;
+    static_assert(DQ % 4 == 0 && (DV % 4 == 0 || DV == 2), "16- or 8-byte operand loads");
     __shared__ float ps[NW][16 * 20];
     __shared__ float wst[NW][16][4];             // per wave and row: m, l, seen0, nan
-    static_assert(NW * 16 * DP <= kTileF, "wave partials fit the key tile buffer");
+    __shared__ __attribute__((aligned(16))) float op[NW * 16 * DP];   // per wave and row: O
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, g = lane >> 4;
     const int hk = blockIdx.y;
     const int64_t b = blockIdx.z;
-    const int64_t row0 = (int64_t)blockIdx.x * 16;
 
-    float qa[D / 4];
+    float qa[DQ];                                 // qa[s] = dim 4 s + g of query row n
     {
-        const int64_t r = row0 + n;
+        const int64_t r = n;
         const bool ok = r < a.rows;
         const int64_t t = ok ? r / a.G : 0;
         const int hq = hk * a.G + (ok ? (int)(r % a.G) : 0);
         const float *qrow = a.q + ((b * a.Hq + hq) * a.T + t) * D;
 #pragma unroll
-        for (int s = 0; s < D / 4; ++s) qa[s] = ok ? qrow[4 * s + g] : 0.0f;
+        for (int s = 0; s < DQ; ++s) qa[s] = ok ? qrow[4 * s + g] : 0.0f;
     }
+    // mask offset of row 4 g + i (key 0); rows past the last add nothing
     bool rok[4];
-    int64_t rt[4];
-    int rh[4];
+    int64_t mrow[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int64_t r = row0 + 4 * g + i;
+        const int r = 4 * g + i;
         rok[i] = r < a.rows;
-        rt[i] = rok[i] ? r / a.G : 0;
-        rh[i] = hk * a.G + (rok[i] ? (int)(r % a.G) : 0);
+        const int t = rok[i] ? r / a.G : 0;
+        const int hq = hk * a.G + (rok[i] ? r % a.G : 0);
+        mrow[i] = b * a.ms_b + hq * a.ms_h + t * a.ms_t;
     }
-    f32x4_t o[D / 16];
+    f32x4_t o[DV];
 #pragma unroll
-    for (int j = 0; j < D / 16; ++j) o[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < DV; ++j) o[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     float m[4], l[4];
     bool seen0[4], nan_row[4];
 #pragma unroll
@@ -263,43 +292,60 @@ __global__ __launch_bounds__(64 * NW) void dense_attn_ks_kernel(DenseArgs a) {
     }
     const float *kb0 = a.k + ((int64_t)b * a.Hkv + hk) * a.S * D;
     const float *vb0 = a.v + ((int64_t)b * a.Hkv + hk) * a.S * D;
-    constexpr int kPer = kDnKsKeys * D / (4 * 64 * NW);
-    float4 nk[kPer], nv[kPer];
-    auto fetch = [&](int64_t s0) {
+    const int S = (int)a.S;                                 // < 2^27 (host check)
+    const int nch = (S + 15) / 16;
+    // chunk c's operands; keys past S read the last key (a valid address)
+    // and their V is zeroed (their P is 0, and 0 * inf would be NaN)
+    auto load = [&](DnChunk<D> &R, int c) {
+        const int key = 16 * c + n, kk = key < S ? key : S - 1;
+        // piece t: dims 16 t + 4 g .. + 3 of key n (transposed at use)
+        const float4 *kp = reinterpret_cast<const float4 *>(kb0 + (int64_t)kk * D + 4 * g);
 #pragma unroll
-        for (int c = 0; c < kPer; ++c) {
-            const int e = 4 * (tid + c * 64 * NW);
-            const int key = e / D, d = e - key * D;
-            nk[c] = nv[c] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (s0 + key < a.S) {
-                nk[c] = *reinterpret_cast<const float4 *>(kb0 + (s0 + key) * D + d);
-                nv[c] = *reinterpret_cast<const float4 *>(vb0 + (s0 + key) * D + d);
+        for (int t = 0; t < DQ / 4; ++t) {
+            const float4 w = kp[4 * t];
+            R.k[4 * t] = w.x; R.k[4 * t + 1] = w.y; R.k[4 * t + 2] = w.z; R.k[4 * t + 3] = w.w;
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int vk = 16 * c + 4 * s + g, vv = vk < S ? vk : S - 1;
+            const bool z = vk >= S;
+            if constexpr (DV == 2) {
+                const float2 w = *reinterpret_cast<const float2 *>(vb0 + (int64_t)vv * D + DV * n);
+                R.v[s * DV] = z ? 0.0f : w.x;
+                R.v[s * DV + 1] = z ? 0.0f : w.y;
+            } else {
+                const float4 *vp = reinterpret_cast<const float4 *>(vb0 + (int64_t)vv * D + DV * n);
+#pragma unroll
+                for (int h = 0; h < DV / 4; ++h) {
+                    const float4 w = vp[h];
+                    R.v[s * DV + 4 * h] = z ? 0.0f : w.x;
+                    R.v[s * DV + 4 * h + 1] = z ? 0.0f : w.y;
+                    R.v[s * DV + 4 * h + 2] = z ? 0.0f : w.z;
+                    R.v[s * DV + 4 * h + 3] = z ? 0.0f : w.w;
+                }
             }
         }
     };
-    fetch(0);
-    for (int64_t s0 = 0; s0 < a.S; s0 += kDnKsKeys) {
-        __syncthreads();
+    auto step = [&](const DnChunk<D> &R, int c) {
+        // all pieces transposed first: the swaps do not wait on the MFMA chain
+        float kx[DQ / 4][4];
 #pragma unroll
-        for (int c = 0; c < kPer; ++c) {
-            const int e = 4 * (tid + c * 64 * NW);
-            const int key = e / D, d = e - key * D;
-            *reinterpret_cast<float4 *>(ks + key * DP + d) = nk[c];
-            *reinterpret_cast<float4 *>(vs + key * DP + d) = nv[c];
+        for (int t = 0; t < DQ / 4; ++t) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) kx[t][u] = R.k[4 * t + u];
+            dn_transpose4(kx[t]);                     // kx[t][u] = dim 16 t + 4 u + g
         }
-        __syncthreads();
-        if (s0 + kDnKsKeys < a.S) fetch(s0 + kDnKsKeys);
-        const int kbase = 16 * wave;                 // this wave's keys in the tile
         f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < D / 4; ++s)
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[s], ks[(kbase + n) * DP + 4 * s + g], acc, 0, 0, 0);
-        const int64_t key = s0 + kbase + n;
+        for (int t = 0; t < DQ / 4; ++t)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[4 * t + u], kx[t][u], acc, 0, 0, 0);
+        const int key = 16 * c + n;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             float v = acc[i] * a.scale;
-            if (key < a.S) {
-                if (a.mask != nullptr && rok[i]) v += a.mask[b * a.ms_b + rh[i] * a.ms_h + rt[i] * a.ms_t + key * a.ms_s];
+            if (key < S) {
+                if (a.mask != nullptr && rok[i]) v += a.mask[mrow[i] + key * a.ms_s];
             } else {
                 v = -INFINITY;
             }
@@ -311,7 +357,7 @@ __global__ __launch_bounds__(64 * NW) void dense_attn_ks_kernel(DenseArgs a) {
             const float p = (m_new == -INFINITY) ? 0.0f : expf(v - m_new);
             l[i] = alpha * l[i] + dn_sum16(p);
 #pragma unroll
-            for (int j = 0; j < D / 16; ++j) o[j][i] *= alpha;
+            for (int j = 0; j < DV; ++j) o[j][i] *= alpha;
             m[i] = m_new;
             ps[wave][(4 * g + i) * 20 + n] = p;
         }
@@ -321,20 +367,35 @@ __global__ __launch_bounds__(64 * NW) void dense_attn_ks_kernel(DenseArgs a) {
         float pa[4];
 #pragma unroll
         for (int s = 0; s < 4; ++s) pa[s] = ps[wave][n * 20 + 4 * s + g];
+        // the next chunk's P writes must not pass these reads
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-        for (int j = 0; j < D / 16; ++j)
+        for (int j = 0; j < DV; ++j)
 #pragma unroll
-            for (int s = 0; s < 4; ++s)
-                o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[s], vs[(kbase + 4 * s + g) * DP + 16 * j + n], o[j], 0, 0, 0);
+            for (int s = 0; s < 4; ++s) o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[s], R.v[s * DV + j], o[j], 0, 0, 0);
+    };
+    if (wave < nch) {
+        // two chunks in flight: loads past the last chunk read valid
+        // addresses and are never consumed
+        DnChunk<D> r0, r1;
+        load(r0, wave);
+        for (int c = wave;; c += 2 * NW) {
+            load(r1, c + NW);
+            step(r0, c);
+            if (c + NW >= nch) break;
+            load(r0, c + 2 * NW);
+            step(r1, c + NW);
+            if (c + 2 * NW >= nch) break;
+        }
     }
 
-    // merge the four waves' states
-    __syncthreads();                                  // tiles are dead: reuse them for the partials
-    float *op = ks;                                   // [wave][row][DP]
+    // merge the waves' states
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
-        for (int j = 0; j < D / 16; ++j) op[(wave * 16 + 4 * g + i) * DP + 16 * j + n] = o[j][i];
+        for (int j = 0; j < DV; ++j) op[(wave * 16 + 4 * g + i) * DP + DV * n + j] = o[j][i];
         if (n == 0) {
             wst[wave][4 * g + i][0] = m[i];
             wst[wave][4 * g + i][1] = l[i];
@@ -345,7 +406,7 @@ __global__ __launch_bounds__(64 * NW) void dense_attn_ks_kernel(DenseArgs a) {
     __syncthreads();
     for (int e = tid; e < 16 * D; e += 64 * NW) {
         const int r = e / D, d = e - r * D;
-        const int64_t row = row0 + r;
+        const int64_t row = r;
         if (row >= a.rows) continue;
         float mx = -INFINITY;
         bool s0seen = false, isnan_row = false;
@@ -399,7 +460,7 @@ extern "C" int omni_dense_attn(const float *q, const float *k, const float *v, c
     a.scale = scale;
     if (S == 0) a.first_tile = 0;   // no keys: every row is NaN (0 / 0), as the reference
     hipStream_t st = as_stream(stream);
-    if (rows <= 16 && head_dim <= 128) {
+    if (rows <= 16 && head_dim <= 128 && S < (int64_t(1) << 27)) {
         // few rows: the waves split the keys instead of the rows
         const dim3 grid(1u, (unsigned)Hkv, (unsigned)B), block(64 * kDnKsWaves);
         if (head_dim == 32) hipLaunchKernelGGL((dense_attn_ks_kernel<32, kDnKsWaves>), grid, block, 0, st, a);
