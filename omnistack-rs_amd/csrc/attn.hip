@@ -546,6 +546,15 @@ constexpr int kDecCscOff = kDecGaOff + kDecRows * 16 * 2 * 16;      // per row: 
 __device__ __forceinline__ int dec_chunk(int row, int c) { return c ^ (2 * (row & 7)); }
 constexpr int kDecCntOff = kDecCscOff + kDecRows * 4;                // next unclaimed tile of the block
 constexpr int kDecLdsBytes = kDecCntOff + 16;
+// Paged cache: the pool row of each page of the split (page p of the split
+// at kDecPtOff + 4 p), staged in the prologue when the split spans at most
+// kDecPtMax pages, so a claimed tile's rows are one LDS read away; longer
+// splits read the page table per tile.
+constexpr int kDecPtOff = (kDecLdsBytes + 15) & ~15;
+constexpr int kDecPtMax = 3072;
+constexpr int kDecPtLoads = kDecPtMax / (64 * kDecWaves);
+static_assert(kDecPtLoads * 64 * kDecWaves == kDecPtMax, "page rows staged by a fixed number of loads per thread");
+constexpr uint32_t kDecPtBad = 0xFFFFFFFFu;                          // staged row of a page id outside the pool
 // epilogue reuse of [0, 68K): per-wave O slabs (rows padded to 132 floats),
 // then per-wave running max and denominator
 constexpr int kObStride = 128 + 4;
@@ -917,7 +926,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     static_assert(!PAGED || SPB == 1, "a paged cache takes one sequence per block");
     constexpr int D = 128, QD = 64;
     constexpr int nw = kDecWaves;
-    __shared__ __attribute__((aligned(16))) unsigned char smem[kDecLdsBytes];
+    __shared__ __attribute__((aligned(16))) unsigned char smem[PAGED && !LORA ? kDecPtOff + 4 * kDecPtMax : kDecLdsBytes];
     float *qs = reinterpret_cast<float *>(smem + kDecQsOff);
     float *gq = qs + kDecRows * D;
 
@@ -999,6 +1008,45 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     bool page_bad = false;
     const int32_t *pt_row = PAGED ? a.page_table + b * a.max_pages : nullptr;
     auto half_rows = [&](int t, uint32_t (&rb)[2]) { paged_half_rows(a, pt_row, hk, t, s_end, page_bad, rb); };
+    // the split's page ids (pages pg0 .. pg0 + npg - 1), requested before
+    // the cache prefetch so that waiting for them does not wait for it;
+    // converted to pool rows and staged in LDS before the first barrier
+    // (not with the fused LoRA prologue, whose scalar registers are full)
+    constexpr bool kStage = PAGED && !LORA;
+    const int pg0 = kStage ? (s_begin >> a.page_shift) : 0;
+    const int npg = kStage && s_end > s_begin ? ((s_end - 1) >> a.page_shift) - pg0 + 1 : 0;
+    const bool pt_lds = kStage && npg <= kDecPtMax;
+    uint32_t ptv[kStage ? kDecPtLoads : 1];
+    if constexpr (kStage) {
+        const __amdgpu_buffer_rsrc_t PT = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(pt_row + pg0), (short)0, pt_lds ? npg * 4 : 0, kBufWord3);
+#pragma unroll
+        for (int k = 0; k < kDecPtLoads; ++k)
+            ptv[k] = __builtin_amdgcn_raw_buffer_load_b32(PT, 4u * (uint32_t)(tid + 64 * nw * k), 0, 0);
+    }
+    // rows of the two 16-token halves of the tile at token t: from the
+    // staged rows when the split's pages fit, else from the page table
+    auto claim_rows = [&](int t, uint32_t (&rb)[2]) {
+        if (!kStage || !pt_lds) {
+            // page-table path: the scalar loads are waited for here, before
+            // the next claim is issued, so that wait does not also wait for
+            // the claim's atomic
+            half_rows(t, rb);
+            asm volatile("" ::"s"(rb[0]), "s"(rb[1]));
+            __builtin_amdgcn_sched_barrier(0);
+            return;
+        }
+        const uint32_t *ptl = reinterpret_cast<const uint32_t *>(smem + kDecPtOff);
+        const uint32_t pmask = (1u << a.page_shift) - 1u;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int th = t + 16 * u;
+            const uint32_t base = ptl[imax(imin((th >> a.page_shift) - pg0, npg - 1), 0)];
+            const bool ok = base != kDecPtBad;
+            page_bad = page_bad || (!ok && th < s_end);
+            rb[u] = (ok ? base : 0u) + ((uint32_t)th & pmask);
+        }
+    };
 
     // ── prologue loads: branch-free buffer loads (an absent input gets a
     //    zero-size descriptor and reads 0), issued before the cache
@@ -1155,6 +1203,17 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
             uint4 *dst = reinterpret_cast<uint4 *>(smem + kDecGaOff + dec_chunk(wave, (wave * 16 + j) * 2) * 16);
             dst[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
             dst[1] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+        }
+    }
+    if constexpr (kStage) {
+        // pool row of each staged page (kDecPtBad for an id outside the pool)
+        uint32_t *ptl = reinterpret_cast<uint32_t *>(smem + kDecPtOff);
+        const uint32_t np = (uint32_t)a.n_pages;
+#pragma unroll
+        for (int k = 0; k < kDecPtLoads; ++k) {
+            const int j = tid + 64 * nw * k;
+            if (pt_lds && j < npg)
+                ptl[j] = ptv[k] < np ? (ptv[k] * (uint32_t)a.Hkv + (uint32_t)hk) << a.page_shift : kDecPtBad;
         }
     }
     __syncthreads();
@@ -1390,15 +1449,9 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
         tile_step(ring[0], tile_tok(i_cur), tile_seq(i_cur));
         const int i_pre = wave + nw;
         if (i_pre < ntiles && PAGED) {
-            // paged: a claimed tile's page rows (scalar loads) are read and
-            // waited for before the next claim is issued, so that wait does
-            // not also wait for the claim's atomic
+            // paged: a claimed tile's pool rows, then the next claim
             uint32_t rb[2];
-            auto next_rows = [&](int i) {
-                half_rows(tile_tok(i), rb);
-                asm volatile("" ::"s"(rb[0]), "s"(rb[1]));
-                __builtin_amdgcn_sched_barrier(0);
-            };
+            auto next_rows = [&](int i) { claim_rows(tile_tok(i), rb); };
             i_cur = claim_value(c_raw);
             next_rows(i_cur);
             c_raw = claim_issue(tile_cnt, lane);

@@ -236,3 +236,69 @@ def test_paged_prefill_bad_page_and_prepared(device):
     want = paged_attention(q, cache, pt, lt, cb.to(device), user_id=uid, causal=True, x=xh,
                            lora_a=la.to(device), lora_b=lb.to(device), lora_indices=ids, lora_alpha=0.5)
     assert torch.equal(run, want)
+
+
+def _random_cache(device, B, Hkv, S, seed):
+    """Packed cache of random bytes (codes and sign bits uniform, norms in
+    [0, 2)): the attention reads any byte pattern, and large caches are
+    made without running the encoder."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    kn = torch.randint(0, 256, (B, Hkv, S, 64), generator=g, dtype=torch.uint8, device=device)
+    kq = torch.randint(0, 256, (B, Hkv, S, 8), generator=g, dtype=torch.uint8, device=device)
+    kr = 2 * torch.rand((B, Hkv, S), generator=g, device=device)
+    vn = torch.randint(0, 256, (B, Hkv, S, 64), generator=g, dtype=torch.uint8, device=device)
+    return kn, kq, kr, vn
+
+
+def test_paged_decode_dynamic_claims_and_bad_page(device):
+    """16 sequences x 8 kv heads x 4096 tokens (two splits of 64 tiles per
+    (sequence, kv head)): tiles past each wave's first two are claimed
+    dynamically and their pool rows come from the split's pages staged in
+    LDS.  Against the oracle; then a page id outside the pool in the
+    dynamically claimed range (token 3200 of sequence 3) and one in the first
+    tiles (token 40 of sequence 5) give NaN rows for those sequences only."""
+    from omnistack_rs.cache import paged_attention
+    B, Hq, Hkv, T, S, uid = 16, 32, 8, 1, 4096, 12
+    kn, kq, kr, vn = _random_cache(device, B, Hkv, S, seed=401)
+    cb = _data.gaussian_codebook(Hkv)
+    q = _data.query((B, Hq, T, 128), seed=402)
+    cache, pt, lt = _paged(device, kn, kq, kr, vn, 16, seed=37)
+    got = paged_attention(q.to(device), cache, pt, lt, cb.to(device), user_id=uid)
+    want = restate.fused_attn_python(q.float(), kn.cpu(), kq.cpu(), kr.cpu(), vn.cpu(), cb, uid, 1 / math.sqrt(128), True)
+    _assert_close(got, want, "paged dynamic claims 16 x 4096")
+    pt_bad = pt.clone()
+    pt_bad[3, 3200 // 16] = cache.n_pages + 7
+    pt_bad[5, 40 // 16] = -1
+    bad = paged_attention(q.to(device), cache, pt_bad, lt, cb.to(device), user_id=uid, validate=False)
+    for b in range(B):
+        if b in (3, 5):
+            assert torch.isnan(bad[b]).all(), f"sequence {b} should be NaN"
+        else:
+            assert torch.isfinite(bad[b]).all()
+            _assert_close(bad[b:b + 1], want[b:b + 1], f"paged dynamic claims b{b} beside bad pages")
+
+
+def test_paged_decode_split_longer_than_staged_pages(device):
+    """32 sequences x 8 kv heads x 49600 tokens in 16-token pages: one split
+    per (sequence, kv head) spans 3100 pages, more than the prologue stages,
+    so claimed tiles read their page ids from the page table.  Equal to the
+    contiguous kernel on the same bytes within the parity bar (the dynamic
+    tile claims sum in run-dependent order); a page id outside the pool in
+    the dynamically claimed range gives NaN rows for that sequence only."""
+    from omnistack_rs.cache import paged_attention
+    from omnistack_rs.kernels.fused_attention import omni_attn
+    B, Hq, Hkv, T, S, uid = 32, 32, 8, 1, 49600, 13
+    kn, kq, kr, vn = _random_cache(device, B, Hkv, S, seed=411)
+    cb = _data.gaussian_codebook(Hkv).to(device)
+    q = _data.query((B, Hq, T, 128), seed=412).to(device)
+    ref = omni_attn(q, kn, kq, kr, vn, cb, user_id=uid)
+    cache, pt, lt = _paged(device, kn, kq, kr, vn, 16, spare=0, seed=41)
+    del kn, kq, kr, vn
+    got = paged_attention(q, cache, pt, lt, cb, user_id=uid)
+    _assert_close(got.cpu(), ref.cpu(), "paged split of 3100 pages vs contiguous")
+    pt_bad = pt.clone()
+    pt_bad[7, 40000 // 16] = cache.n_pages
+    bad = paged_attention(q, cache, pt_bad, lt, cb, user_id=uid, validate=False)
+    assert torch.isnan(bad[7]).all()
+    keep = [b for b in range(B) if b != 7]
+    assert torch.isfinite(bad[keep]).all()
