@@ -757,6 +757,18 @@ __device__ __forceinline__ float dpp_mov(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
 }
 
+// fmaxf over the 64 lanes of a wave without LDS: DPP quad permutes and row
+// rotates within each 16-lane row, then the row and half-wave swaps
+// (max is exact and order-free, so every lane gets the same value as an
+// xor-shuffle tree would give)
+__device__ __forceinline__ float wave_max(float m) {
+    m = fmaxf(m, dpp_mov<0xB1>(m));     // quad_perm [1,0,3,2]
+    m = fmaxf(m, dpp_mov<0x4E>(m));     // quad_perm [2,3,0,1]
+    m = fmaxf(m, dpp_mov<0x124>(m));    // row_ror:4
+    m = fmaxf(m, dpp_mov<0x128>(m));    // row_ror:8
+    return max_over_groups(m);
+}
+
 // x[lane ^ H] without LDS: DPP quad permutes (H = 1, 2), row rotates
 // (H = 4, 8; lane i reads lane i - k mod 16 for row_ror:k) and the gfx950
 // row / half-wave swaps (H = 16, 32).
@@ -1159,8 +1171,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
             // and G q (|.| <= 128 * 2^15 * sqrt(2/pi) / 128) stay in fp16 range
             // for any finite q; scores take scale * log2(e) * 2^-k
             float m = row_ok ? fmaxf(fabsf(lo), fabsf(hi)) : 0.0f;
-#pragma unroll
-            for (int sh = 32; sh >= 1; sh >>= 1) m = fmaxf(m, __shfl_xor(m, sh));
+            m = wave_max(m);
             int ex = 0;
             if (m > 0.0f && m < INFINITY) frexpf(m, &ex);
             const float sr = ldexpf(1.0f, 15 - imax(ex, -100));     // 2^k stays finite for tiny rows
@@ -1648,8 +1659,7 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
             if (!ok) lo = hi = 0.0f;
             // row max |q| -> 2^k with max * 2^k in [2^14, 2^15)
             float m = fmaxf(fabsf(lo), fabsf(hi));
-#pragma unroll
-            for (int sh = 32; sh >= 1; sh >>= 1) m = fmaxf(m, __shfl_xor(m, sh));
+            m = wave_max(m);
             int ex = 0;
             if (m > 0.0f && m < INFINITY) { frexpf(m, &ex); }
             const float sr = ldexpf(1.0f, 15 - imax(ex, -100));   // m * sr in [2^14, 2^15) unless m < 2^-101
