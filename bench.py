@@ -13,7 +13,8 @@ same K calls, timed by HIP events on the launch stream; `sustained` times
 
 Also reported (extra keys): C2 serving (B=64, S=50, 32q/8kv, 256-adapter
 rank-8 LoRA gather on Q) p50/p99 latency and users/s; C4 encode GB/s
-(16 x 4096 x 8 kv heads, K and V, fused rotation); a plain streaming read of
+(16 x 4096 x 8 kv heads, K and V, fused rotation), also straight into
+16-token pages, and one decode step's append; a plain streaming read of
 C3's byte count (the device's achievable read rate, for comparison with
 `value`); the reference's CPU path (the oracle restatement) timed on a
 bounded C3 sample on this host.
@@ -544,7 +545,44 @@ def main() -> int:
             "note": "PackedKVEncoder.encode(K, V, out=...): code tables built once, K and V in one launch"}
         log(f"[bench] C4 prepared (K and V in one launch): {t4p * 1e6:.0f} us -> {bytes4 / t4p / 1e9:.0f} GB/s; "
             f"K equal to encode_kv: {eq4}")
-        del k4, v4, enc4, outs4, ref_k
+        # the same tokens encoded straight into 16-token pages (random pool
+        # order): K codes, signs and norms, V codes only
+        from omnistack_rs.cache import PagedKVCache
+        npg4 = B4 * T4 // 16
+        pool4 = PagedKVCache(npg4, Hkv, 16, device=dev)
+        pool4._free = torch.randperm(npg4, generator=torch.Generator().manual_seed(47)).tolist()
+        pt4 = pool4.page_table([pool4.allocate(T4) for _ in range(B4)])
+        pos4 = torch.zeros(B4, dtype=torch.int32, device=dev)
+        app = lambda: pool4.append(enc4, k4, v4, pt4, pos4, validate=False)
+        t4a = wall_eager(app, max(5, args.steps // 5), 2)
+        rows1 = B4 * Hkv * T4
+        bytes4a = rows1 * (D * 2 + 64 + 8 + 4) + rows1 * (D * 2 + 64)
+        idx4 = pt4.long()
+        eq4a = all(torch.equal(pool.index_select(0, idx4[b]).transpose(0, 1).reshape(Hkv, T4, -1), ref[b].reshape(Hkv, T4, -1))
+                   for b in (0, B4 - 1)
+                   for pool, ref in ((pool4.k_nibbles, outs4[0][0]), (pool4.k_qjl, outs4[0][1]),
+                                     (pool4.k_norms, outs4[0][2]), (pool4.v_nibbles, outs4[1][0])))
+        result["encode_c4_paged"] = {
+            "GB_s": round(bytes4a / t4a / 1e9, 1), "us_per_call": round(t4a * 1e6, 1), "bytes": bytes4a,
+            "pct_of_hbm_peak": round(100 * bytes4a / t4a / 1e9 / HBM_PEAK_GBS, 2), "equal_to_prepared": eq4a,
+            "note": "PagedKVCache.append: K and V of C4 encoded into 16-token pages in random order, one launch; "
+                    "V codes only (the attention reads no V residual)"}
+        log(f"[bench] C4 into pages (V codes only): {t4a * 1e6:.0f} us -> {bytes4a / t4a / 1e9:.0f} GB/s; "
+            f"equal to the prepared encoder's output: {eq4a}")
+        # one decode step's new tokens (64 users x 8 kv heads x 1 token) into
+        # their pages, replayed in a HIP graph
+        B1 = 64
+        pool1 = PagedKVCache(B1 * 4, Hkv, 16, device=dev)
+        pt1 = pool1.page_table([pool1.allocate(50) for _ in range(B1)])
+        pos1 = torch.randint(0, 50, (B1,), generator=torch.Generator().manual_seed(48), dtype=torch.int32).to(dev)
+        k1 = k4[:, :, :4].permute(0, 2, 1, 3).reshape(B1, Hkv, 1, D).contiguous()
+        v1 = v4[:, :, :4].permute(0, 2, 1, 3).reshape(B1, Hkv, 1, D).contiguous()
+        step1 = lambda: pool1.append(enc4, k1, v1, pt1, pos1, validate=False)
+        t1 = wall_graph(step1, max(20, args.steps), 5)
+        result["append_decode_step"] = {"us_per_step": round(t1 * 1e6, 2), "users": B1,
+                                        "note": "64 users x 8 kv heads x 1 new token into 16-token pages, HIP graph"}
+        log(f"[bench] decode-step append (64 users x 8 kv heads): {t1 * 1e6:.1f} us/step in a graph")
+        del k4, v4, enc4, outs4, ref_k, pool4, pool1
 
     # C5: chunked prefill, a 512-token bf16 query chunk at the end of a
     # 16384-token cache (query t sees keys 0 .. 15872 + t)

@@ -127,6 +127,27 @@ int omni_encode_pair(const void *x0, const void *x1, int x_dtype, int64_t B, int
                      uint8_t *nibbles1, uint8_t *qjl1, float *norms1, void *stream);
 
 /*
+ * Encode one step's new K (and V) tokens straight into the pages of a paged
+ * pool (the layout of omni_attn_paged): token t of batch entry b is
+ * position p = positions[b] + t of its sequence and goes to slot
+ * p % page_size of page page_table[b * max_pages + p / page_size].  K rows
+ * get codes, sign bits and norms (as omni_encode_pair), V rows codes only
+ * (the attention reads no V residual: fused_attention.py:456-463 passes
+ * zero V signs and norms).  16-bit K / V (B, H, T, 128); `tables` from
+ * omni_encode_build_tables.  A row whose position is negative or past the
+ * table, or whose page id lies outside [0, n_pages), is not written (the
+ * host wrapper checks and raises first).  The reference has no paged cache
+ * (its bake writes a contiguous one, scripts/run_criteo_benchmark.py:355-367);
+ * the codes, signs and norms are those of quantize_heads (quantize.py:542-590).
+ */
+int omni_encode_paged(const void *k, const void *v, int x_dtype, int64_t B, int H, int64_t T,
+                      int rotate, const int8_t *sign_flip, const float *codebooks,
+                      int per_head_codebook, const uint32_t *g_bits, const uint8_t *tables,
+                      size_t tables_bytes, const int32_t *page_table, int64_t max_pages,
+                      const int32_t *positions, int64_t n_pages, int page_size, uint8_t *k_nibbles,
+                      uint8_t *k_qjl, float *k_norms, uint8_t *v_nibbles, void *stream);
+
+/*
  * Dequantize packed rows to f32 (B, H, T, D):
  *   out = cb_h[code] + (b+- . G_h) * fp32(norm * fp32(sqrt(2/pi)/D))   (with_qjl)
  *   out = cb_h[code]                                                   (otherwise)

@@ -283,9 +283,18 @@ struct EncArgs {
     const int8_t *sign_flip;
     uint8_t *nibbles[2], *qjl[2];
     float *norms[2];
-    int64_t T, nrows_head, rows_per_block;
+    int64_t T, nrows_head, rows_per_block[2];    // per tensor
+    int nx0;                                      // paged: blocks of the first tensor
     int H, per_head, rotate;
     float scale;
+    // paged output (encode128_kernel<..., true>): row (b, h, t) goes to pool
+    // row (page_table[b][p >> page_shift] * H + h) * page_size + p %
+    // page_size, p = positions[b] + t; rows whose page is outside the pool
+    // (or past the table) are not written; the second tensor (V) writes
+    // its codes only
+    const int32_t *page_table, *positions;
+    int64_t max_pages, n_pages;
+    int page_shift;
 };
 
 template <int XDT>
@@ -404,20 +413,25 @@ __device__ __forceinline__ double wave_row_dot(const float *st, const uint32_t *
     return s + c;
 }
 
-template <int XDT, bool ROT>
+template <int XDT, bool ROT, bool PAGED>
 __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
     __shared__ __attribute__((aligned(16))) unsigned char smem[kEncLdsBytes];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n = lane & 15, g = lane >> 4;
     const int h = blockIdx.y;
-    // tensor blockIdx.z (K or V of one encode_pair call)
-    const void *const xz = a.x[blockIdx.z];
-    uint8_t *const nibz = a.nibbles[blockIdx.z];
-    uint8_t *const qjlz = a.qjl[blockIdx.z];
-    float *const nrmz = a.norms[blockIdx.z];
-    const int64_t v_begin = (int64_t)blockIdx.x * a.rows_per_block;
-    const int64_t v_end = v_begin + a.rows_per_block < a.nrows_head ? v_begin + a.rows_per_block : a.nrows_head;
+    // tensor zb (K or V of one encode_pair call): blockIdx.z, or (paged, where
+    // K and V take different block counts) blocks x >= nx0 of one row
+    const int zb = PAGED ? (blockIdx.x >= (unsigned)a.nx0 ? 1 : 0) : (int)blockIdx.z;
+    const int64_t xb = PAGED && zb ? (int64_t)blockIdx.x - a.nx0 : (int64_t)blockIdx.x;
+    const void *const xz = a.x[zb];
+    uint8_t *const nibz = a.nibbles[zb];
+    uint8_t *const qjlz = a.qjl[zb];
+    float *const nrmz = a.norms[zb];
+    const int64_t rpb = a.rows_per_block[zb];
+    const int64_t v_begin = xb * rpb;
+    if (v_begin >= a.nrows_head) return;                     // block-uniform, before any barrier
+    const int64_t v_end = v_begin + rpb < a.nrows_head ? v_begin + rpb : a.nrows_head;
 
     // ── prologue: code table, centroids, G bits and bf16 images ───────
     {
@@ -457,12 +471,31 @@ __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
 
     // row of lane n in the 16-row group at virtual row v (< v_end): v + n
     // (clamped) -> (b, t) -> memory row
-    auto group_row = [&](int64_t v) {
+    auto group_bt = [&](int64_t v, int64_t &bq, int64_t &t) {
         const int64_t b0 = v / a.T;                          // uniform
-        int64_t t = (v - b0 * a.T) + (v + n < v_end ? n : (v_end - 1 - v));
-        int64_t bq = b0;
+        t = (v - b0 * a.T) + (v + n < v_end ? n : (v_end - 1 - v));
+        bq = b0;
         while (t >= a.T) { t -= a.T; ++bq; }                 // at most 16 / T + 1 steps
+    };
+    auto group_row = [&](int64_t v) {
+        int64_t bq, t;
+        group_bt(v, bq, t);
         return (bq * a.H + h) * a.T + t;
+    };
+    // output row of lane n's row: the memory row, or (paged) its pool row,
+    // -1 where the page is outside the pool or the position past the table
+    auto group_orow = [&](int64_t v, int64_t irow) -> int64_t {
+        if constexpr (!PAGED) {
+            return irow;
+        } else {
+            int64_t bq, t;
+            group_bt(v, bq, t);
+            const int64_t pos = (int64_t)a.positions[bq] + t;
+            const int64_t pi = pos >> a.page_shift;
+            const int32_t pg = (pos >= 0 && pi < a.max_pages) ? a.page_table[bq * a.max_pages + pi] : -1;
+            if (pg < 0 || pg >= a.n_pages) return -1;
+            return (((int64_t)pg * a.H + h) << a.page_shift) + (pos & ((1 << a.page_shift) - 1));
+        }
     };
     auto load_group = [&](uint4 (&w)[4], int64_t row) {
         const uint4 *src = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(xz) + row * 128);
@@ -472,7 +505,7 @@ __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
     // One 16-row group: w4 holds lane (n, g)'s four 16-byte chunks of row
     // mrow (virtual row v0 + n).
     auto encode_group = [&](const uint4 (&w4)[4], const int64_t mrow, const int64_t v0) {
-        const bool store = v0 + n < v_end && g == 0;
+        const bool store = v0 + n < v_end && g == 0 && (!PAGED || mrow >= 0);
 
         // flip signs on the raw words (8 x 16-bit per chunk), widen
         float x[4][8];
@@ -570,6 +603,16 @@ __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
             for (int i = 0; i < 8; i += 2)
                 wn |= ((vb[s][i] & 0x0Fu) | (vb[s][i + 1] & 0xF0u)) << (4 * i);
             nib[s] = wn;
+        }
+        if (PAGED && zb == 1) {
+            // V in the paged pool: codes only (the attention reads no V
+            // residual), so no residual, norm or projection
+            if (v0 + n < v_end && mrow >= 0) {
+                uint32_t *np = reinterpret_cast<uint32_t *>(nibz + mrow * 64);
+#pragma unroll
+                for (int s = 0; s < 4; ++s) np[4 * s + g] = nib[s];
+            }
+            return;
         }
         float cv[4][8];
 #pragma unroll
@@ -721,7 +764,7 @@ __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
         shi |= xlane_u32<32>(shi);
 
         // stores: nibble dword s of lane (n, g) is bytes 16 s + 4 g .. + 3
-        if (v0 + n < v_end) {
+        if (v0 + n < v_end && (!PAGED || mrow >= 0)) {
             uint32_t *np = reinterpret_cast<uint32_t *>(nibz + mrow * 64);
 #pragma unroll
             for (int s = 0; s < 4; ++s) np[4 * s + g] = nib[s];
@@ -745,12 +788,12 @@ __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
     for (;;) {
         row1 = v0 + kStep < v_end ? group_row(v0 + kStep) : row0;
         load_group(ring1, row1);
-        encode_group(ring0, row0, v0);
+        encode_group(ring0, group_orow(v0, row0), v0);
         v0 += kStep;
         if (v0 >= v_end) break;
         row0 = v0 + kStep < v_end ? group_row(v0 + kStep) : row1;
         load_group(ring0, row0);
-        encode_group(ring1, row1, v0);
+        encode_group(ring1, group_orow(v0, row1), v0);
         v0 += kStep;
         if (v0 >= v_end) break;
     }
@@ -864,11 +907,21 @@ static void launch_code_tables(const float *codebooks, int per_head_codebook, in
 }
 
 // The wave kernel over nz (1 or 2) tensors of one shape, tables built.
+// Paged output of the encoder (omni_encode_paged).  V rows there cost less
+// (codes only): K takes this share (%) of the blocks.
+constexpr int kEncPagedKShare = 55;
+struct EncPaged {
+    const int32_t *page_table, *positions;
+    int64_t max_pages, n_pages;
+    int page_shift;
+};
+
 static int launch_encode128(const void *const xs[2], int nz, int x_dtype, int64_t B, int H, int64_t T, int rotate,
                             const int8_t *sign_flip, const float *codebooks, int per_head_codebook,
                             const uint32_t *g_bits, const uint8_t *tables, uint8_t *const nib[2],
-                            uint8_t *const qjl[2], float *const nrm[2], hipStream_t st) {
-    EncArgs a;
+                            uint8_t *const qjl[2], float *const nrm[2], hipStream_t st,
+                            const EncPaged *paged = nullptr) {
+    EncArgs a{};
     for (int z = 0; z < 2; ++z) {
         const int zz = z < nz ? z : 0;
         a.x[z] = xs[zz]; a.nibbles[z] = nib[zz]; a.qjl[z] = qjl[zz]; a.norms[z] = nrm[zz];
@@ -885,20 +938,43 @@ static int launch_encode128(const void *const xs[2], int nz, int x_dtype, int64_
         if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&p, dev) == hipSuccess && p.multiProcessorCount > 0)
             cus = p.multiProcessorCount;
     }
-    const int64_t per_head_blocks = (cus + (int64_t)H * nz - 1) / ((int64_t)H * nz);
+    // paged K and V: V writes codes only (about 0.4 of K's work per row),
+    // so K's rows are spread over more blocks
     const int64_t grp = 16 * kEncWaves;
-    int64_t rpb = (a.nrows_head + per_head_blocks - 1) / per_head_blocks;
-    rpb = (rpb + grp - 1) / grp * grp;
-    a.rows_per_block = rpb;
-    const int64_t nx = (a.nrows_head + rpb - 1) / rpb;
+    const int64_t per_tensor = (cus + (int64_t)H - 1) / H;         // blocks per head over the tensors
+    int64_t nxz[2] = {1, 1};
+    for (int z = 0; z < 2; ++z) {
+        int64_t blocks = (per_tensor + nz - 1) / nz;
+        if (paged && nz == 2) blocks = z == 0 ? per_tensor * kEncPagedKShare / 100
+                                              : per_tensor - per_tensor * kEncPagedKShare / 100;
+        if (blocks < 1) blocks = 1;
+        int64_t rpb = (a.nrows_head + blocks - 1) / blocks;
+        rpb = (rpb + grp - 1) / grp * grp;
+        a.rows_per_block[z] = rpb;
+        nxz[z] = (a.nrows_head + rpb - 1) / rpb;
+    }
+    a.nx0 = (int)nxz[0];
+    // paged: one grid row of K's blocks then V's (no empty blocks); else
+    // blockIdx.z picks the tensor
+    const int64_t nx = paged ? nxz[0] + (nz > 1 ? nxz[1] : 0) : nxz[0];
     OMNI_CHECK_ARG(nx <= 2147483647LL, "omni_encode: grid too large");
-    const dim3 eg((unsigned)nx, (unsigned)H, (unsigned)nz), eb(64 * kEncWaves);
-    if (x_dtype == OMNI_BF16) {
-        if (rotate) hipLaunchKernelGGL((encode128_kernel<OMNI_BF16, true>), eg, eb, 0, st, a);
-        else hipLaunchKernelGGL((encode128_kernel<OMNI_BF16, false>), eg, eb, 0, st, a);
+    const dim3 eg((unsigned)nx, (unsigned)H, paged ? 1u : (unsigned)nz), eb(64 * kEncWaves);
+    if (paged) {
+        a.page_table = paged->page_table; a.positions = paged->positions;
+        a.max_pages = paged->max_pages; a.n_pages = paged->n_pages; a.page_shift = paged->page_shift;
+        if (x_dtype == OMNI_BF16) {
+            if (rotate) hipLaunchKernelGGL((encode128_kernel<OMNI_BF16, true, true>), eg, eb, 0, st, a);
+            else hipLaunchKernelGGL((encode128_kernel<OMNI_BF16, false, true>), eg, eb, 0, st, a);
+        } else {
+            if (rotate) hipLaunchKernelGGL((encode128_kernel<OMNI_F16, true, true>), eg, eb, 0, st, a);
+            else hipLaunchKernelGGL((encode128_kernel<OMNI_F16, false, true>), eg, eb, 0, st, a);
+        }
+    } else if (x_dtype == OMNI_BF16) {
+        if (rotate) hipLaunchKernelGGL((encode128_kernel<OMNI_BF16, true, false>), eg, eb, 0, st, a);
+        else hipLaunchKernelGGL((encode128_kernel<OMNI_BF16, false, false>), eg, eb, 0, st, a);
     } else {
-        if (rotate) hipLaunchKernelGGL((encode128_kernel<OMNI_F16, true>), eg, eb, 0, st, a);
-        else hipLaunchKernelGGL((encode128_kernel<OMNI_F16, false>), eg, eb, 0, st, a);
+        if (rotate) hipLaunchKernelGGL((encode128_kernel<OMNI_F16, true, false>), eg, eb, 0, st, a);
+        else hipLaunchKernelGGL((encode128_kernel<OMNI_F16, false, false>), eg, eb, 0, st, a);
     }
     OMNI_CHECK_LAUNCH("omni_encode");
     return OMNI_OK;
@@ -1004,6 +1080,39 @@ extern "C" int omni_encode_pair(const void *x0, const void *x1, int x_dtype, int
         rc = launch_encode_rows(x1, x_dtype, B, H, T, head_dim, rotate, sign_flip, codebooks, per_head_codebook,
                                 g_bits, nibbles1, qjl1, norms1, st);
     return rc;
+}
+
+extern "C" int omni_encode_paged(const void *k, const void *v, int x_dtype, int64_t B, int H, int64_t T,
+                                 int rotate, const int8_t *sign_flip, const float *codebooks,
+                                 int per_head_codebook, const uint32_t *g_bits, const uint8_t *tables,
+                                 size_t tables_bytes, const int32_t *page_table, int64_t max_pages,
+                                 const int32_t *positions, int64_t n_pages, int page_size, uint8_t *k_nibbles,
+                                 uint8_t *k_qjl, float *k_norms, uint8_t *v_nibbles, void *stream) {
+    OMNI_CHECK_ARG(x_dtype == OMNI_BF16 || x_dtype == OMNI_F16, "omni_encode_paged: K and V must be bf16 or f16");
+    OMNI_CHECK_ARG(B >= 0 && H >= 0 && T >= 0, "omni_encode_paged: negative shape");
+    if (B == 0 || H == 0 || T == 0) return OMNI_OK;
+    OMNI_CHECK_ARG(k && codebooks && g_bits && page_table && positions && k_nibbles && k_qjl && k_norms,
+                   "omni_encode_paged: NULL pointer");
+    OMNI_CHECK_ARG(v == nullptr || v_nibbles, "omni_encode_paged: NULL V pool for a V input");
+    OMNI_CHECK_ARG(B <= 65535 && H <= 65535, "omni_encode_paged: B and H must be <= 65535");
+    int shift = 4;
+    while (shift < 11 && (1 << shift) < page_size) ++shift;
+    OMNI_CHECK_ARG(page_size >= 16 && page_size <= 1024 && (1 << shift) == page_size,
+                   "omni_encode_paged: page_size must be a power of two in [16, 1024], got %d", page_size);
+    OMNI_CHECK_ARG(n_pages >= 1 && max_pages >= 1, "omni_encode_paged: need n_pages >= 1, max_pages >= 1");
+    OMNI_CHECK_ARG(n_pages * H * (int64_t)page_size < (int64_t(1) << 40), "omni_encode_paged: pool too large");
+    const size_t need = omni_encode_tables_size(H, per_head_codebook);
+    if (tables == nullptr || tables_bytes < need) {
+        set_error("omni_encode_paged: %zu bytes of code tables required, %zu given", need, tables_bytes);
+        return OMNI_EWORKSPACE;
+    }
+    const int nz = v ? 2 : 1;
+    const void *xs[2] = {k, v ? v : k};
+    uint8_t *nib[2] = {k_nibbles, v ? v_nibbles : k_nibbles}, *qj[2] = {k_qjl, k_qjl};
+    float *nr[2] = {k_norms, k_norms};
+    const EncPaged pg{page_table, positions, max_pages, n_pages, shift};
+    return launch_encode128(xs, nz, x_dtype, B, H, T, rotate, sign_flip, codebooks, per_head_codebook, g_bits,
+                            tables, nib, qj, nr, as_stream(stream), &pg);
 }
 
 extern "C" int omni_dequantize(const uint8_t *nibbles, const uint8_t *qjl, const float *norms,

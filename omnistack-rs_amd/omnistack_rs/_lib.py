@@ -35,6 +35,8 @@ SIGNATURES = {
     "omni_encode_build_tables": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _c_sz, _vp]),
     "omni_encode_pair": (_c_int, [_vp, _vp, _c_int, _c_i64, _c_int, _c_i64, _c_int, _c_int, _vp, _vp, _c_int,
                                   _vp, _vp, _c_sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "omni_encode_paged": (_c_int, [_vp, _vp, _c_int, _c_i64, _c_int, _c_i64, _c_int, _vp, _vp, _c_int, _vp,
+                                   _vp, _c_sz, _vp, _c_i64, _vp, _c_i64, _c_int, _vp, _vp, _vp, _vp, _vp]),
     "omni_dequantize": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _vp, _c_i64, _c_int, _c_i64, _c_int,
                                  _c_int, _vp, _vp]),
     "omni_lora_apply": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _c_int, _vp, _c_i64, _c_int, _c_i64,

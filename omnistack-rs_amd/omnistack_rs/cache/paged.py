@@ -106,6 +106,70 @@ class PagedKVCache:
                           (self.v_nibbles, v_nibbles)):
             pool[pg, :, slot] = src.to(device=self.device, dtype=pool.dtype).transpose(0, 1)
 
+    def append(self, encoder, k: torch.Tensor, v: Optional[torch.Tensor], page_table: torch.Tensor,
+               positions: torch.Tensor, validate: bool = True) -> None:
+        """Encode new K (and V) tokens straight into the pool, one launch
+        (``omni_encode_paged``): k, v are (B, n_kv_heads, T, head_dim) in the
+        encoder's 16-bit dtype; token t of batch entry b is position p =
+        positions[b] + t of its sequence and lands in slot p % page_size of
+        page page_table[b, p // page_size].  K rows get the codes, sign bits
+        and norms ``encoder.encode`` gives, V rows their codes (the attention
+        reads no V residual).  ``encoder`` is a ``PackedKVEncoder`` (16-bit,
+        head_dim 128) for this pool's heads.  The pages must be allocated;
+        the caller advances its sequence lengths.  ``validate`` checks the
+        positions and the touched page ids on the host (a device sync);
+        without it (inside graph capture) a row whose page lies outside the
+        pool is not written."""
+        from ..kernels.quantize import PackedKVEncoder
+        if not isinstance(encoder, PackedKVEncoder):
+            raise TypeError("encoder must be a PackedKVEncoder")
+        if encoder.H != self.n_kv_heads or encoder.D != self.head_dim or encoder.tables is None:
+            raise ValueError(f"encoder must be a 16-bit head_dim {self.head_dim} encoder for "
+                             f"{self.n_kv_heads} kv heads")
+        if encoder.device != self.device:
+            raise ValueError(f"encoder is on {encoder.device}, the pool on {self.device}")
+        want = (k.shape[0], self.n_kv_heads, k.shape[2] if k.dim() == 4 else -1, self.head_dim)
+        if k.dim() != 4 or tuple(k.shape) != want or k.dtype != encoder.dtype:
+            raise ValueError(f"k must be {encoder.dtype} (B, {self.n_kv_heads}, T, {self.head_dim}), "
+                             f"got {k.dtype} {tuple(k.shape)}")
+        if v is not None and (v.shape != k.shape or v.dtype != k.dtype):
+            raise ValueError(f"v must match k: {k.dtype} {tuple(k.shape)}, got {v.dtype} {tuple(v.shape)}")
+        B, _, T, _ = k.shape
+        if page_table.dim() != 2 or page_table.shape[0] != B or page_table.dtype != torch.int32:
+            raise ValueError(f"page_table must be int32 ({B}, max_pages), got {page_table.dtype} "
+                             f"{tuple(page_table.shape)}")
+        if tuple(positions.shape) != (B,) or positions.dtype != torch.int32:
+            raise ValueError(f"positions must be int32 ({B},), got {positions.dtype} {tuple(positions.shape)}")
+        for t in (k, v, page_table, positions):
+            if t is not None and t.device != self.device:
+                raise ValueError(f"inputs must be on {self.device}")
+        if B == 0 or T == 0:
+            return
+        ps, mp = self.page_size, page_table.shape[1]
+        pt = page_table.contiguous()
+        pos = positions.contiguous()
+        if validate:
+            ph = pos.cpu().to(torch.int64)
+            if (ph < 0).any() or (ph + T > mp * ps).any():
+                raise ValueError(f"positions must lie in [0, {mp * ps - T}] for {T} new tokens "
+                                 f"and {mp} pages of {ps}")
+            first, last = ph // ps, (ph + T - 1) // ps
+            ids = pt.cpu().to(torch.int64)
+            cols = torch.arange(mp)
+            touched = (cols[None, :] >= first[:, None]) & (cols[None, :] <= last[:, None])
+            bad = touched & ((ids < 0) | (ids >= self.n_pages))
+            if bad.any():
+                b, c = (int(x) for x in bad.nonzero()[0])
+                raise IndexError(f"page_table[{b}, {c}] = {int(ids[b, c])} lies outside the pool of "
+                                 f"{self.n_pages} pages")
+        kc = k.contiguous()
+        vc = v.contiguous() if v is not None else None
+        _lib.check(_lib.lib().omni_encode_paged(
+            _lib.ptr(kc), _lib.ptr(vc), encoder.code, B, self.n_kv_heads, T, encoder.rotate, _lib.ptr(encoder.sf),
+            _lib.ptr(encoder.cb), encoder.per_head, _lib.ptr(encoder.gb), _lib.ptr(encoder.tables),
+            encoder.tables_bytes, _lib.ptr(pt), mp, _lib.ptr(pos), self.n_pages, ps, _lib.ptr(self.k_nibbles),
+            _lib.ptr(self.k_qjl), _lib.ptr(self.k_norms), _lib.ptr(self.v_nibbles), _lib.stream_of(self.device)))
+
     def page_table(self, sequences: Sequence[Sequence[int]], max_pages: Optional[int] = None) -> torch.Tensor:
         """int32 (len(sequences), max_pages) table; unused entries are -1."""
         width = max([len(s) for s in sequences] + [1]) if max_pages is None else int(max_pages)

@@ -302,3 +302,118 @@ def test_paged_decode_split_longer_than_staged_pages(device):
     assert torch.isnan(bad[7]).all()
     keep = [b for b in range(B) if b != 7]
     assert torch.isfinite(bad[keep]).all()
+
+
+# ── encode straight into pages (PagedKVCache.append, omni_encode_paged) ────
+
+def _encoder(device, H, uid, dtype=torch.bfloat16, rotate=True):
+    from omnistack_rs.kernels.quantize import PackedKVEncoder
+    cb = _data.gaussian_codebook(H).to(device)
+    s = _data.sign_flip().to(device) if rotate else None
+    return PackedKVEncoder(cb, H, user_id=uid, rotate=rotate, sign_flip=s, dtype=dtype, device=device), cb
+
+
+def _pools_equal(a, b):
+    for name in ("k_nibbles", "k_qjl", "k_norms", "v_nibbles"):
+        x, y = getattr(a, name), getattr(b, name)
+        assert torch.equal(x, y), f"{name} differs in {(x != y).sum().item()} elements"
+
+
+@pytest.mark.parametrize("page_size", [16, 64])
+@pytest.mark.parametrize("dtype,rotate", [(torch.bfloat16, True), (torch.float16, False)])
+def test_paged_append_equals_encode_and_write(device, page_size, dtype, rotate):
+    """A 40-token chunk and then one decode token per sequence, encoded
+    straight into pages at ragged positions, leave the pool exactly as the
+    prepared encoder's output copied in by PagedKVCache.write (K codes, sign
+    bits and norms; V codes)."""
+    from omnistack_rs.cache import PagedKVCache
+    B, H, cap, uid = 5, 8, 320, 21
+    enc, _ = _encoder(device, H, uid, dtype, rotate)
+    pos0 = [0, 17, 100, 255, 3]
+    got = PagedKVCache(B * cap // page_size + 4, H, page_size, device=device)
+    ref = PagedKVCache(got.n_pages, H, page_size, device=device)
+    g = torch.Generator().manual_seed(page_size)
+    order = torch.randperm(got.n_pages, generator=g).tolist()
+    got._free = list(order)
+    ref._free = list(order)
+    pages = [got.allocate(cap) for _ in range(B)]
+    for _ in range(B):
+        ref.allocate(cap)
+    pt = got.page_table(pages)
+    for step, T in enumerate((40, 1)):
+        k = _data.kv((B, H, T, 128), seed=500 + step, dtype=dtype).to(device)
+        v = _data.kv((B, H, T, 128), seed=600 + step, dtype=dtype).to(device)
+        pos = [p + (40 if step else 0) for p in pos0]
+        got.append(enc, k, v, pt, torch.tensor(pos, dtype=torch.int32, device=device))
+        (kn, kq, kr), (vn, _, _) = enc.encode(k, v)
+        for b in range(B):
+            ref.write(pages[b], kn[b], kq[b], kr[b], vn[b], start=pos[b])
+        torch.cuda.synchronize()
+        _pools_equal(got, ref)
+
+
+def test_paged_append_decode_batch_and_bad_pages(device):
+    """The serving shape (64 users x 8 kv heads, one new token each): equal
+    to encode + write; without validation a row whose page id lies outside
+    the pool is not written (every other row is), with validation the host
+    raises; positions past the table raise."""
+    from omnistack_rs.cache import PagedKVCache
+    B, H, uid = 64, 8, 22
+    enc, _ = _encoder(device, H, uid)
+    got = PagedKVCache(B * 4 + 8, H, 16, device=device)
+    ref = PagedKVCache(got.n_pages, H, 16, device=device)
+    pages = [got.allocate(50) for _ in range(B)]
+    for _ in range(B):
+        ref.allocate(50)
+    pt = got.page_table(pages)
+    pos = torch.randint(0, 50, (B,), generator=torch.Generator().manual_seed(5), dtype=torch.int32)
+    k = _data.kv((B, H, 1, 128), seed=701).to(device)
+    v = _data.kv((B, H, 1, 128), seed=702).to(device)
+    pt_bad = pt.clone()
+    b_bad = 9
+    pt_bad[b_bad, int(pos[b_bad]) // 16] = got.n_pages + 3
+    with pytest.raises(IndexError):
+        got.append(enc, k, v, pt_bad, pos.to(device))
+    with pytest.raises(ValueError):
+        got.append(enc, k, v, pt, torch.full((B,), 4 * 16, dtype=torch.int32, device=device))
+    got.append(enc, k, v, pt_bad, pos.to(device), validate=False)
+    (kn, kq, kr), (vn, _, _) = enc.encode(k, v)
+    for b in range(B):
+        if b != b_bad:
+            ref.write(pages[b], kn[b], kq[b], kr[b], vn[b], start=int(pos[b]))
+    torch.cuda.synchronize()
+    _pools_equal(got, ref)
+
+
+def test_paged_serving_loop_append_then_attend(device):
+    """Prefill 64 tokens into pages, then three decode steps that each
+    append one token and attend over the pages: every step's output equals
+    omni_attn over the contiguous encoding of the same tokens bit for bit
+    (at most 12 tiles per split, one per wave) and meets the oracle bar."""
+    from omnistack_rs.cache import PagedKVCache, paged_attention
+    from omnistack_rs.kernels.fused_attention import omni_attn
+    from omnistack_rs.kernels.quantize import encode_kv
+    B, Hq, H, uid = 4, 32, 8, 23
+    enc, cb = _encoder(device, H, uid)
+    s = _data.sign_flip().to(device)
+    cache = PagedKVCache(B * 8 + 2, H, 16, device=device)
+    g = torch.Generator().manual_seed(3)
+    cache._free = torch.randperm(cache.n_pages, generator=g).tolist()
+    pages = [cache.allocate(100) for _ in range(B)]
+    pt = cache.page_table(pages)
+    K = _data.kv((B, H, 67, 128), seed=801).to(device)
+    V = _data.kv((B, H, 67, 128), seed=802).to(device)
+    cache.append(enc, K[:, :, :64], V[:, :, :64], pt, torch.zeros(B, dtype=torch.int32, device=device))
+    for step in range(3):
+        L = 64 + step
+        cache.append(enc, K[:, :, L:L + 1], V[:, :, L:L + 1], pt, torch.full((B,), L, dtype=torch.int32, device=device))
+        lens = torch.full((B,), L + 1, dtype=torch.int32, device=device)
+        q = _data.query((B, Hq, 1, 128), seed=810 + step).to(device)
+        got = paged_attention(q, cache, pt, lens, cb, user_id=uid)
+        kn, kq, kr = encode_kv(K[:, :, :L + 1], cb, user_id=uid, sign_flip=s)
+        vn, _, _ = encode_kv(V[:, :, :L + 1], cb, user_id=uid, sign_flip=s)
+        ref = omni_attn(q, kn, kq, kr, vn, cb, user_id=uid)
+        assert torch.equal(got, ref), f"step {step}: paged differs by {(got - ref).abs().max().item():.3e}"
+        want = restate.fused_attn_python(q.float().cpu(), kn.cpu(), kq.cpu(), kr.cpu(), vn.cpu(), cb.cpu(), uid,
+                                         1 / math.sqrt(128), True)
+        _assert_close(got, want, f"serving loop step {step}")

@@ -214,6 +214,22 @@ def test_encode_pair_host_checks(L):
     assert L.omni_encode_pair(None, None, 2, 0, 4, 100, 128, 1, None, None, 1, None, None, 0, *tail) == 0
 
 
+def test_encode_paged_host_checks(L):
+    """omni_encode_paged argument checks (no launch)."""
+    from omnistack_rs import _lib
+
+    def call(k=1, v=1, dt=2, B=4, page_size=16, tables=1, tb=1 << 20, v_nib=1):
+        return L.omni_encode_paged(k, v, dt, B, 8, 1, 1, None, 1, 1, 1, tables, tb, 1, 4, 1, 64, page_size,
+                                   1, 1, 1, v_nib, None)
+    assert call(dt=0) == _lib.OMNI_EINVAL and "bf16 or f16" in _lib.last_error()
+    assert call(page_size=24) == _lib.OMNI_EINVAL and "power of two" in _lib.last_error()
+    assert call(page_size=2048) == _lib.OMNI_EINVAL
+    assert call(v_nib=None) == _lib.OMNI_EINVAL and "V pool" in _lib.last_error()
+    assert call(tables=None) == _lib.OMNI_EWORKSPACE and "code tables" in _lib.last_error()
+    assert call(tb=1000) == _lib.OMNI_EWORKSPACE
+    assert call(B=0) == 0
+
+
 def test_prepared_encoder_refuses_cpu():
     from omnistack_rs.kernels.quantize import PackedKVEncoder
     with pytest.raises(RuntimeError):
