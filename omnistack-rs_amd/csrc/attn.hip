@@ -545,7 +545,8 @@ constexpr int kDecCscOff = kDecGaOff + kDecRows * 16 * 2 * 16;      // per row: 
 // ~32 ways)
 __device__ __forceinline__ int dec_chunk(int row, int c) { return c ^ (2 * (row & 7)); }
 constexpr int kDecCntOff = kDecCscOff + kDecRows * 4;                // next unclaimed tile of the block
-constexpr int kDecLdsBytes = kDecCntOff + 16;
+constexpr int kDecLrOff = kDecCntOff + 16;                           // fused LoRA: x A^T of two row groups
+constexpr int kDecLdsBytes = kDecLrOff + 2 * 16 * 4;
 // Paged cache: the pool row of each page of the split (page p of the split
 // at kDecPtOff + 4 p), staged in the prologue when the split spans at most
 // kDecPtMax pages, so a claimed tile's rows are one LDS read away; longer
@@ -848,8 +849,49 @@ __device__ __forceinline__ void lora_x_load(uint32_t (&xw)[4], const AttnArgs &a
     for (int kh = 0; kh < 4; ++kh) xw[kh] = __builtin_amdgcn_raw_buffer_load_b16(XR, 2u * (64 * kh + lane), 0, 0);
 }
 
+// Rank components 2 s and 2 s + 1 of each 8-block of x A_id^T (s = row slot
+// % 4), the lora_row sums, into `dst` (rank <= 16 floats) for the row
+// group of four slots that shares the (sequence, token).
+__device__ __forceinline__ void lora_rank_share(const AttnArgs &a, int32_t id_raw, const uint32_t (&xw)[4], int slot,
+                                                int lane, float *dst) {
+    const int32_t id = __builtin_amdgcn_readfirstlane(id_raw);
+    const bool active = id >= 0 && id < a.lora_n;
+    const int64_t sid = active ? id : 0;
+    const bool bf = a.lora_w_dtype == OMNI_BF16;
+    const int hidden = a.lora_hidden, rank = a.lora_rank;
+    const __amdgpu_buffer_rsrc_t AR = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(reinterpret_cast<const uint16_t *>(a.lora_a) + sid * rank * (int64_t)hidden), (short)0,
+        2 * rank * hidden, kBufWord3);
+    float xv[4];
+#pragma unroll
+    for (int kh = 0; kh < 4; ++kh) xv[kh] = lora_w16(xw[kh], bf);
+    const int sub = slot & 3;
+    for (int j0 = 0; j0 < rank; j0 += 8) {
+        uint32_t aw[2][4];
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+            const uint32_t j = j0 + 2 * sub + jj;
+#pragma unroll
+            for (int kh = 0; kh < 4; ++kh)
+                aw[jj][kh] = __builtin_amdgcn_raw_buffer_load_b16(AR, 2u * (j * hidden + 64 * kh + lane), 0, 0);
+        }
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+            float part = 0.0f;
+#pragma unroll
+            for (int kh = 0; kh < 4; ++kh) {
+                const float f = __builtin_fmaf(xv[kh], lora_w16(aw[jj][kh], bf), part);
+                part = 64 * kh + lane < hidden ? f : part;
+            }
+            const float dr = lora_wave_sum(part);
+            if (lane == 0) dst[j0 + 2 * sub + jj] = dr;
+        }
+    }
+}
+
+// `shared`: the rank components from lora_rank_share (NULL: computed here).
 __device__ __forceinline__ void lora_row(float &lo, float &hi, const AttnArgs &a, int32_t id_raw,
-                                         const uint32_t (&xw)[4], int hq, int lane) {
+                                         const uint32_t (&xw)[4], int hq, int lane, const float *shared = nullptr) {
     const int32_t id = __builtin_amdgcn_readfirstlane(id_raw);
     const bool active = id >= 0 && id < a.lora_n, bad = id >= a.lora_n;
     const int64_t sid = active ? id : 0;
@@ -870,12 +912,14 @@ __device__ __forceinline__ void lora_row(float &lo, float &hi, const AttnArgs &a
         // all loads of eight rank components first (one latency); rows past
         // the rank read 0 (A) or are not used (B)
         uint32_t aw[8][4], bl[8], bh[8];
+        if (shared == nullptr) {
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-            const uint32_t j = j0 + jj;
+            for (int jj = 0; jj < 8; ++jj) {
+                const uint32_t j = j0 + jj;
 #pragma unroll
-            for (int kh = 0; kh < 4; ++kh)
-                aw[jj][kh] = __builtin_amdgcn_raw_buffer_load_b16(AR, 2u * (j * hidden + 64 * kh + lane), 0, 0);
+                for (int kh = 0; kh < 4; ++kh)
+                    aw[jj][kh] = __builtin_amdgcn_raw_buffer_load_b16(AR, 2u * (j * hidden + 64 * kh + lane), 0, 0);
+            }
         }
         {
             // B rows lane and 64 + lane, components j0 .. j0 + 7: one 16-byte
@@ -892,16 +936,21 @@ __device__ __forceinline__ void lora_row(float &lo, float &hi, const AttnArgs &a
             }
         }
         float dr[8];
+        if (shared != nullptr) {
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-            float part = 0.0f;
+            for (int jj = 0; jj < 8; ++jj) dr[jj] = shared[j0 + jj];
+        } else {
 #pragma unroll
-            for (int kh = 0; kh < 4; ++kh) {
-                // a select, not a branch: the load must not sink into one
-                const float f = __builtin_fmaf(xv[kh], lora_w16(aw[jj][kh], bf), part);
-                part = 64 * kh + lane < hidden ? f : part;
+            for (int jj = 0; jj < 8; ++jj) {
+                float part = 0.0f;
+#pragma unroll
+                for (int kh = 0; kh < 4; ++kh) {
+                    // a select, not a branch: the load must not sink into one
+                    const float f = __builtin_fmaf(xv[kh], lora_w16(aw[jj][kh], bf), part);
+                    part = 64 * kh + lane < hidden ? f : part;
+                }
+                dr[jj] = lora_wave_sum(part);
             }
-            dr[jj] = lora_wave_sum(part);
         }
         // B values live in registers here: keeps the compiler from sinking
         // their loads into the (uniform) rank test below
@@ -1127,6 +1176,18 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     if (tid == 0) *reinterpret_cast<int *>(smem + kDecCntOff) = 2 * nw;
     // ── sign table (threads 0..511) ───────────────────────────────────
     if (tid < 512) sign_table_store(smem, tid);
+    // fused LoRA with G % 4 == 0: row slots 4 k .. 4 k + 3 hold one
+    // (sequence, token), so x A^T is shared: each of the four waves sums a
+    // quarter of its rank components, the others read them after a barrier
+    // (same per-lane order and lane tree: the same values)
+    const bool lora_share = LORA && (a.G & 3) == 0;
+    float *lora_dr = reinterpret_cast<float *>(smem + kDecLrOff) + 16 * (wave >> 2);
+    if constexpr (LORA) {
+        if (lora_share) {
+            if (wave < kDecRows && row_ok) lora_rank_share(a, lora_id, lora_xw, wave, lane, lora_dr);
+            __syncthreads();
+        }
+    }
     if (wave >= kDecRows) {
         // ── byte LUT, built by the waves without a query row while the
         //    others rotate theirs: entry e at e * 256, 32 copies of (hi
@@ -1158,7 +1219,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
                 hi = f16_to_f32((uint16_t)q16_hi);
             }
             if constexpr (LORA) {
-                if (row_ok) lora_row(lo, hi, a, lora_id, lora_xw, hq_q, lane);
+                if (row_ok) lora_row(lo, hi, a, lora_id, lora_xw, hq_q, lane, lora_share ? lora_dr : nullptr);
             }
             lo = (sf_lo & 0x80u) ? -lo : lo;
             hi = (sf_hi & 0x80u) ? -hi : hi;
