@@ -417,3 +417,56 @@ def test_paged_serving_loop_append_then_attend(device):
         want = restate.fused_attn_python(q.float().cpu(), kn.cpu(), kq.cpu(), kr.cpu(), vn.cpu(), cb.cpu(), uid,
                                          1 / math.sqrt(128), True)
         _assert_close(got, want, f"serving loop step {step}")
+
+
+def test_decode_step_graph_append_and_attend(device):
+    """One serving decode step as a HIP graph: the new tokens' K and V
+    encoded into their pages, then attention over the pages; each replay
+    (new tokens, queries, positions and lengths written between replays)
+    leaves the pool and the output exactly as eager calls do."""
+    from omnistack_rs.cache import PagedKVAttention, PagedKVCache, paged_attention
+    B, Hq, H, uid = 8, 32, 8, 24
+    enc, cb = _encoder(device, H, uid)
+    got = PagedKVCache(B * 8, H, 16, device=device)
+    ref = PagedKVCache(got.n_pages, H, 16, device=device)
+    order = torch.randperm(got.n_pages, generator=torch.Generator().manual_seed(9)).tolist()
+    got._free = list(order)
+    ref._free = list(order)
+    pages = [got.allocate(100) for _ in range(B)]
+    for _ in range(B):
+        ref.allocate(100)
+    pt = got.page_table(pages)
+    k0 = _data.kv((B, H, 40, 128), seed=901).to(device)
+    v0 = _data.kv((B, H, 40, 128), seed=902).to(device)
+    zero = torch.zeros(B, dtype=torch.int32, device=device)
+    got.append(enc, k0, v0, pt, zero)
+    ref.append(enc, k0, v0, pt, zero)
+    att = PagedKVAttention(got, cb, n_heads=Hq, batch=B, max_pages=pt.shape[1], user_id=uid)
+    ks = torch.zeros(B, H, 1, 128, dtype=torch.bfloat16, device=device)
+    vs = torch.zeros_like(ks)
+    qs = torch.zeros(B, Hq, 1, 128, dtype=torch.bfloat16, device=device)
+    pos = torch.full((B,), 40, dtype=torch.int32, device=device)
+    lens = pos + 1
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        got.append(enc, ks, vs, pt, pos, validate=False)
+        att.run(qs, pt, lens)
+    for r in range(3):
+        L = 40 + r
+        k = _data.kv((B, H, 1, 128), seed=910 + r).to(device)
+        v = _data.kv((B, H, 1, 128), seed=920 + r).to(device)
+        q = _data.query((B, Hq, 1, 128), seed=930 + r).to(device)
+        ks.copy_(k)
+        vs.copy_(v)
+        qs.copy_(q)
+        pos.fill_(L)
+        lens.fill_(L + 1)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        out = att.out.clone()
+        ref.append(enc, k, v, pt, pos.clone())
+        want = paged_attention(q, ref, pt, lens.clone(), cb, user_id=uid)
+        _pools_equal(got, ref)
+        assert torch.equal(out, want), f"replay {r} differs by {(out - want).abs().max().item():.3e}"
