@@ -488,6 +488,30 @@ def main() -> int:
                                         "p50/p99 from HIP events per eager call, users/s from a HIP graph of steps"}
         log(f"[bench] C2: p50 {p50 * 1e6:.1f} us p99 {p99 * 1e6:.1f} us (events), "
             f"{t2 * 1e6:.1f} us/step graph -> {B2 / t2:.0f} users/s")
+        # the whole decode step over a paged cache: each user's new K / V
+        # token encoded into its page, then the same attention over the pages
+        from omnistack_rs.cache import PagedKVAttention, PagedKVCache
+        from omnistack_rs.kernels.quantize import PackedKVEncoder
+        pool2, pt2, _ = PagedKVCache.from_contiguous(kn2, kq2, kr2, vn2, page_size=16,
+                                                     generator=torch.Generator().manual_seed(49))
+        enc2 = PackedKVEncoder(cb, Hkv, user_id=uid, sign_flip=sign)
+        kt = torch.randn(B2, Hkv, 1, D, generator=g2, device=dev).to(torch.bfloat16)
+        vt = torch.randn(B2, Hkv, 1, D, generator=g2, device=dev).to(torch.bfloat16)
+        pos2 = torch.full((B2,), S2, dtype=torch.int32, device=dev)
+        lens2 = pos2 + 1
+        attpg = PagedKVAttention(pool2, cb, n_heads=Hq, batch=B2, max_pages=pt2.shape[1], user_id=uid,
+                                 rotate_q=True, sign_flip=sign, lora_a=la, lora_b=lb, lora_alpha=1.0)
+
+        def step_paged():
+            pool2.append(enc2, kt, vt, pt2, pos2, validate=False)
+            attpg.run(q2, pt2, lens2, xh, ids)
+        t2p = wall_graph(step_paged, steps2, args.warmup)
+        result["serving_c2_paged_step"] = {
+            "us_per_step_graph": round(t2p * 1e6, 2), "users_per_s": round(B2 / t2p, 1),
+            "note": "the C2 step over 16-token pages with the new token appended first: one launch encodes each "
+                    "user's new K and V into its page, one runs LoRA + rotate_q + attention over 51 tokens"}
+        log(f"[bench] C2 paged step with append: {t2p * 1e6:.1f} us/step graph -> {B2 / t2p:.0f} users/s")
+        del pool2, enc2, attpg
 
     if "c2pool" in sections:
         # the reference serving loop's shape: 64 users drawn with replacement
