@@ -984,10 +984,9 @@ __device__ __forceinline__ int claim_value(int v) { return __builtin_amdgcn_read
 template <bool QJL, int PF, int SPB, bool LORA, bool PAGED>
 __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs a) {
     static_assert(SPB == 1 || SPB == 2, "one or two sequences per block");
-    static_assert(!PAGED || SPB == 1, "a paged cache takes one sequence per block");
     constexpr int D = 128, QD = 64;
     constexpr int nw = kDecWaves;
-    __shared__ __attribute__((aligned(16))) unsigned char smem[PAGED && !LORA ? kDecPtOff + 4 * kDecPtMax : kDecLdsBytes];
+    __shared__ __attribute__((aligned(16))) unsigned char smem[PAGED && !LORA && SPB == 1 ? kDecPtOff + 4 * kDecPtMax : kDecLdsBytes];
     float *qs = reinterpret_cast<float *>(smem + kDecQsOff);
     float *gq = qs + kDecRows * D;
 
@@ -1018,16 +1017,24 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
 
     // ── cache stream descriptors ──────────────────────────────────────
     const int s_begin = split * (int)a.split_len;
-    // paged: this sequence's length; one outside [0, capacity] reads nothing
-    // and its rows come out NaN
-    int seq_len = (int)a.S;
-    bool len_bad = false;
+    // paged: each sequence's length; one outside [0, capacity] reads nothing
+    // and its rows come out NaN (with two sequences per block, seq_len1 ..
+    // s_end1 are the second's; otherwise they repeat the first's)
+    int seq_len = (int)a.S, seq_len1 = (int)a.S;
+    bool len_bad = false, len_bad1 = false;
     if constexpr (PAGED) {
         const int32_t L = a.seq_lens[b32];
         len_bad = L < 0 || (int64_t)L > a.S;
         seq_len = len_bad ? 0 : L;
+        seq_len1 = seq_len;
+        if (SPB > 1 && nseq > 1) {
+            const int32_t L1 = a.seq_lens[b32 + 1];
+            len_bad1 = L1 < 0 || (int64_t)L1 > a.S;
+            seq_len1 = len_bad1 ? 0 : L1;
+        }
     }
     const int s_end = imax(s_begin, (int)imin64(seq_len, (int64_t)s_begin + a.split_len));
+    const int s_end1 = imax(s_begin, (int)imin64(seq_len1, (int64_t)s_begin + a.split_len));
     auto stream_bufs = [&](int64_t bb) {
         if constexpr (PAGED) {
             // the whole pool (its row count times 64 fits 32 bits: the host checks)
@@ -1055,9 +1062,10 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     };
     const DecBufs P = stream_bufs(b);
     const DecBufs P1 = stream_bufs(nseq > 1 ? b + 1 : b);
-    // tiles of the split per sequence; claim index i -> sequence i / tps
+    // tiles of the split per sequence; claim index i -> sequence (i >= tps)
     const int tps = (s_end - s_begin + kDecTile - 1) / kDecTile;
-    const int ntiles = tps * nseq;
+    const int tps1 = (s_end1 - s_begin + kDecTile - 1) / kDecTile;
+    const int ntiles = tps + (nseq > 1 ? tps1 : 0);
     DecOffsets OFS;
     OFS.k = (uint32_t)n * 64u + 16u * g;
     OFS.sg = (uint32_t)n * 8u;
@@ -1066,14 +1074,18 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
 
     // Paged cache: pool rows of a tile's two halves; a page id outside the
     // pool marks this wave's state bad (the sequence's rows come out NaN)
-    bool page_bad = false;
+    bool page_bad = false, page_bad1 = false;
     const int32_t *pt_row = PAGED ? a.page_table + b * a.max_pages : nullptr;
-    auto half_rows = [&](int t, uint32_t (&rb)[2]) { paged_half_rows(a, pt_row, hk, t, s_end, page_bad, rb); };
+    const int32_t *pt_row1 = PAGED && SPB > 1 && nseq > 1 ? pt_row + a.max_pages : pt_row;
+    auto half_rows = [&](int t, int sq, uint32_t (&rb)[2]) {
+        if (SPB > 1 && sq) paged_half_rows(a, pt_row1, hk, t, s_end1, page_bad1, rb);
+        else paged_half_rows(a, pt_row, hk, t, s_end, page_bad, rb);
+    };
     // the split's page ids (pages pg0 .. pg0 + npg - 1), requested before
     // the cache prefetch so that waiting for them does not wait for it;
     // converted to pool rows and staged in LDS before the first barrier
     // (not with the fused LoRA prologue, whose scalar registers are full)
-    constexpr bool kStage = PAGED && !LORA;
+    constexpr bool kStage = PAGED && !LORA && SPB == 1;
     const int pg0 = kStage ? (s_begin >> a.page_shift) : 0;
     const int npg = kStage && s_end > s_begin ? ((s_end - 1) >> a.page_shift) - pg0 + 1 : 0;
     const bool pt_lds = kStage && npg <= kDecPtMax;
@@ -1087,12 +1099,12 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     }
     // rows of the two 16-token halves of the tile at token t: from the
     // staged rows when the split's pages fit, else from the page table
-    auto claim_rows = [&](int t, uint32_t (&rb)[2]) {
+    auto claim_rows = [&](int t, int sq, uint32_t (&rb)[2]) {
         if (!kStage || !pt_lds) {
             // page-table path: the scalar loads are waited for here, before
             // the next claim is issued, so that wait does not also wait for
             // the claim's atomic
-            half_rows(t, rb);
+            half_rows(t, sq, rb);
             asm volatile("" ::"s"(rb[0]), "s"(rb[1]));
             __builtin_amdgcn_sched_barrier(0);
             return;
@@ -1160,8 +1172,8 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     auto tile_tok = [&](int i) { return s_begin + (i - tile_seq(i) * tps) * kDecTile; };
     if constexpr (PAGED) {
         uint32_t rb0[2], rb1[2];
-        half_rows(tile_tok(wave), rb0);
-        half_rows(tile_tok(wave + nw), rb1);
+        half_rows(tile_tok(wave), tile_seq(wave), rb0);
+        half_rows(tile_tok(wave + nw), tile_seq(wave + nw), rb1);
         tile_load_paged<QJL>(ring[0], P, OFS, rb0);
         tile_load_paged<QJL>(ring[1], P, OFS, rb1);
     } else {
@@ -1359,7 +1371,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     // causal: query token t sees keys <= coff + t (a paged cache aligns the
     // last query token with the sequence's last key: coff = length - T)
     const bool causal = a.causal_offset >= 0;
-    const int64_t coff = PAGED ? (int64_t)seq_len - a.T : a.causal_offset;
+    const int64_t coff = PAGED ? (int64_t)(seq_n ? seq_len1 : seq_len) - a.T : a.causal_offset;
     const int64_t key_limit64 = (causal && row_valid(rn)) ? coff + div_small(rho_n, a.g_magic) : INT64_MAX;
 
     // ── main loop ─────────────────────────────────────────────────────
@@ -1431,7 +1443,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int tn = tt + 16 * u + 4 * g + i;
-                    if (tn >= s_end || tn > key_limit || seq_n != tseq) sc[4 * u + i] = -INFINITY;
+                    if (tn >= (tseq ? s_end1 : s_end) || tn > key_limit || seq_n != tseq) sc[4 * u + i] = -INFINITY;
                 }
         }
 
@@ -1523,14 +1535,14 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
         if (i_pre < ntiles && PAGED) {
             // paged: a claimed tile's pool rows, then the next claim
             uint32_t rb[2];
-            auto next_rows = [&](int i) { claim_rows(tile_tok(i), rb); };
+            auto next_rows = [&](int i) { claim_rows(tile_tok(i), tile_seq(i), rb); };
             i_cur = claim_value(c_raw);
             next_rows(i_cur);
             c_raw = claim_issue(tile_cnt, lane);
             __builtin_amdgcn_sched_barrier(0);
             tile_load_paged<QJL>(ring[0], P, OFS, rb);
             __builtin_amdgcn_sched_barrier(0);
-            tile_step(ring[1], tile_tok(i_pre), 0);
+            tile_step(ring[1], tile_tok(i_pre), tile_seq(i_pre));
             for (;;) {
                 if (i_cur >= ntiles) break;
                 const int i_nxt = claim_value(c_raw);
@@ -1539,7 +1551,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
                 __builtin_amdgcn_sched_barrier(0);
                 tile_load_paged<QJL>(ring[1], P, OFS, rb);
                 __builtin_amdgcn_sched_barrier(0);
-                tile_step(ring[0], tile_tok(i_cur), 0);
+                tile_step(ring[0], tile_tok(i_cur), tile_seq(i_cur));
                 if (i_nxt >= ntiles) break;
                 i_cur = claim_value(c_raw);
                 next_rows(i_cur);
@@ -1547,7 +1559,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
                 __builtin_amdgcn_sched_barrier(0);
                 tile_load_paged<QJL>(ring[0], P, OFS, rb);
                 __builtin_amdgcn_sched_barrier(0);
-                tile_step(ring[1], tile_tok(i_nxt), 0);
+                tile_step(ring[1], tile_tok(i_nxt), tile_seq(i_nxt));
             }
         } else if (i_pre < ntiles) {
             i_cur = claim_value(c_raw);
@@ -1594,7 +1606,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
             if (ge == 0) {
                 wm[wave * kDecRows + ne] = m_run;
                 // a page outside the pool poisons the sequence's denominator
-                wl[wave * kDecRows + ne] = page_bad ? __builtin_nanf("") : lacc_sum[0];
+                wl[wave * kDecRows + ne] = (row_seq(ne) ? page_bad1 : page_bad) ? __builtin_nanf("") : lacc_sum[0];
             }
             float *dst = ob + (wave * kDecRows + ne) * kObStride;
 #pragma unroll
@@ -1633,7 +1645,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
             (void)cache_seq(a, rr_b, bad);
             if (bad) lsum = __builtin_nanf("");
         }
-        if (len_bad) lsum = __builtin_nanf("");
+        if (row_seq(rr) ? len_bad1 : len_bad) lsum = __builtin_nanf("");
         if (a.splits == 1) {
             const int t = div_small(rr_rho, a.g_magic);
             const int hq = hk * a.G + (rr_rho - t * a.G);
@@ -2578,7 +2590,7 @@ static Plan make_plan(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int D, b
     // than CUs, at most 4 query rows each): two sequences share a block's 8
     // row slots, halving the blocks (and the per-block prologues) without
     // idling any slot.
-    p.spb = (!paged && p.dec128 && T * G <= kDecRows / 2 && B >= 2 && B * (int64_t)Hkv > cus) ? 2 : 1;
+    p.spb = (p.dec128 && T * G <= kDecRows / 2 && B >= 2 && B * (int64_t)Hkv > cus) ? 2 : 1;
     const int64_t units = ((B + p.spb - 1) / p.spb) * (int64_t)Hkv * p.n_rchunks;
     if (p.prefill || p.prefill32) {
         const int64_t tiles = (S + kDecTile - 1) / kDecTile;
@@ -2759,7 +2771,9 @@ static int attn_run(const void *q, int q_dtype, const uint8_t *k_nib, const uint
         }
     } else if (p.dec128 && paged) {
         hipStream_t st = as_stream(stream);
-        if (with_qjl) launch_decode128<true, 1, true>(lora_fused, grid, block, st, a);
+        if (with_qjl && p.spb > 1) launch_decode128<true, 2, true>(lora_fused, grid, block, st, a);
+        else if (with_qjl) launch_decode128<true, 1, true>(lora_fused, grid, block, st, a);
+        else if (p.spb > 1) launch_decode128<false, 2, true>(lora_fused, grid, block, st, a);
         else launch_decode128<false, 1, true>(lora_fused, grid, block, st, a);
     } else if (p.dec128) {
         hipStream_t st = as_stream(stream);

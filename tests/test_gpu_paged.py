@@ -470,3 +470,46 @@ def test_decode_step_graph_append_and_attend(device):
         want = paged_attention(q, ref, pt, lens.clone(), cb, user_id=uid)
         _pools_equal(got, ref)
         assert torch.equal(out, want), f"replay {r} differs by {(out - want).abs().max().item():.3e}"
+
+
+def test_paged_two_sequences_per_block(device):
+    """More (sequence, kv head) pairs than CUs with one query token each: the
+    paged decode kernel packs two sequences into a block (each with its own
+    page table row and length).  Ragged lengths against the oracle (41
+    sequences: the last block holds one); a bad page or length of one
+    sequence gives NaN rows for it only, not for its block partner; equal
+    lengths with LoRA and rotation equal the contiguous call bit for bit."""
+    from omnistack_rs.cache import paged_attention
+    from omnistack_rs.kernels.fused_attention import omni_attn
+    B, Hq, Hkv, T, S, uid = 41, 32, 8, 1, 96, 14
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=421, user_id=uid)
+    q = _data.query((B, Hq, T, 128), seed=422)
+    lens = torch.randint(1, S + 1, (B,), generator=torch.Generator().manual_seed(423)).tolist()
+    cache, pt, lt = _paged(device, kn, kq, kr, vn, 16, lens=lens, seed=43)
+    got = paged_attention(q.to(device), cache, pt, lt, cb.to(device), user_id=uid).cpu()
+    for b, L in enumerate(lens):
+        sl = slice(b, b + 1)
+        want = restate.fused_attn_python(q[sl].float(), kn[sl, :, :L], kq[sl, :, :L], kr[sl, :, :L],
+                                         vn[sl, :, :L], cb, uid, 1 / math.sqrt(128), True)
+        _assert_close(got[sl], want, f"paged two per block b{b} len{L}")
+    pt_bad, lt_bad = pt.clone(), lt.clone()
+    pt_bad[3, 0] = cache.n_pages + 1
+    lt_bad[6] = -1
+    bad = paged_attention(q.to(device), cache, pt_bad, lt_bad, cb.to(device), user_id=uid, validate=False).cpu()
+    for b in range(B):
+        if b in (3, 6):
+            assert torch.isnan(bad[b]).all(), f"sequence {b} should be NaN"
+        else:
+            assert torch.equal(bad[b], got[b]), f"sequence {b} changed beside a bad partner"
+    # equal lengths: the same tiles per block as the contiguous kernel
+    R, HID, NL = 8, 128, 16
+    la, lb = (t.to(torch.bfloat16) for t in _data.lora_bank(NL, R, HID, Hq * 128))
+    ids = _data.lora_ids(B, NL)
+    xh = _data.query((B, T, HID), seed=424)
+    s = _data.sign_flip(128)
+    cache2, pt2, lt2 = _paged(device, kn, kq, kr, vn, 16, seed=47)
+    kw = dict(user_id=uid, rotate_q=True, sign_flip=s.to(device), x=xh.to(device), lora_a=la.to(device),
+              lora_b=lb.to(device), lora_indices=ids.to(device), lora_alpha=0.5)
+    got2 = paged_attention(q.to(device), cache2, pt2, lt2, cb.to(device), **kw)
+    ref2 = omni_attn(*(t.to(device) for t in (q, kn, kq, kr, vn, cb)), **kw)
+    assert torch.equal(got2, ref2), f"paged LoRA two per block differs by {(got2 - ref2).abs().max().item():.3e}"
