@@ -2562,18 +2562,6 @@ struct Plan {
     size_t lds, ws_bytes;
 };
 
-static int device_cus() {
-    static int cached[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (!cached[dev]) {
-        hipDeviceProp_t p;
-        cached[dev] = (hipGetDeviceProperties(&p, dev) == hipSuccess && p.multiProcessorCount > 0)
-                          ? p.multiProcessorCount : 256;
-    }
-    return cached[dev];
-}
-
 static int64_t clamp64(int64_t v, int64_t lo, int64_t hi) { return v < lo ? lo : (v > hi ? hi : v); }
 
 static Plan make_plan(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int D, bool q32, bool paged = false) {

@@ -931,13 +931,7 @@ static int launch_encode128(const void *const xs[2], int nz, int x_dtype, int64_
     a.scale = inv_sqrt_dim_f32(128);
     // about one block per CU across the tensors and heads; each block a run
     // of rows of one head of one tensor
-    int cus = 256;
-    {
-        int dev = 0;
-        hipDeviceProp_t p;
-        if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&p, dev) == hipSuccess && p.multiProcessorCount > 0)
-            cus = p.multiProcessorCount;
-    }
+    const int cus = device_cus();
     // paged K and V: V writes codes only (about 0.4 of K's work per row),
     // so K's rows are spread over more blocks
     const int64_t grp = 16 * kEncWaves;

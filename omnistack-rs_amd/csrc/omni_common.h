@@ -32,6 +32,20 @@ static inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream
 
 // fp32 1/sqrt(D) exactly as torch forms `x * (1.0 / math.sqrt(D))` on an fp32
 // tensor: the Python double is rounded to fp32 before the multiply.
+// Compute units of the current device, queried once per device (a full
+// property query costs far more than a launch; 256 if it fails).
+static inline int device_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cached[dev]) {
+        int n = 0;
+        cached[dev] = (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+                          ? n : 256;
+    }
+    return cached[dev];
+}
+
 static inline float inv_sqrt_dim_f32(int D) { return (float)(1.0 / __builtin_sqrt((double)D)); }
 
 // ── element conversions (round-to-nearest-even, like torch) ─────────────
