@@ -315,7 +315,7 @@ class PackedKVAttention:
                 (cache_index is not None and cache_index.device != dev):
             raise ValueError(f"q, x, lora_indices and cache_index must be on {dev}")
         B, Hq, T, D = self.shape
-        stream = torch.cuda.current_stream(self.device).cuda_stream
+        stream = _lib.stream_of(self.device)
         qp = q.data_ptr()
         lora_args = None
         if x is not None:
