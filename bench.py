@@ -130,14 +130,22 @@ def make_cache32(B, Hkv, S, dev, seed, uid, cb, P):
 
 
 def cpu_model() -> str:
+    """/proc/cpuinfo's model name of the first CPU, with its family and model
+    numbers (a virtual machine may report only the vendor's brand there) and
+    the logical CPUs visible to this process."""
+    info = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if not line.strip():
+                    break                      # first CPU only
+                k, _, v = line.partition(":")
+                info.setdefault(k.strip(), v.strip())
     except OSError:
         pass
-    return platform.processor() or platform.machine()
+    name = info.get("model name") or platform.processor() or platform.machine()
+    fam = f"family {info['cpu family']} model {info['model']}, " if "cpu family" in info and "model" in info else ""
+    return f"{name} ({fam}{os.cpu_count()} logical CPUs visible)"
 
 
 def timed_region(fn, steps, warmup, stream):
