@@ -4,8 +4,10 @@ fused_attention.py:435-466; max-abs <= 2e-3, mean-abs <= 2e-4): batch,
 GQA group, query tokens, cache length, causal or not, QJL on or off,
 query dtype and head_dim are drawn together, so kernel choices (decode with
 one or two sequences per block, split-K, chunked prefill, head_dim 32)
-meet combinations the targeted tests do not list."""
+meet combinations the targeted tests do not list.  OMNI_RANDOM_CASES and
+OMNI_RANDOM_PAGED (default 14 and 6) draw longer sweeps from the same seed."""
 import math
+import os
 import random
 
 import pytest
@@ -19,7 +21,7 @@ pytestmark = pytest.mark.gpu
 
 _CASES = []
 _rng = random.Random(20261202)
-for _i in range(14):
+for _i in range(int(os.environ.get("OMNI_RANDOM_CASES", "14"))):
     Hkv = _rng.choice([1, 2, 4, 8])
     G = _rng.choice([1, 2, 4, 8])
     T = _rng.choice([1, 1, 1, 2, 3, 7, 20])
@@ -49,7 +51,7 @@ def test_random_shape_matches_oracle(device, B, Hq, Hkv, T, S, causal, qjl, dtyp
 
 
 _PCASES = []
-for _i in range(6):
+for _i in range(int(os.environ.get("OMNI_RANDOM_PAGED", "6"))):
     Hkv = _rng.choice([2, 8])
     G = _rng.choice([1, 4])
     B = _rng.choice([3, 9, 70])
