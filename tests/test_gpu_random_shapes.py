@@ -4,8 +4,11 @@ fused_attention.py:435-466; max-abs <= 2e-3, mean-abs <= 2e-4): batch,
 GQA group, query tokens, cache length, causal or not, QJL on or off,
 query dtype and head_dim are drawn together, so kernel choices (decode with
 one or two sequences per block, split-K, chunked prefill, head_dim 32)
-meet combinations the targeted tests do not list.  OMNI_RANDOM_CASES and
-OMNI_RANDOM_PAGED (default 14 and 6) draw longer sweeps from the same seed."""
+meet combinations the targeted tests do not list; the encoder likewise
+(dtype, head_dim, rotation with or without a sign flip, per-head or shared
+codebook, user id) against the oracle's codes, signs and norms.
+OMNI_RANDOM_CASES, OMNI_RANDOM_PAGED and OMNI_RANDOM_ENC (default 14, 6 and
+10) draw longer sweeps from the same seed."""
 import math
 import os
 import random
@@ -79,3 +82,40 @@ def test_random_paged_matches_oracle(device, B, Hq, Hkv, S, ps):
         want = restate.fused_attn_python(q[sl].float(), kn[sl, :, :L], kq[sl, :, :L], kr[sl, :, :L],
                                          vn[sl, :, :L], cb, uid, 1 / math.sqrt(128), True)
         _assert_close(got[sl], want, f"random paged B{B} Hq{Hq} Hkv{Hkv} ps{ps} b{b} len{L}")
+
+
+_ECASES = []
+for _i in range(int(os.environ.get("OMNI_RANDOM_ENC", "10"))):
+    B = _rng.choice([1, 2, 3, 5])
+    H = _rng.choice([1, 2, 4, 8])
+    T = _rng.choice([1, 7, 16, 33, 200, 513])
+    dt = _rng.choice([torch.bfloat16, torch.float16, torch.float32])
+    D = _rng.choice([128, 128, 32])
+    rot = _rng.random() < 0.6
+    flip = rot and _rng.random() < 0.5
+    shared = _rng.random() < 0.3
+    _ECASES.append((B, H, T, dt, D, rot, flip, shared, _rng.randint(0, 5000)))
+
+
+@pytest.mark.parametrize("B,H,T,dtype,D,rot,flip,shared,uid", _ECASES)
+def test_random_encode_bit_exact(device, B, H, T, dtype, D, rot, flip, shared, uid):
+    """The prepared encoder (rotation in the kernel or not, per-head or
+    shared codebook, any user id) and quantize_heads on the rotated input,
+    both against the oracle's codes, signs and norms."""
+    from omnistack_rs.kernels.quantize import PackedKVEncoder, quantize_heads
+    from tests._checks import check_encode
+    tag = f"B{B} H{H} T{T} {dtype} D{D} rot{int(rot)} flip{int(flip)} shared{int(shared)} uid{uid}"
+    print(f"[random encode] {tag}", flush=True)
+    x = _data.kv((B, H, T, D), seed=B * 100 + T + D, dtype=dtype)
+    s = _data.sign_flip(D) if flip else None
+    xr = restate.rotate(x, s) if rot else x
+    cb = torch.stack([restate.lloyd_max(xr[:, h].reshape(-1).float()[:50000], max_iters=40) for h in range(H)])
+    if shared:
+        cb = cb[0].contiguous()
+    enc = PackedKVEncoder(cb.to(device), H, user_id=uid, rotate=rot, sign_flip=s.to(device) if flip else None,
+                          dtype=dtype, head_dim=D)
+    nib, qjl, nrm = enc.encode(x.to(device))
+    check_encode(xr, cb, uid, nib, qjl, nrm, tag=f"encoder {tag}")
+    nib2, qjl2, nrm2 = quantize_heads(xr.to(device), cb.to(device), user_id=uid)
+    assert torch.equal(nib2.cpu(), nib.cpu()) and torch.equal(qjl2.cpu(), qjl.cpu()) and \
+        torch.equal(nrm2.cpu(), nrm.cpu()), f"quantize_heads differs from the encoder: {tag}"
