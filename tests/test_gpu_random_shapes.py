@@ -7,8 +7,10 @@ one or two sequences per block, split-K, chunked prefill, head_dim 32)
 meet combinations the targeted tests do not list; the encoder likewise
 (dtype, head_dim, rotation with or without a sign flip, per-head or shared
 codebook, user id) against the oracle's codes, signs and norms.
-OMNI_RANDOM_CASES, OMNI_RANDOM_PAGED and OMNI_RANDOM_ENC (default 14, 6 and
-10) draw longer sweeps from the same seed."""
+Adapters: fused and separate LoRA paths equal bit for bit and match the
+oracle.  OMNI_RANDOM_CASES, OMNI_RANDOM_PAGED, OMNI_RANDOM_ENC and
+OMNI_RANDOM_LORA (default 14, 6, 10 and 8) draw longer sweeps from the same
+seed."""
 import math
 import os
 import random
@@ -119,3 +121,47 @@ def test_random_encode_bit_exact(device, B, H, T, dtype, D, rot, flip, shared, u
     nib2, qjl2, nrm2 = quantize_heads(xr.to(device), cb.to(device), user_id=uid)
     assert torch.equal(nib2.cpu(), nib.cpu()) and torch.equal(qjl2.cpu(), qjl.cpu()) and \
         torch.equal(nrm2.cpu(), nrm.cpu()), f"quantize_heads differs from the encoder: {tag}"
+
+
+_LCASES = []
+for _i in range(int(os.environ.get("OMNI_RANDOM_LORA", "8"))):
+    Hkv = _rng.choice([1, 2, 8])
+    G = _rng.choice([1, 2, 4])
+    _LCASES.append((_rng.choice([2, 5, 40, 70]), Hkv * G, Hkv, _rng.choice([1, 1, 2, 3]), _rng.choice([17, 50, 120]),
+                    _rng.choice([torch.bfloat16, torch.float16, torch.float32]),
+                    _rng.choice([torch.bfloat16, torch.float16]), _rng.choice([8, 16, 16, 4, 12]),
+                    _rng.choice([64, 96, 128, 200, 256]), _rng.random() < 0.5))
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,T,S,qdt,wdt,rank,hidden,rot", _LCASES)
+def test_random_lora_attention(device, B, Hq, Hkv, T, S, qdt, wdt, rank, hidden, rot):
+    """Attention with per-user adapters in one call (fused into the decode
+    prologue where the adapter shape allows, else gather-apply first) equals
+    the gather-apply kernel followed by attention, bit for bit, and (without
+    the in-kernel rotation) the oracle within the attention tolerance."""
+    from omnistack_rs.kernels.fused_attention import _apply_lora_to_q, omni_attn
+    uid, L = 9, 11
+    tag = f"B{B} Hq{Hq} Hkv{Hkv} T{T} S{S} q{qdt} w{wdt} rank{rank} hidden{hidden} rot{int(rot)}"
+    print(f"[random lora] {tag}", flush=True)
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=B + S + rank, user_id=uid)
+    a, bw = _data.lora_bank(L, rank, hidden, Hq * 128, seed=hidden + rank)
+    a, bw = a.to(wdt), bw.to(wdt)
+    q = _data.query((B, Hq, T, 128), seed=B * 7 + T, dtype=qdt)
+    x = torch.randn(B, T, hidden, generator=_data.gen(B + hidden)).to(wdt)
+    ids = _data.lora_ids(B, L, seed=B + rank)
+    ids[0] = -1
+    s = _data.sign_flip() if rot else None
+    dv = [t.to(device) for t in (kn, kq, kr, vn, cb)]
+    kw = dict(user_id=uid, rotate_q=rot, sign_flip=s.to(device) if rot else None)
+    got = omni_attn(q.to(device), *dv, x=x.to(device), lora_a=a.to(device), lora_b=bw.to(device),
+                    lora_indices=ids.to(device), lora_alpha=0.5, **kw)
+    q_eff = _apply_lora_to_q(q.to(device), x.to(device), a.to(device), bw.to(device), ids.to(device), 0.5)
+    want = omni_attn(q_eff, *dv, **kw)
+    assert torch.equal(got, want), f"fused and separate LoRA differ: {tag}"
+    if not rot:
+        # q_eff in q's dtype as the reference computes it, attention in fp32
+        # (the oracle would round its output to a 16-bit q's dtype; the
+        # kernels return fp32)
+        q_ref = restate.apply_lora_to_q(q, x, a, bw, ids, 0.5)
+        ref = restate.fused_attn_python(q_ref.float(), kn, kq, kr, vn, cb, uid, 1 / math.sqrt(128), True)
+        _assert_close(got, ref, f"random lora {tag}")
