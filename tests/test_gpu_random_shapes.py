@@ -8,9 +8,10 @@ meet combinations the targeted tests do not list; the encoder likewise
 (dtype, head_dim, rotation with or without a sign flip, per-head or shared
 codebook, user id) against the oracle's codes, signs and norms.
 Adapters: fused and separate LoRA paths equal bit for bit and match the
-oracle.  OMNI_RANDOM_CASES, OMNI_RANDOM_PAGED, OMNI_RANDOM_ENC and
-OMNI_RANDOM_LORA (default 14, 6, 10 and 8) draw longer sweeps from the same
-seed."""
+oracle; dense reference_attn cases within fp32 conditioning.
+OMNI_RANDOM_CASES, OMNI_RANDOM_PAGED, OMNI_RANDOM_ENC, OMNI_RANDOM_LORA and
+OMNI_RANDOM_DENSE (default 14, 6, 10, 8 and 8) draw longer sweeps from the
+same seed."""
 import math
 import os
 import random
@@ -165,3 +166,48 @@ def test_random_lora_attention(device, B, Hq, Hkv, T, S, qdt, wdt, rank, hidden,
         q_ref = restate.apply_lora_to_q(q, x, a, bw, ids, 0.5)
         ref = restate.fused_attn_python(q_ref.float(), kn, kq, kr, vn, cb, uid, 1 / math.sqrt(128), True)
         _assert_close(got, ref, f"random lora {tag}")
+
+
+_DCASES = []
+for _i in range(int(os.environ.get("OMNI_RANDOM_DENSE", "8"))):
+    Hkv = _rng.choice([1, 2, 4])
+    _DCASES.append((_rng.choice([1, 2, 3]), Hkv * _rng.choice([1, 2, 4]), Hkv, _rng.choice([1, 2, 5, 40]),
+                    _rng.choice([1, 17, 128, 129, 300]), _rng.choice([32, 64, 128, 256]),
+                    _rng.choice(["none", "causal", "bias"]), _rng.choice([None, 0.3])))
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,T,S,D,mask,scale", _DCASES)
+def test_random_dense_attention(device, B, Hq, Hkv, T, S, D, mask, scale):
+    """reference_attn on fp32 K / V (the dense MFMA kernels) against the
+    oracle's reference_attn: GQA, head_dim, masks (none, causal, additive
+    per-batch bias) and score scale drawn together."""
+    from omnistack_rs.attention import reference_attn
+    tag = f"B{B} Hq{Hq} Hkv{Hkv} T{T} S{S} D{D} mask {mask} scale {scale}"
+    print(f"[random dense] {tag}", flush=True)
+    g = _data.gen(B * 1000 + T * 10 + S + D)
+    q = torch.randn(B, Hq, T, D, generator=g)
+    k = torch.randn(B, Hkv, S, D, generator=g)
+    v = torch.randn(B, Hkv, S, D, generator=g)
+    m = None
+    if mask == "causal":
+        m = torch.full((T, S), float("-inf")).triu(S - T + 1) if S >= T else None
+    elif mask == "bias":
+        m = torch.randn(B, 1, T, S, generator=g)
+    got = reference_attn(q.to(device), k.to(device), v.to(device), mask=None if m is None else m.to(device),
+                         scale=scale)
+    want = restate.reference_attn(q, k, v, mask=m, scale=scale)
+    # fp32 scores carry a relative error of a few ulps of the largest score
+    # magnitude (sums of D products, in another order on the MFMA), which
+    # the softmax turns into an absolute error of that size times |v|: an
+    # output that nearly cancels to 0 is held to that, not to 2e-5 of itself
+    sc = scale if scale is not None else 1 / math.sqrt(D)
+    smax = (q @ k.repeat_interleave(Hq // Hkv, dim=1).transpose(-1, -2)).abs().max().item() * abs(sc)
+    if m is not None:
+        smax += m.abs().max().item()
+    g_, w_ = got.cpu().float(), want.float()
+    assert torch.equal(torch.isnan(g_), torch.isnan(w_)), f"{tag}: NaN pattern differs"
+    fin = ~torch.isnan(w_)
+    d = (g_[fin] - w_[fin]).abs()
+    lim = 2e-6 + 2e-5 * w_[fin].abs() + 2 ** -21 * max(1.0, smax) * v.abs().max().item()
+    print(f"[random dense] {tag}: max {d.max().item() if d.numel() else 0:.3e} (score max {smax:.1f})", flush=True)
+    assert bool((d <= lim).all()), f"{tag}: max {d.max().item():.3e}"
