@@ -8,10 +8,11 @@ meet combinations the targeted tests do not list; the encoder likewise
 (dtype, head_dim, rotation with or without a sign flip, per-head or shared
 codebook, user id) against the oracle's codes, signs and norms.
 Adapters: fused and separate LoRA paths equal bit for bit and match the
-oracle; dense reference_attn cases within fp32 conditioning.
-OMNI_RANDOM_CASES, OMNI_RANDOM_PAGED, OMNI_RANDOM_ENC, OMNI_RANDOM_LORA and
-OMNI_RANDOM_DENSE (default 14, 6, 10, 8 and 8) draw longer sweeps from the
-same seed."""
+oracle; dense reference_attn cases within fp32 conditioning; GPU Lloyd-Max
+on drawn distributions against the oracle's recipe.  OMNI_RANDOM_CASES,
+OMNI_RANDOM_PAGED, OMNI_RANDOM_ENC, OMNI_RANDOM_LORA, OMNI_RANDOM_DENSE and
+OMNI_RANDOM_CALIB (default 14, 6, 10, 8, 8 and 6) draw longer sweeps from
+the same seed."""
 import math
 import os
 import random
@@ -211,3 +212,41 @@ def test_random_dense_attention(device, B, Hq, Hkv, T, S, D, mask, scale):
     lim = 2e-6 + 2e-5 * w_[fin].abs() + 2 ** -21 * max(1.0, smax) * v.abs().max().item()
     print(f"[random dense] {tag}: max {d.max().item() if d.numel() else 0:.3e} (score max {smax:.1f})", flush=True)
     assert bool((d <= lim).all()), f"{tag}: max {d.max().item():.3e}"
+
+
+_CCASES = []
+for _i in range(int(os.environ.get("OMNI_RANDOM_CALIB", "6"))):
+    _CCASES.append((_rng.choice(["normal", "uniform", "laplace", "bimodal", "lognormal"]),
+                    _rng.choice([64, 1000, 5003, 20000, 65543]), _rng.choice([0.02, 1.0, 30.0]),
+                    _rng.choice([torch.float32, torch.float32, torch.bfloat16, torch.float16])))
+
+
+@pytest.mark.parametrize("dist,n,scale,dtype", _CCASES)
+def test_random_calibration(device, dist, n, scale, dtype):
+    """GPU Lloyd-Max against the oracle's recipe (codebook.py:64-108) on drawn
+    distributions, sizes, scales and sample dtypes: centroids within the
+    stopping tolerance, quantizer MSE within 1e-5 relative."""
+    from tests.test_gpu_calib import _fit
+    tag = f"{dist} n{n} scale{scale} {dtype}"
+    print(f"[random calib] {tag}", flush=True)
+    g = _data.gen(n + int(scale * 100))
+    if dist == "normal":
+        x = torch.randn(n, generator=g)
+    elif dist == "uniform":
+        x = torch.rand(n, generator=g) * 2 - 1
+    elif dist == "laplace":
+        u = torch.rand(n, generator=g) - 0.5
+        x = -torch.sign(u) * torch.log1p(-2 * u.abs())
+    elif dist == "bimodal":
+        x = torch.randn(n, generator=g) * 0.3 + torch.where(torch.rand(n, generator=g) < 0.5, -2.0, 2.0)
+    else:
+        x = torch.exp(torch.randn(n, generator=g))
+    x = (x * scale).to(dtype)
+    got, iters = _fit(x, device)
+    want = restate.lloyd_max(x.float())
+    assert 1 <= iters <= 300
+    assert (got - want).abs().max().item() <= 3e-6 + 2e-6 * want.abs().max().item(), \
+        f"{tag}: centroids differ by {(got - want).abs().max().item():.3e}"
+    xf = x.float()
+    mse = lambda cb: ((xf.unsqueeze(1) - cb.unsqueeze(0)).abs().min(dim=1).values ** 2).mean().item()
+    assert abs(mse(got) - mse(want)) <= 1e-5 * mse(want), tag
