@@ -9,10 +9,10 @@ meet combinations the targeted tests do not list; the encoder likewise
 codebook, user id) against the oracle's codes, signs and norms.
 Adapters: fused and separate LoRA paths equal bit for bit and match the
 oracle; dense reference_attn cases within fp32 conditioning; GPU Lloyd-Max
-on drawn distributions against the oracle's recipe.  OMNI_RANDOM_CASES,
-OMNI_RANDOM_PAGED, OMNI_RANDOM_ENC, OMNI_RANDOM_LORA, OMNI_RANDOM_DENSE and
-OMNI_RANDOM_CALIB (default 14, 6, 10, 8, 8 and 6) draw longer sweeps from
-the same seed."""
+on drawn distributions against the oracle's recipe; dequantize and the
+row-seeded API.  OMNI_RANDOM_CASES, OMNI_RANDOM_PAGED, OMNI_RANDOM_ENC,
+OMNI_RANDOM_LORA, OMNI_RANDOM_DENSE, OMNI_RANDOM_CALIB and OMNI_RANDOM_DEQ
+(default 14, 6, 10, 8, 8, 6 and 6) draw longer sweeps from the same seed."""
 import math
 import os
 import random
@@ -20,7 +20,7 @@ import random
 import pytest
 import torch
 
-from oracle import restate
+from oracle import exact, restate
 from tests import _data
 from tests.test_gpu_attn import _assert_close, _cache, _causal_mask, _run
 
@@ -250,3 +250,41 @@ def test_random_calibration(device, dist, n, scale, dtype):
     xf = x.float()
     mse = lambda cb: ((xf.unsqueeze(1) - cb.unsqueeze(0)).abs().min(dim=1).values ** 2).mean().item()
     assert abs(mse(got) - mse(want)) <= 1e-5 * mse(want), tag
+
+
+_QCASES = []
+for _i in range(int(os.environ.get("OMNI_RANDOM_DEQ", "6"))):
+    _QCASES.append((_rng.choice([1, 2, 3]), _rng.choice([1, 2, 8]), _rng.choice([1, 5, 77, 300]),
+                    _rng.choice([128, 32]), _rng.random() < 0.7, _rng.random() < 0.3, _rng.randint(0, 3000),
+                    _rng.randint(0, 40)))
+
+
+@pytest.mark.parametrize("B,H,T,D,with_qjl,shared,uid,base", _QCASES)
+def test_random_dequantize_and_rows(device, B, H, T, D, with_qjl, shared, uid, base):
+    """dequantize_heads of arbitrary packed bytes (bit-exact against the
+    oracle), and the row-seeded API (quantize_rows / dequantize_rows with a
+    base head index) on rotated rows of the same shape."""
+    from omnistack_rs.kernels.quantize import dequantize_heads, dequantize_rows, quantize_rows
+    tag = f"B{B} H{H} T{T} D{D} qjl{int(with_qjl)} shared{int(shared)} uid{uid} base{base}"
+    print(f"[random dequant] {tag}", flush=True)
+    g = _data.gen(B * 100 + H * 10 + T + D)
+    nib = torch.randint(0, 256, (B, H, T, D // 2), generator=g, dtype=torch.uint8)
+    qjl = torch.randint(0, 256, (B, H, T, D // 16), generator=g, dtype=torch.uint8)
+    nrm = torch.rand(B, H, T, generator=g) * 3
+    cb = _data.gaussian_codebook(H) * torch.linspace(0.5, 2.0, H).reshape(H, 1)
+    if shared:
+        cb = cb[0].contiguous()
+    got = dequantize_heads(nib.to(device), qjl.to(device), nrm.to(device), cb.to(device), user_id=uid,
+                           with_qjl=with_qjl).cpu()
+    want = restate.dequantize_heads(nib, qjl, nrm, cb, user_id=uid, with_qjl=with_qjl)
+    assert torch.equal(got.view(torch.int32), want.view(torch.int32)), f"dequantize differs: {tag}"
+    # row-seeded API: every row its own seed (base + row index)
+    x = restate.wht(torch.randn(B, H, T, D, generator=g))
+    cb1 = (cb if shared else cb[0]).contiguous()
+    rn, rq, rr = quantize_rows(x.to(device), cb1.to(device), base_head_idx=base, user_id=uid)
+    wn, wq, wr = restate.quantize_rows(x, cb1, base_head_idx=base, user_id=uid)
+    assert torch.equal(rn.cpu(), wn) and torch.equal(rq.cpu(), wq), f"rows codes / signs differ: {tag}"
+    assert exact.ulp_distance_f32(rr.cpu().numpy(), wr.numpy()).max() <= 2, f"rows norms: {tag}"
+    out = dequantize_rows(rn, rq, rr, cb1.to(device), base_head_idx=base, user_id=uid).cpu()
+    ref = restate.dequantize_rows(rn.cpu(), rq.cpu(), rr.cpu(), cb1, base_head_idx=base, user_id=uid)
+    assert (out - ref).abs().max().item() < 1e-6, f"dequantize_rows: {tag}"
