@@ -64,28 +64,35 @@ for _i in range(int(os.environ.get("OMNI_RANDOM_PAGED", "6"))):
     B = _rng.choice([3, 9, 70])
     S = _rng.choice([40, 130, 300])
     ps = _rng.choice([16, 32, 64])
-    if (B, Hkv * G, Hkv, S, ps) not in _PCASES:
-        _PCASES.append((B, Hkv * G, Hkv, S, ps))
+    T = _rng.choice([1, 1, 3, 12])
+    causal = T > 1 and _rng.random() < 0.7
+    if (B, Hkv * G, Hkv, S, ps, T, causal) not in _PCASES:
+        _PCASES.append((B, Hkv * G, Hkv, S, ps, T, causal))
 
 
-@pytest.mark.parametrize("B,Hq,Hkv,S,ps", _PCASES)
-def test_random_paged_matches_oracle(device, B, Hq, Hkv, S, ps):
-    """Ragged lengths in random page order, one query token per sequence."""
+@pytest.mark.parametrize("B,Hq,Hkv,S,ps,T,causal", _PCASES)
+def test_random_paged_matches_oracle(device, B, Hq, Hkv, S, ps, T, causal):
+    """Ragged lengths in random page order; T query tokens per sequence
+    (more than 32 rows per kv head take the chunked-prefill kernel), causal
+    chunks aligned with the end of each sequence."""
     from omnistack_rs.cache import PagedKVCache, paged_attention
     uid = 32
+    print(f"[random paged] B{B} Hq{Hq} Hkv{Hkv} S{S} ps{ps} T{T} causal{int(causal)}", flush=True)
     kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=B * 77 + S, user_id=uid)
-    q = _data.query((B, Hq, 1, 128), seed=B + S)
+    q = _data.query((B, Hq, T, 128), seed=B + S + T)
     r = random.Random(B * 131 + S * 7 + ps)
-    lens = [r.randint(1, S) for _ in range(B)]
+    lens = [r.randint(T if causal else 1, S) for _ in range(B)]
     g = torch.Generator().manual_seed(B + ps)
     cache, pt, lt = PagedKVCache.from_contiguous(*(t.to(device) for t in (kn, kq, kr, vn)), page_size=ps,
                                                  seq_lens=lens, spare_pages=2, generator=g)
-    got = paged_attention(q.to(device), cache, pt, lt, cb.to(device), user_id=uid).cpu()
+    got = paged_attention(q.to(device), cache, pt, lt, cb.to(device), user_id=uid, causal=causal).cpu()
     for b, L in enumerate(lens):
         sl = slice(b, b + 1)
         want = restate.fused_attn_python(q[sl].float(), kn[sl, :, :L], kq[sl, :, :L], kr[sl, :, :L],
-                                         vn[sl, :, :L], cb, uid, 1 / math.sqrt(128), True)
-        _assert_close(got[sl], want, f"random paged B{B} Hq{Hq} Hkv{Hkv} ps{ps} b{b} len{L}")
+                                         vn[sl, :, :L], cb, uid, 1 / math.sqrt(128), True,
+                                         mask=_causal_mask(T, L, L - T) if causal else None)
+        _assert_close(got[sl], want, f"random paged B{B} Hq{Hq} Hkv{Hkv} ps{ps} T{T} causal{int(causal)} "
+                                     f"b{b} len{L}")
 
 
 _ECASES = []
