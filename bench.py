@@ -11,15 +11,17 @@ call with inputs resident in HBM (K back-to-back calls).  `roofline` uses the
 same K calls, timed by HIP events on the launch stream; `sustained` times
 2000 further back-to-back calls in 50-call blocks.
 
-Also reported (extra keys): C2 serving (B=64, S=50, 32q/8kv, 256-adapter
+Also reported (extra keys): C1 (the reference's synthetic server setup)
+through the module API; C2 serving (B=64, S=50, 32q/8kv, 256-adapter
 rank-8 LoRA gather on Q) p50/p99 latency and users/s; C4 encode GB/s
 (16 x 4096 x 8 kv heads, K and V, fused rotation), also straight into
 16-token pages, and one decode step's append; a plain streaming read of
 C3's byte count (the device's achievable read rate, for comparison with
 `value`); the reference's CPU path (the oracle restatement) timed on a
-bounded C3 sample on this host.
+bounded C3 sample on this host; and, after the timing, the outputs of the
+timed C1, C2, C3 and C5 calls against the oracle (`c*_parity`).
 
-    python bench.py [--gpus 1] [--steps 200] [--warmup 1000] [--only c3,c3paged,c2,c2pool,c4,c5,c5paged,c5d32,calib,dense] [--no-cpu]
+    python bench.py [--gpus 1] [--steps 200] [--warmup 1000] [--only c3,c3paged,c1,c2,c2pool,c4,c5,c5paged,c5d32,calib,dense] [--no-cpu]
 Prints one JSON line on stdout; progress goes to stderr.
 """
 from __future__ import annotations
@@ -98,6 +100,165 @@ def c3_inputs(dev):
     q = torch.randn(c["B"], c["Hq"], 1, c["D"], generator=torch.Generator(device=dev).manual_seed(43),
                     device=dev).to(torch.bfloat16)
     return kn, kq, kr, vn, cb, q, sign
+
+
+C2_SHAPE = dict(B=64, Hq=32, Hkv=8, S=50, D=128, uid=42, n_loras=256, rank=8, hidden=128)
+
+
+def lora_bank(dev, n_loras, rank, hidden, out_dim, B, seed=44, id_low=0, dtype=None):
+    """The configs' adapter bank: A (n_loras, rank, hidden) and B (n_loras,
+    out_dim, rank) ~ N(0, 0.02) from one device generator (seed 44), and
+    uniform adapter ids in [id_low, n_loras) from a CPU generator (seed 45).
+    Returns (A, B, ids, generator); the callers draw each user's x row and
+    query from the generator next."""
+    import torch
+    dtype = dtype or torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(seed)
+    la = (torch.randn(n_loras, rank, hidden, generator=g, device=dev) * 0.02).to(dtype)
+    lb = (torch.randn(n_loras, out_dim, rank, generator=g, device=dev) * 0.02).to(dtype)
+    ids = torch.randint(id_low, n_loras, (B,), generator=torch.Generator().manual_seed(45), dtype=torch.int32).to(dev)
+    return la, lb, ids, g
+
+
+def c2_inputs(dev):
+    """The C2 serving step's inputs: a 64-user x 8 kv head x 50-token cache
+    encoded with the configs' rotation, the 256 x rank-8 bank on q (hidden
+    128), one x row and one bf16 query (32 heads) per user.  Returns a dict;
+    `g` is the device generator, positioned after the query draw."""
+    import torch
+    c = C2_SHAPE
+    cb, sign = c3_codebook_and_sign(dev)
+    kn, kq, kr, vn = make_cache(c["B"], c["Hkv"], c["S"], c["D"], dev, 52, c["uid"], cb, sign)
+    la, lb, ids, g = lora_bank(dev, c["n_loras"], c["rank"], c["hidden"], c["Hq"] * c["D"], c["B"])
+    x = torch.randn(c["B"], 1, c["hidden"], generator=g, device=dev).to(torch.bfloat16)
+    q = torch.randn(c["B"], c["Hq"], 1, c["D"], generator=g, device=dev).to(torch.bfloat16)
+    return dict(kn=kn, kq=kq, kr=kr, vn=vn, cb=cb, sign=sign, la=la, lb=lb, ids=ids, x=x, q=q, g=g)
+
+
+def c2_oracle(inp, b):
+    """Oracle output of user b of the C2 step: the reference's
+    _apply_lora_to_q (q's dtype), then rotate_queries with the configs' sign
+    flip, then _fused_attn_python in fp32 (oracle/ restatement)."""
+    from oracle import restate
+    sl = slice(b, b + 1)
+    h = {k: inp[k][sl].cpu() for k in ("kn", "kq", "kr", "vn", "x", "q", "ids")}
+    q_eff = restate.apply_lora_to_q(h["q"], h["x"], inp["la"].cpu(), inp["lb"].cpu(), h["ids"], 1.0)
+    qr = restate.rotate(q_eff, inp["sign"].cpu()).float()
+    return restate.fused_attn_python(qr, h["kn"], h["kq"], h["kr"], h["vn"], inp["cb"].cpu(), C2_SHAPE["uid"],
+                                     1 / math.sqrt(C2_SHAPE["D"]), True)
+
+
+C1_SHAPE = dict(B=64, Hq=8, Hkv=8, S=50, D=128, uid=42, n_loras=256, rank=8, hidden=128)
+
+
+def c1_inputs(dev):
+    """C1, the reference's own synthetic server setup: 64 users x 8 heads
+    (MHA) x 50 tokens of bf16 N(0,1) K / V with the 2 % outlier channels,
+    raw (not yet rotated or encoded), the configs' codebook and sign flip,
+    the 256 x rank-8 bank on q (hidden 128), one x row and one bf16 query per
+    user and head."""
+    import torch
+    c = C1_SHAPE
+    cb, sign = c3_codebook_and_sign(dev)
+    g = torch.Generator(device=dev).manual_seed(51)
+    ch = torch.randperm(c["D"], generator=torch.Generator().manual_seed(51))[:3].to(dev)
+    kv = []
+    for _ in range(2):
+        t = torch.randn(c["B"], c["Hkv"], c["S"], c["D"], generator=g, device=dev)
+        t[..., ch] *= 8.0
+        kv.append(t.to(torch.bfloat16))
+    la, lb, ids, g2 = lora_bank(dev, c["n_loras"], c["rank"], c["hidden"], c["Hq"] * c["D"], c["B"])
+    x = torch.randn(c["B"], 1, c["hidden"], generator=g2, device=dev).to(torch.bfloat16)
+    q = torch.randn(c["B"], c["Hq"], 1, c["D"], generator=g2, device=dev).to(torch.bfloat16)
+    return dict(k=kv[0], v=kv[1], cb=cb, sign=sign, la=la, lb=lb, ids=ids, x=x, q=q)
+
+
+def c1_round_trip(inp):
+    """C1 through the reference's module API on the device: rotate K and V
+    (sign-flipped WHT), quantize_heads, then omni_attn with the LoRA bank and
+    the query rotated in-kernel.  Returns ((kn, kq, kr), (vn, vq, vr), out)."""
+    from omnistack_rs.kernels.fused_attention import omni_attn
+    from omnistack_rs.kernels.hadamard import rotate
+    from omnistack_rs.kernels.quantize import quantize_heads
+    c = C1_SHAPE
+    kr_, vr_ = rotate(inp["k"], inp["sign"]), rotate(inp["v"], inp["sign"])
+    kp = quantize_heads(kr_, inp["cb"], user_id=c["uid"])
+    vp = quantize_heads(vr_, inp["cb"], user_id=c["uid"])
+    out = omni_attn(inp["q"], kp[0], kp[1], kp[2], vp[0], inp["cb"], user_id=c["uid"], x=inp["x"],
+                    lora_a=inp["la"], lora_b=inp["lb"], lora_indices=inp["ids"], lora_alpha=1.0,
+                    rotate_q=True, sign_flip=inp["sign"])
+    return kp, vp, out
+
+
+C5_SHAPE = dict(B=8, Hq=32, Hkv=8, T=512, S=16384, uid=42)
+
+
+def c5_inputs(dev, head_dim=128):
+    """C5: 8 sequences x 8 kv heads x 16384 cached tokens and a 512-token
+    bf16 query chunk (32 heads) at the end of the cache (query t sees keys
+    0 .. 15872 + t).  head_dim 128: the configs' recipe with the sign-flipped
+    rotation; head_dim 32: the same recipe projected by the seeded
+    orthonormal 128 x 32 matrix, queries likewise.  Returns (kn, kq, kr, vn,
+    cb, q, causal_offset)."""
+    import torch
+    c = C5_SHAPE
+    cb, sign = c3_codebook_and_sign(dev)
+    off = c["S"] - c["T"]
+    if head_dim == 128:
+        kn, kq, kr, vn = make_cache(c["B"], c["Hkv"], c["S"], 128, dev, 55, c["uid"], cb, sign)
+        q = torch.randn(c["B"], c["Hq"], c["T"], 128, generator=torch.Generator(device=dev).manual_seed(56),
+                        device=dev).to(torch.bfloat16)
+    else:
+        P = ortho_proj()
+        kn, kq, kr, vn = make_cache32(c["B"], c["Hkv"], c["S"], dev, 57, c["uid"], cb, P)
+        q = torch.randn(c["B"], c["Hq"], c["T"], 128, generator=torch.Generator(device=dev).manual_seed(58), device=dev)
+        q = (q.to(torch.bfloat16).float() @ P.to(dev)).to(torch.bfloat16)
+    return kn, kq, kr, vn, cb, q, off
+
+
+def causal_mask(T, S, off):
+    """Additive (1, 1, T, S) mask: query t sees keys 0 .. off + t (the
+    chunked-prefill convention, applied as reference.py:149-150 applies a
+    mask)."""
+    import torch
+    mask = torch.zeros(1, 1, T, S)
+    cols = torch.arange(S).unsqueeze(0)
+    mask[0, 0][cols > (off + torch.arange(T)).unsqueeze(1)] = float("-inf")
+    return mask
+
+
+def oracle_parity(gpu_out, want_fn, seqs, note):
+    """Max / mean absolute difference of `gpu_out` (B, ...) against the
+    oracle's output for each sequence b in `seqs` (want_fn(b) -> the (1, ...)
+    oracle tensor), with the north-star bar."""
+    gh = gpu_out.cpu().double()
+    mx, sm, n = 0.0, 0.0, 0
+    for b in seqs:
+        d = (gh[b:b + 1] - want_fn(b).double()).abs()
+        mx = max(mx, d.max().item())
+        sm += d.sum().item()
+        n += d.numel()
+    return {"max_abs": mx, "mean_abs": sm / n, "bar_max_abs": 2e-3, "bar_mean_abs": 2e-4,
+            "within_bar": mx <= 2e-3 and sm / n <= 2e-4, "sequences": len(seqs), "note": note}
+
+
+def c5_parity(gpu_out, cache, cb, q, off, head_dim):
+    """C5 output of the timed calls vs the masked oracle (reference CPU path
+    restated: _fused_attn_python with the additive causal mask), every
+    sequence, one at a time."""
+    from oracle import restate
+    c = C5_SHAPE
+    host = [t.cpu() for t in cache]
+    qh, cbh = q.cpu(), cb.cpu()
+    mask = causal_mask(c["T"], c["S"], off)
+
+    def want(b):
+        sl = slice(b, b + 1)
+        return restate.fused_attn_python(qh[sl].float(), *(t[sl] for t in host), cbh, c["uid"],
+                                         1 / math.sqrt(head_dim), True, mask=mask)
+    return oracle_parity(gpu_out, want, range(c["B"]),
+                         f"output of the timed C5 calls (head_dim {head_dim}) vs the masked oracle "
+                         "(_fused_attn_python restated, fp32, causal additive mask), all 8 sequences")
 
 
 def ortho_proj(D_in=128, D_out=32, seed=13):
@@ -314,11 +475,11 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="C3 (and the CPU baseline) only")
     ap.add_argument("--only", default="",
-                    help="comma-separated sections to run (c3, c3paged, c2, c2pool, c4, c5, c5paged, c5d32, calib, dense), for profiling one "
+                    help="comma-separated sections to run (c3, c3paged, c1, c2, c2pool, c4, c5, c5paged, c5d32, calib, dense), for profiling one "
                          "configuration; the JSON line then carries only those sections")
     args = ap.parse_args()
     sections = set(args.only.split(",")) if args.only else (
-        {"c3"} if args.no_extras else {"c3", "c3paged", "c2", "c2pool", "c4", "c5", "c5paged", "c5d32", "calib", "dense"})
+        {"c3"} if args.no_extras else {"c3", "c3paged", "c1", "c2", "c2pool", "c4", "c5", "c5paged", "c5d32", "calib", "dense"})
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -471,20 +632,17 @@ def main() -> int:
 
     # ── extras: C2 serving, C4 encode, C5 prefill ────────────────────────
     if "c2" in sections:
-        B2, S2, L2, R2, HID = 64, 50, 256, 8, 128
+        B2, S2 = C2_SHAPE["B"], C2_SHAPE["S"]
         log("[bench] C2: serving B=64 S=50 with 256 x rank-8 LoRA")
-        kn2, kq2, kr2, vn2 = make_cache(B2, Hkv, S2, D, dev, 52, uid, cb, sign)
-        g2 = torch.Generator(device=dev).manual_seed(44)
-        la = (torch.randn(L2, R2, HID, generator=g2, device=dev) * 0.02).to(torch.bfloat16)
-        lb = (torch.randn(L2, Hq * D, R2, generator=g2, device=dev) * 0.02).to(torch.bfloat16)
-        ids = torch.randint(0, L2, (B2,), generator=torch.Generator().manual_seed(45), dtype=torch.int32).to(dev)
-        xh = torch.randn(B2, 1, HID, generator=g2, device=dev).to(torch.bfloat16)
-        q2 = torch.randn(B2, Hq, 1, D, generator=g2, device=dev).to(torch.bfloat16)
+        inp2 = c2_inputs(dev)
+        kn2, kq2, kr2, vn2 = inp2["kn"], inp2["kq"], inp2["kr"], inp2["vn"]
+        la, lb, ids, xh, q2, g2 = inp2["la"], inp2["lb"], inp2["ids"], inp2["x"], inp2["q"], inp2["g"]
         att2 = PackedKVAttention(kn2, kq2, kr2, vn2, cb, n_heads=Hq, user_id=uid, rotate_q=True, sign_flip=sign,
                                  lora_a=la, lora_b=lb, lora_alpha=1.0)
         serve = lambda: att2.run(q2, xh, ids)
         steps2 = max(args.steps, 100)
         per2 = per_call_events(serve, steps2, args.warmup, stream)
+        c2_out = att2.out.clone()
         t2 = wall_graph(serve, steps2, args.warmup)
         per2s = sorted(per2)
         p50, p99 = per2s[len(per2s) // 2], per2s[min(len(per2s) - 1, int(0.99 * len(per2s)))]
@@ -496,6 +654,13 @@ def main() -> int:
                                         "p50/p99 from HIP events per eager call, users/s from a HIP graph of steps"}
         log(f"[bench] C2: p50 {p50 * 1e6:.1f} us p99 {p99 * 1e6:.1f} us (events), "
             f"{t2 * 1e6:.1f} us/step graph -> {B2 / t2:.0f} users/s")
+        if not args.no_cpu:
+            result["c2_parity"] = oracle_parity(
+                c2_out, lambda b: c2_oracle(inp2, b), range(B2),
+                "output of the timed C2 calls (fused LoRA, rotate_q) vs the oracle (_apply_lora_to_q -> "
+                "rotate_queries -> _fused_attn_python restated, fp32), all 64 users")
+            log(f"[bench] C2 parity vs oracle: max-abs {result['c2_parity']['max_abs']:.3e} "
+                f"mean-abs {result['c2_parity']['mean_abs']:.3e}")
         # the whole decode step over a paged cache: each user's new K / V
         # token encoded into its page, then the same attention over the pages
         from omnistack_rs.cache import PagedKVAttention, PagedKVCache
@@ -528,10 +693,7 @@ def main() -> int:
         NP, B2, S2, L2, R2, HID = 256, 64, 50, 256, 8, 128
         log("[bench] C2 pool: 64 of 256 cached users per step, 256 x rank-8 LoRA")
         knp, kqp, krp, vnp = make_cache(NP, Hkv, S2, D, dev, 53, uid, cb, sign)
-        g2 = torch.Generator(device=dev).manual_seed(44)
-        la = (torch.randn(L2, R2, HID, generator=g2, device=dev) * 0.02).to(torch.bfloat16)
-        lb = (torch.randn(L2, Hq * D, R2, generator=g2, device=dev) * 0.02).to(torch.bfloat16)
-        ids = torch.randint(-1, L2, (B2,), generator=torch.Generator().manual_seed(45), dtype=torch.int32).to(dev)
+        la, lb, ids, g2 = lora_bank(dev, L2, R2, HID, Hq * D, B2, id_low=-1)
         users = torch.randint(0, NP, (B2,), generator=torch.Generator().manual_seed(46)).to(dev)
         xh = torch.randn(B2, 1, HID, generator=g2, device=dev).to(torch.bfloat16)
         q2 = torch.randn(B2, Hq, 1, D, generator=g2, device=dev).to(torch.bfloat16)
@@ -549,12 +711,58 @@ def main() -> int:
         log(f"[bench] C2 pool: p50 {p50 * 1e6:.1f} us p99 {p99 * 1e6:.1f} us (events), "
             f"{t2 * 1e6:.1f} us/step graph -> {B2 / t2:.0f} users/s")
 
+    if "c1" in sections:
+        # the reference's own synthetic server setup through its module API:
+        # rotate + quantize_heads for K and V, then omni_attn with the LoRA bank
+        c1 = C1_SHAPE
+        log("[bench] C1: 64 users x 8 heads x 50 tokens round trip (rotate, quantize_heads, omni_attn + LoRA)")
+        inp1 = c1_inputs(dev)
+        kp1, vp1, out1 = c1_round_trip(inp1)
+        t1rt = wall_eager(lambda: c1_round_trip(inp1), max(20, args.steps // 5), 5)
+        from omnistack_rs.kernels.fused_attention import omni_attn
+        att1 = lambda: omni_attn(inp1["q"], kp1[0], kp1[1], kp1[2], vp1[0], inp1["cb"], user_id=c1["uid"],
+                                 x=inp1["x"], lora_a=inp1["la"], lora_b=inp1["lb"], lora_indices=inp1["ids"],
+                                 lora_alpha=1.0, rotate_q=True, sign_flip=inp1["sign"])
+        t1a = wall_eager(att1, max(50, args.steps), 5)
+        result["c1_round_trip"] = {"us_per_round_trip": round(t1rt * 1e6, 1), "us_per_attention_call": round(t1a * 1e6, 2),
+                                   "users_per_s_attention": round(c1["B"] / t1a, 1),
+                                   "note": "C1 through the module API (each call validates and allocates its "
+                                           "outputs): rotate + quantize_heads of K and V, then omni_attn with "
+                                           "LoRA and rotate_q; wall time per eager call"}
+        log(f"[bench] C1: round trip {t1rt * 1e6:.0f} us, attention call {t1a * 1e6:.1f} us")
+        if not args.no_cpu:
+            from oracle import restate
+            sg, cbh = inp1["sign"].cpu(), inp1["cb"].cpu()
+            okp = restate.quantize_heads(restate.rotate(inp1["k"].cpu(), sg), cbh, user_id=c1["uid"])
+            ovp = restate.quantize_heads(restate.rotate(inp1["v"].cpu(), sg), cbh, user_id=c1["uid"])
+            q_eff = restate.apply_lora_to_q(inp1["q"].cpu(), inp1["x"].cpu(), inp1["la"].cpu(), inp1["lb"].cpu(),
+                                            inp1["ids"].cpu(), 1.0)
+            want1 = restate.fused_attn_python(restate.rotate(q_eff, sg).float(), *okp, ovp[0], cbh, c1["uid"],
+                                              1 / math.sqrt(D), True)
+            par = oracle_parity(out1, lambda b: want1[b:b + 1], range(c1["B"]),
+                                "C1 attention (device-encoded cache, LoRA, rotate_q) vs the oracle's own "
+                                "encode + _apply_lora_to_q + rotate_queries + _fused_attn_python, fp32")
+            par["nibbles_equal"] = bool(torch.equal(kp1[0].cpu(), okp[0]) and torch.equal(vp1[0].cpu(), ovp[0]))
+            par["sign_bytes_equal_fp32_oracle"] = bool(torch.equal(kp1[1].cpu(), okp[1]))
+            result["c1_parity"] = par
+            log(f"[bench] C1 parity: nibbles equal {par['nibbles_equal']}, attention max-abs {par['max_abs']:.3e} "
+                f"mean-abs {par['mean_abs']:.3e}")
+        del inp1, kp1, vp1, out1
+
     if "c4" in sections:
         B4, T4 = 16, 4096
         log("[bench] C4: encode 16 x 4096 x 8 K and V")
+        # bf16 N(0,1) with the 2 % outlier channels (x8), as the config states
         g4 = torch.Generator(device=dev).manual_seed(46)
-        k4 = torch.randn(B4, Hkv, T4, D, generator=g4, device=dev).to(torch.bfloat16)
-        v4 = torch.randn(B4, Hkv, T4, D, generator=g4, device=dev).to(torch.bfloat16)
+        ch4 = torch.randperm(D, generator=torch.Generator().manual_seed(46))[: max(1, round(0.02 * D))].to(dev)
+        kv4 = []
+        for _ in range(2):
+            t = torch.randn(B4, Hkv, T4, D, generator=g4, device=dev)
+            t[..., ch4] *= 8.0
+            kv4.append(t.to(torch.bfloat16))
+            del t
+        k4, v4 = kv4
+        del kv4
         enc = lambda: (encode_kv(k4, cb, user_id=uid, sign_flip=sign), encode_kv(v4, cb, user_id=uid, sign_flip=sign))
         t4 = wall_eager(enc, max(5, args.steps // 5), 2)
         rows = 2 * B4 * Hkv * T4
@@ -621,20 +829,26 @@ def main() -> int:
     B5, T5, S5 = 8, 512, 16384
     off5 = S5 - T5
     keys = T5 * off5 + T5 * (T5 + 1) // 2            # visible (query, key) pairs per (b, q head)
+    # C5 legs: at least 10 timed calls after at least 3 warm-up calls, whatever --steps is
+    steps5, warm5 = max(10, args.steps // 10), 3
     if "c5" in sections:
         log("[bench] C5: prefill 8 x 512 queries over 8 x 16384 cached tokens (causal)")
-        kn5, kq5, kr5, vn5 = make_cache(B5, Hkv, S5, D, dev, 55, uid, cb, sign)
-        q5 = torch.randn(B5, Hq, T5, D, generator=torch.Generator(device=dev).manual_seed(56), device=dev).to(torch.bfloat16)
+        kn5, kq5, kr5, vn5, _, q5, _ = c5_inputs(dev, 128)
         att5 = PackedKVAttention(kn5, kq5, kr5, vn5, cb, n_heads=Hq, q_tokens=T5, user_id=uid, causal_offset=off5)
-        t5 = wall_eager(lambda: att5.run(q5), max(3, args.steps // 10), 1)
+        t5 = wall_eager(lambda: att5.run(q5), steps5, warm5)
+        c5_out = att5.out.clone()
         fl_qkpv = 2 * 2 * B5 * Hq * keys * D             # Q.K and P.V
         fl_qjl = 2 * B5 * Hq * keys * (D // 2)           # signs . (G q) score correction
         tf5 = (fl_qkpv + fl_qjl) / t5 / 1e12
         result["prefill_c5"] = {"us_per_call": round(t5 * 1e6, 1), "TFLOP_s": round(tf5, 2),
-                                "flops_per_call": fl_qkpv + fl_qjl,
+                                "flops_per_call": fl_qkpv + fl_qjl, "calls": steps5, "warmup": warm5,
                                 "frac_of_fp16_dense_peak": round(tf5 / 2500.0, 4),
                                 "note": "useful flops (QK, PV, QJL correction) over the causally visible keys"}
         log(f"[bench] C5: {t5 * 1e6:.0f} us -> {tf5:.1f} TFLOP/s ({tf5 / 2500:.1%} of fp16 dense MFMA peak)")
+        if not args.no_cpu:
+            result["c5_parity"] = c5_parity(c5_out, (kn5, kq5, kr5, vn5), cb, q5, off5, 128)
+            log(f"[bench] C5 parity vs oracle: max-abs {result['c5_parity']['max_abs']:.3e} "
+                f"mean-abs {result['c5_parity']['mean_abs']:.3e}")
         if "c5paged" in sections:
             # the same chunk over the same tokens in 16-token pages (random
             # pool order); the prefill kernel has a static tile order, so the
@@ -649,7 +863,10 @@ def main() -> int:
             # contiguous and paged calls alternate, so drifting clocks (this
             # workload heats the chip) affect both the same way
             t5c, t5p = [], []
-            for _ in range(max(3, args.steps // 10)):
+            for _ in range(warm5):
+                att5.run(q5)
+                att5p.run(q5, pt5, lens5)
+            for _ in range(steps5):
                 t5c.append(wall_eager(lambda: att5.run(q5), 1, 0))
                 t5p.append(wall_eager(lambda: att5p.run(q5, pt5, lens5), 1, 0))
             t5c, t5p = statistics.median(t5c), statistics.median(t5p)
@@ -670,20 +887,23 @@ def main() -> int:
         # C5 at head_dim 32 (the generalized codec: 16 B nibbles, 2 B signs)
         D32 = 32
         log("[bench] C5 (head_dim 32): prefill 8 x 512 queries over 8 x 16384 cached tokens (causal)")
-        P32 = ortho_proj()
-        kn6, kq6, kr6, vn6 = make_cache32(B5, Hkv, S5, dev, 57, uid, cb, P32)
-        q6 = torch.randn(B5, Hq, T5, 128, generator=torch.Generator(device=dev).manual_seed(58), device=dev)
-        q6 = (q6.to(torch.bfloat16).float() @ P32.to(dev)).to(torch.bfloat16)
+        kn6, kq6, kr6, vn6, _, q6, _ = c5_inputs(dev, D32)
         att6 = PackedKVAttention(kn6, kq6, kr6, vn6, cb, n_heads=Hq, q_tokens=T5, user_id=uid, causal_offset=off5)
-        t6 = wall_eager(lambda: att6.run(q6), max(3, args.steps // 10), 1)
+        t6 = wall_eager(lambda: att6.run(q6), steps5, warm5)
+        c6_out = att6.out.clone()
         fl6 = 2 * 2 * B5 * Hq * keys * D32 + 2 * B5 * Hq * keys * (D32 // 2)
         tf6 = fl6 / t6 / 1e12
         result["prefill_c5_d32"] = {"us_per_call": round(t6 * 1e6, 1), "TFLOP_s": round(tf6, 2), "flops_per_call": fl6,
+                                    "calls": steps5, "warmup": warm5,
                                     "frac_of_fp16_dense_peak": round(tf6 / 2500.0, 4),
                                     "note": "head_dim 32 variant of C5: K/V and q of the 128-dim recipe projected "
                                             "by a seeded orthonormal 128 x 32 matrix (QR, seed 13); no reference "
                                             "implementation at D=32"}
         log(f"[bench] C5 (head_dim 32): {t6 * 1e6:.0f} us -> {tf6:.1f} TFLOP/s")
+        if not args.no_cpu:
+            result["c5_d32_parity"] = c5_parity(c6_out, (kn6, kq6, kr6, vn6), cb, q6, off5, D32)
+            log(f"[bench] C5 (head_dim 32) parity vs oracle: max-abs {result['c5_d32_parity']['max_abs']:.3e} "
+                f"mean-abs {result['c5_d32_parity']['mean_abs']:.3e}")
         del kn6, kq6, kr6, vn6, att6
 
     # ── CPU baseline (reference CPU path restated in oracle/) ────────────

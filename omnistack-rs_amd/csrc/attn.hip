@@ -1880,6 +1880,7 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
     const int64_t coff = PAGED ? seq_len - a.T : a.causal_offset;
     const int s_begin = split * (int)a.split_len;
     int s_end = (int)imin64(seq_len, (int64_t)s_begin + a.split_len);
+    const int s_full = imax(s_end, s_begin);     // the split's keys before the causal trim
     int lim[NCB];
     bool rowok[NCB];
 #pragma unroll
@@ -2114,6 +2115,18 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
 #pragma unroll
     for (int p = 0; p < PF - 1; ++p)
         if (tt0 + p * stride < s_end) tile_step(ring[p], tt0 + p * stride);
+    if constexpr (PAGED) {
+        // pages of the split past this wave's causal window were never
+        // loaded: a page id outside the pool there still makes every row of
+        // the sequence NaN (as the decode kernel, which reads every page)
+        if (causal && s_full > s_end) {
+            const int p_hi = ((s_full - 1) >> a.page_shift) + 1;      // <= max_pages: seq_len <= S
+            bool bad = false;
+            for (int p = (s_end >> a.page_shift) + lane; p < p_hi; p += 64)
+                bad = bad || (uint32_t)pt_row[p] >= (uint32_t)a.n_pages;
+            page_bad = page_bad || __builtin_amdgcn_ballot_w64(bad) != 0;
+        }
+    }
 
     // ── rows out (or split partials) ──────────────────────────────────────
     const int64_t unit = (b * a.Hkv + hk) * a.n_rchunks + rc;

@@ -30,8 +30,6 @@ void set_error(const char *fmt, ...);
 
 static inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
 
-// fp32 1/sqrt(D) exactly as torch forms `x * (1.0 / math.sqrt(D))` on an fp32
-// tensor: the Python double is rounded to fp32 before the multiply.
 // Compute units of the current device, queried once per device (a full
 // property query costs far more than a launch; 256 if it fails).
 static inline int device_cus() {
@@ -46,6 +44,8 @@ static inline int device_cus() {
     return cached[dev];
 }
 
+// fp32 1/sqrt(D) exactly as torch forms `x * (1.0 / math.sqrt(D))` on an fp32
+// tensor: the Python double is rounded to fp32 before the multiply.
 static inline float inv_sqrt_dim_f32(int D) { return (float)(1.0 / __builtin_sqrt((double)D)); }
 
 // ── element conversions (round-to-nearest-even, like torch) ─────────────

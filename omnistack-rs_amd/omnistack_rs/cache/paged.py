@@ -274,6 +274,35 @@ def paged_attention(q: torch.Tensor, cache: PagedKVCache, page_table: torch.Tens
     return out
 
 
+def _check_paged_run(q, page_table, seq_lens, x, lora_indices, shape, q_dtype, max_pages, lora_hidden, lora_dtype,
+                     dev) -> None:
+    """Host-only checks of PagedKVAttention.run's arguments (no device work,
+    safe under graph capture): every tensor contiguous, on `dev`, with the
+    shape and dtype the kernel reads it with; `lora_hidden` / `lora_dtype`
+    are None without a LoRA bank."""
+    B, Hq, T, D = shape
+    if tuple(q.shape) != shape or q.dtype != q_dtype or not q.is_contiguous():
+        raise ValueError(f"q must be a contiguous {q_dtype} tensor of shape {shape}")
+    if tuple(page_table.shape) != (B, max_pages) or page_table.dtype != torch.int32 or \
+            not page_table.is_contiguous():
+        raise ValueError(f"page_table must be a contiguous int32 tensor of shape {(B, max_pages)}")
+    if seq_lens.dtype != torch.int32 or seq_lens.numel() != B or not seq_lens.is_contiguous():
+        raise ValueError(f"seq_lens must be a contiguous int32 tensor of {B} entries")
+    for t in (q, page_table, seq_lens, x, lora_indices):
+        if t is not None and t.device != dev:
+            raise ValueError(f"q, page_table, seq_lens, x and lora_indices must be on {dev}")
+    if lora_hidden is None:
+        if x is not None or lora_indices is not None:
+            raise ValueError("run(..., x, lora_indices) needs a LoRA bank at construction")
+        return
+    if x is None or lora_indices is None:
+        raise ValueError("this attention has a LoRA bank: pass x and lora_indices")
+    if tuple(x.shape) != (B, T, lora_hidden) or x.dtype != lora_dtype or not x.is_contiguous():
+        raise ValueError(f"x must be a contiguous {lora_dtype} tensor of shape {(B, T, lora_hidden)}")
+    if lora_indices.dtype != torch.int32 or lora_indices.numel() != B or not lora_indices.is_contiguous():
+        raise ValueError(f"lora_indices must be a contiguous int32 tensor of {B} entries")
+
+
 class PagedKVAttention:
     """Prepared ``paged_attention`` over one page pool (serving loops).
 
@@ -286,7 +315,10 @@ class PagedKVAttention:
     sequence with a page id outside the pool or a bad length gives NaN rows.
     With a LoRA bank (``lora_a``, ``lora_b``, ``lora_alpha``),
     ``run(q, page_table, seq_lens, x, lora_indices)`` applies the per-user
-    update of q inside the same call.
+    update of q inside the same call.  ``run`` takes its tensors as they are
+    (contiguous, on the pool's device, q in ``q_dtype``, x in the bank's
+    dtype, int32 tables, lengths and indices) and raises ValueError
+    otherwise; it makes no copies.
     """
 
     def __init__(self, cache: PagedKVCache, codebooks: torch.Tensor, n_heads: int, batch: int, max_pages: int,
@@ -302,9 +334,13 @@ class PagedKVAttention:
             raise ValueError(f"q_dtype must be one of {list(_lib.DTYPE_CODE)}")
         _check_packed(cache.k_nibbles, cache.k_qjl if with_qjl else None, cache.k_norms if with_qjl else None,
                       "cache.k_nibbles")
-        dev = cache.device
+        dev = _lib.require_device(cache.k_nibbles, cache.v_nibbles)
         self.cache, self.B, self.Hq, self.T, self.max_pages = cache, int(batch), int(n_heads), int(q_tokens), int(max_pages)
+        if self.B < 0 or self.T < 1 or self.max_pages < 1:
+            raise ValueError("batch must be >= 0, q_tokens and max_pages >= 1")
         self.cb, self.per_head = _prep_codebooks(codebooks, H, dev)
+        if not bool((self.cb.abs() <= 65504.0).all()):
+            raise ValueError("codebook centroids must lie within fp16 range (|c| <= 65504)")
         self.gb = _lib.g_bits(_lib.head_seeds(user_id, H), D, dev) if with_qjl else None
         self.sf = _lib.sign_flip_i8(sign_flip, D, dev) if (rotate_q and sign_flip is not None) else None
         self.scale = float(1.0 / math.sqrt(D) if scale is None else scale)
@@ -312,8 +348,14 @@ class PagedKVAttention:
         self.qcode = _lib.dtype_code(q_dtype)
         self.q_dtype = q_dtype
         self.lora = None
+        if (lora_a is None) != (lora_b is None):
+            raise ValueError("lora_a and lora_b must be given together")
         if lora_a is not None:
+            if lora_a.dim() != 3:
+                raise ValueError(f"lora_a must be (n_loras, rank, hidden), got {tuple(lora_a.shape)}")
             n_loras, rank, hidden = lora_a.shape
+            if tuple(lora_b.shape) != (n_loras, n_heads * D, rank):
+                raise ValueError(f"lora_b must be ({n_loras}, {n_heads * D}, {rank}), got {tuple(lora_b.shape)}")
             wdt = torch.promote_types(lora_a.dtype, lora_b.dtype)
             if wdt not in _lib.DTYPE_CODE:
                 wdt = torch.float32
@@ -328,27 +370,18 @@ class PagedKVAttention:
     def run(self, q: torch.Tensor, page_table: torch.Tensor, seq_lens: torch.Tensor,
             x: Optional[torch.Tensor] = None, lora_indices: Optional[torch.Tensor] = None) -> torch.Tensor:
         c = self.cache
-        if tuple(q.shape) != (self.B, self.Hq, self.T, c.head_dim) or q.dtype != self.q_dtype:
-            raise ValueError(f"q must be {self.q_dtype} {(self.B, self.Hq, self.T, c.head_dim)}")
-        if tuple(page_table.shape) != (self.B, self.max_pages) or page_table.dtype != torch.int32:
-            raise ValueError(f"page_table must be int32 {(self.B, self.max_pages)}")
-        if seq_lens.dtype != torch.int32 or seq_lens.numel() != self.B:
-            raise ValueError(f"seq_lens must be int32 with {self.B} entries")
         dev = c.device
-        for t in (q, page_table, seq_lens, x, lora_indices):
-            if t is not None and t.device != dev:
-                raise ValueError(f"q, page_table, seq_lens, x and lora_indices must be on {dev}")
+        _check_paged_run(q, page_table, seq_lens, x, lora_indices, (self.B, self.Hq, self.T, c.head_dim),
+                         self.q_dtype, self.max_pages, self.lora[4] if self.lora is not None else None,
+                         self.lora[3] if self.lora is not None else None, dev)
         if self.lora is not None:
-            if x is None or lora_indices is None:
-                raise ValueError("this attention has a LoRA bank: pass x and lora_indices")
             la, lb, wcode, wdt, hidden, rank, n_loras, alpha = self.lora
-            xc = x if x.dtype == wdt else x.to(wdt)
-            lora = (_lib.ptr(xc.contiguous()), _lib.ptr(la), _lib.ptr(lb), wcode, _lib.ptr(lora_indices),
+            lora = (_lib.ptr(x), _lib.ptr(la), _lib.ptr(lb), wcode, _lib.ptr(lora_indices),
                     hidden, rank, n_loras, alpha)
         else:
             lora = (None, None, None, 0, None, 0, 0, 0, 0.0)
         _lib.check(_lib.lib().omni_attn_paged(
-            _lib.ptr(q.contiguous()), self.qcode, _lib.ptr(c.k_nibbles), _lib.ptr(c.k_qjl if self.with_qjl else None),
+            _lib.ptr(q), self.qcode, _lib.ptr(c.k_nibbles), _lib.ptr(c.k_qjl if self.with_qjl else None),
             _lib.ptr(c.k_norms if self.with_qjl else None), _lib.ptr(c.v_nibbles), c.n_pages, c.page_size,
             _lib.ptr(page_table), self.max_pages, _lib.ptr(seq_lens), *lora,
             _lib.ptr(self.cb), self.per_head, _lib.ptr(self.gb), self.B, self.Hq, c.n_kv_heads, self.T,

@@ -29,6 +29,16 @@ PINS = {
                    "tests/unit/test_hadamard.py:166-188), equality with the "
                    "scipy Sylvester Hadamard matrix / sqrt(128) in fp64, "
                    "self-inverse, norm preservation",
+    "restate.rotate": "tests/test_oracle_pins.py::test_rotate_sign_flip_matches_"
+                      "hadamard_times_flip: equals scipy's Sylvester H / sqrt(D) @ "
+                      "(s * x) in fp64 at D = 128 and 32 (a flip after the transform, "
+                      "or none, misses by O(1)); bf16 inputs rounded once",
+    "restate.make_g_matrix": "tests/test_oracle_pins.py::test_make_g_matrix_is_one_"
+                             "mt19937_stream_packed_lsb_first: every lo / hi word "
+                             "equals textbook MT19937 low bits in (head, row, "
+                             "column) order packed with Python integers; it is the "
+                             "checker of the product's make_g_matrix "
+                             "(tests/test_native_lib.py)",
     "restate.qjl_g": "tests/test_oracle_pins.py: bits equal textbook MT19937 "
                      "low bits (C, mt19937_ref.c); MT19937 itself pinned by "
                      "the C++ [rand.predef] value (10000th draw of seed 5489 "
@@ -57,6 +67,30 @@ PINS = {
                          "bin means (math.fsum, n % 16 largest left out); the "
                          "N(0,1) quantile grid converges to Max's 1960 table "
                          "(levels within 2.5e-3, MSE 0.009497)",
+    "restate.qjl_reconstruct_batch": "signed sum of textbook-MT19937 G rows (an "
+                                     "exact integer vector) times the fp32 scale, "
+                                     "bit for bit; also via dequantize_heads",
+    "restate.quantize_rows": "per-row seed (uid % 1024) ^ (base + i): codes equal "
+                             "the explicit argmin, signs the exact projection signs "
+                             "on each row's MT19937 G (boundary rule), norms within "
+                             "2 ulp of the exact norm",
+    "restate.dequantize_rows": "exact integer reconstruction with each row's own "
+                               "seed, bit for bit; centroids alone without QJL",
+    "restate.repeat_kv": "explicit layout known answer (kv head h on q heads "
+                         "h*G .. h*G+G-1)",
+    "restate.fused_attn_python": "fp64 brute force over a K / V reconstruction "
+                                 "built from textbook pieces (shift unpacking, "
+                                 "MT19937 G), D = 128 and 32, with and without "
+                                 "QJL and the causal mask, at 2e-5",
+    "restate.omni_attn_cpu": "fp64 brute force with q updated by the merged LoRA "
+                             "weight (sentinel row unchanged) and scale None = "
+                             "1/sqrt(128), at 2e-5",
+    "exact.argmin_first / pack_bits_lsb / ulp_distance_f32 / residual_norm / "
+    "projections_fp64 / exact_dot / g_from_mt / attention":
+        "tests/test_oracle_pins.py::test_exact_helpers_known_answers (hand-worked "
+        "cases: ties and NaN, bit order, adjacent floats, 3-4-5, exact dyadic "
+        "sums, raw MT19937 low bits, uniform softmax = mean of V); g_from_mt "
+        "rests on the C++ [rand.predef] MT19937 value",
     "exact.projection_signs_exact": "tests/test_oracle_pins.py::"
                                     "test_exact_projection_signs_survive_cancellation: "
                                     "rows whose fp64 sum loses the small terms after "

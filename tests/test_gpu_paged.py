@@ -513,3 +513,50 @@ def test_paged_two_sequences_per_block(device):
     got2 = paged_attention(q.to(device), cache2, pt2, lt2, cb.to(device), **kw)
     ref2 = omni_attn(*(t.to(device) for t in (q, kn, kq, kr, vn, cb)), **kw)
     assert torch.equal(got2, ref2), f"paged LoRA two per block differs by {(got2 - ref2).abs().max().item():.3e}"
+
+
+def test_paged_prefill_bad_page_past_early_rows_causal_window(device):
+    """Causal chunked prefill over pages: a page id outside the pool in the
+    sequence's last page (which the first query rows' causal windows never
+    reach, so their waves never load it) still makes every row of that
+    sequence NaN; a bad id in a table column past the sequence's length is
+    never read and changes nothing."""
+    from omnistack_rs.cache import paged_attention
+    B, Hq, Hkv, T, S, uid = 2, 16, 4, 64, 400, 6       # 256 query rows per kv head: 8 waves of 32 rows
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=395, user_id=uid)
+    q = _data.query((B, Hq, T, 128), seed=396).to(device)
+    print(f"[paged prefill bad page] B={B} Hq={Hq} Hkv={Hkv} T={T} S={S}", flush=True)
+    cache, pt, lt = _paged(device, kn, kq, kr, vn, 16, spare=2, seed=37)
+    ok = paged_attention(q, cache, pt, lt, cb.to(device), user_id=uid, causal=True)
+    assert torch.isfinite(ok).all()
+    last = (S - 1) // 16
+    pt_bad = pt.clone()
+    pt_bad[1, last] = cache.n_pages + 5
+    got = paged_attention(q, cache, pt_bad, lt, cb.to(device), user_id=uid, causal=True, validate=False)
+    assert torch.equal(got[0], ok[0])
+    assert torch.isnan(got[1]).all(), "rows whose causal window ends before the bad page must be NaN too"
+    # a shorter length leaves the last page unused: the bad id is never read
+    lt2 = lt.clone()
+    lt2[1] = last * 16
+    want2 = paged_attention(q, cache, pt, lt2, cb.to(device), user_id=uid, causal=True)
+    got2 = paged_attention(q, cache, pt_bad, lt2, cb.to(device), user_id=uid, causal=True, validate=False)
+    assert torch.equal(got2, want2) and torch.isfinite(got2).all()
+
+
+def test_prepared_paged_attention_refuses_bad_lora_bank(device):
+    """PagedKVAttention checks the B bank's shape against (n_loras,
+    n_heads * head_dim, rank), and that A and B come together."""
+    from omnistack_rs.cache import PagedKVAttention, PagedKVCache
+    pool = PagedKVCache(8, 2, page_size=16, device=device)
+    cb = torch.linspace(-2, 2, 16, device=device)
+    la = torch.zeros(4, 8, 64, dtype=torch.bfloat16, device=device)
+    for lb in (torch.zeros(4, 8 * 128, 8, dtype=torch.bfloat16, device=device)[:, :1000],
+               torch.zeros(4, 8 * 128, 4, dtype=torch.bfloat16, device=device),
+               torch.zeros(3, 8 * 128, 8, dtype=torch.bfloat16, device=device)):
+        with pytest.raises(ValueError):
+            PagedKVAttention(pool, cb, n_heads=8, batch=2, max_pages=4, lora_a=la, lora_b=lb)
+    with pytest.raises(ValueError):
+        PagedKVAttention(pool, cb, n_heads=8, batch=2, max_pages=4, lora_a=la)
+    att = PagedKVAttention(pool, cb, n_heads=8, batch=2, max_pages=4, lora_a=la,
+                           lora_b=torch.zeros(4, 8 * 128, 8, dtype=torch.bfloat16, device=device))
+    assert att.lora is not None

@@ -319,6 +319,12 @@ def test_make_g_matrix_packing():
     j = 5
     assert ((lo[1, 3] >> j) & 1).item() == bits[1, 3, j].item()
     assert ((hi[0, 7] >> j) & 1).item() == bits[0, 7, 64 + j].item()
+    # every word equals the oracle's (pinned on textbook MT19937 bits)
+    from oracle import restate
+    for H, seed in ((2, 42), (8, 7), (1, 0)):
+        lo, hi = make_g_matrix(H, seed)
+        want_lo, want_hi = restate.make_g_matrix(H, seed)
+        assert torch.equal(lo, want_lo) and torch.equal(hi, want_hi)
 
 
 def test_omni_config_validation():
@@ -358,3 +364,47 @@ def test_calibrator_api():
     # Lloyd-Max for N(0,1): outer centroids near +-2.73 (Max 1960)
     assert abs(cb[-1].item() - 2.733) < 0.15 and abs(cb[0].item() + 2.733) < 0.15
     assert calibrate_per_group([torch.randn(500, generator=g), torch.randn(500, generator=g) * 3]).shape == (2, 16)
+
+
+def test_prepared_paged_attention_run_refusals():
+    """PagedKVAttention.run's host checks (cache/paged.py _check_paged_run):
+    every tensor must be contiguous, of the dtype and shape the kernel reads
+    (int32 tables, lengths and adapter ids; x of the bank's shape and dtype),
+    with no copies made on the way; the prepared class refuses CPU pools and
+    a B bank of the wrong shape."""
+    from omnistack_rs.cache.paged import PagedKVAttention, PagedKVCache, _check_paged_run
+    cpu = torch.device("cpu")
+    B, Hq, T, D, mp, hid = 3, 8, 2, 128, 4, 64
+    shape = (B, Hq, T, D)
+    q = torch.zeros(shape, dtype=torch.bfloat16)
+    pt = torch.zeros(B, mp, dtype=torch.int32)
+    ln = torch.zeros(B, dtype=torch.int32)
+    x = torch.zeros(B, T, hid, dtype=torch.bfloat16)
+    ids = torch.zeros(B, dtype=torch.int32)
+
+    def chk(q=q, pt=pt, ln=ln, x=x, ids=ids, hidden=hid, wdt=torch.bfloat16):
+        _check_paged_run(q, pt, ln, x, ids, shape, torch.bfloat16, mp, hidden, wdt, cpu)
+
+    chk()                                                         # well-formed: no error
+    _check_paged_run(q, pt, ln, None, None, shape, torch.bfloat16, mp, None, None, cpu)
+    bad = [
+        dict(q=q.float()), dict(q=q[:, :4]), dict(q=q.transpose(2, 3).contiguous().transpose(2, 3)),
+        dict(pt=pt.long()), dict(pt=pt[:, :2]),
+        dict(pt=torch.zeros(B, 2 * mp, dtype=torch.int32)[:, ::2]),           # right shape, strided
+        dict(ln=ln.long()), dict(ln=ln[:2]), dict(ln=torch.zeros(2 * B, dtype=torch.int32)[::2]),
+        dict(x=None), dict(x=x[:, :1]), dict(x=x.float()), dict(x=torch.zeros(B, T, 2 * hid, dtype=torch.bfloat16)[..., ::2]),
+        dict(ids=None), dict(ids=ids.long()), dict(ids=ids[:2]), dict(ids=torch.zeros(2 * B, dtype=torch.int32)[::2]),
+    ]
+    for kw in bad:
+        with pytest.raises(ValueError):
+            chk(**kw)
+    # x / lora_indices without a bank
+    with pytest.raises(ValueError):
+        _check_paged_run(q, pt, ln, x, ids, shape, torch.bfloat16, mp, None, None, cpu)
+    # tensors on another device than the pool's
+    with pytest.raises(ValueError):
+        _check_paged_run(q, pt, ln, None, None, shape, torch.bfloat16, mp, None, None, torch.device("cuda", 0))
+    # the prepared class refuses a pool in host memory
+    pool = PagedKVCache(4, 2, page_size=16, device="cpu")
+    with pytest.raises(RuntimeError):
+        PagedKVAttention(pool, torch.zeros(16), n_heads=4, batch=1, max_pages=2)

@@ -82,6 +82,59 @@ def test_wht_self_inverse_and_norm():
     assert torch.allclose(restate.wht(x).norm(dim=-1), x.norm(dim=-1), rtol=1e-5)
 
 
+@pytest.mark.parametrize("D", [128, 32])
+def test_rotate_sign_flip_matches_hadamard_times_flip(D):
+    """restate.rotate(x, s) = H_D / sqrt(D) @ (s * x): the flip multiplies the
+    input before the transform.  Checked in fp64 against scipy's Sylvester
+    matrix with an explicit diag(s); a flip applied after the transform
+    (s * WHT(x)), or the flip dropped, misses by O(1)."""
+    g = torch.Generator().manual_seed(D)
+    x = torch.randn(256, D, generator=g)
+    s = torch.randint(0, 2, (D,), generator=g).to(torch.int8) * 2 - 1
+    assert (s == 1).any() and (s == -1).any()
+    H = torch.tensor(scipy.linalg.hadamard(D), dtype=torch.float64) / math.sqrt(D)
+    want = (x.double() * s.double()) @ H.T
+    got = restate.rotate(x, s).double()
+    assert (got - want).abs().max().item() < 2e-6
+    wrong_after = (x.double() @ H.T) * s.double()
+    assert (wrong_after - want).abs().max().item() > 0.5
+    assert (restate.rotate(x).double() - want).abs().max().item() > 0.5
+    # bf16 input: the flip is exact in bf16, the transform runs in fp32 and
+    # the result is rounded to bf16 once (hadamard.py:85)
+    xb = x.to(torch.bfloat16)
+    gotb = restate.rotate(xb, s)
+    assert gotb.dtype == torch.bfloat16
+    wantb = ((xb.double() * s.double()) @ H.T).float().to(torch.bfloat16)
+    # fp32 butterflies then one bf16 rounding: equal to the fp64 product
+    # rounded to bf16 except where the fp32 value sits within its rounding
+    # error of a bf16 rounding boundary (then one bf16 ulp apart)
+    d = (gotb.float() - wantb.float()).abs()
+    ulp = wantb.float().abs() * 2.0 ** -7
+    assert (d <= ulp + 1e-30).all()
+    assert (d == 0).float().mean().item() > 0.99
+
+
+def test_make_g_matrix_is_one_mt19937_stream_packed_lsb_first():
+    """restate.make_g_matrix (fused_attention.py:296-317): one generator
+    stream of H x 64 x 128 bits in (head, row, column) order, column j of the
+    first 64 in bit j of the lo word and column 64 + j in bit j of the hi
+    word, as int64 (two's complement of the 64-bit word).  Pinned on the
+    textbook MT19937's low bits, packed here with Python integers."""
+    for H, seed in ((1, 0), (3, 42), (8, 1234)):
+        lo, hi = restate.make_g_matrix(H, seed)
+        assert lo.shape == (H, 64) and hi.shape == (H, 64) and lo.dtype == torch.int64
+        b = mt19937.bits(seed, H * 64 * 128).reshape(H, 64, 128)
+        for h in range(H):
+            for i in range(64):
+                for half, words in ((0, lo), (1, hi)):
+                    w = 0
+                    for j in range(64):
+                        w |= int(b[h, i, 64 * half + j]) << j
+                    if w >= 1 << 63:
+                        w -= 1 << 64
+                    assert int(words[h, i]) == w, (H, seed, h, i, half)
+
+
 def test_wht_scale_is_fp32_rounded():
     # torch multiplies an fp32 tensor by a Python double via the fp32-rounded
     # scalar; the restatement inherits it (the GPU kernel relies on it).
@@ -373,3 +426,192 @@ def test_lloyd_max_gaussian_matches_max_1960():
     code = exact.argmin_first(x.numpy(), cb.numpy())
     mse = float(((x.double() - cb.double()[torch.from_numpy(code).long()]) ** 2).mean())
     assert abs(mse - 0.009497) < 2e-5
+
+
+# ── row-seeded codec and the composed attention oracle ──────────────────
+
+def test_quantize_rows_per_row_seed_against_exact():
+    """restate.quantize_rows (quantize.py:456-499, torch branch): row i of
+    the flattened input uses seed (user_id % 1024) ^ (base + i).  Codes are
+    the explicit first-index argmin, signs the exact projection signs on
+    that row's textbook-MT19937 G (boundary rule), norms within 2 ulp of the
+    exact norm."""
+    g = torch.Generator().manual_seed(31)
+    x = restate.wht(torch.randn(2, 3, 128, generator=g))
+    cb = restate.lloyd_max(x.reshape(-1), max_iters=30)
+    base, uid = 5, 1030
+    nib, qjl, nrm = restate.quantize_rows(x, cb, base_head_idx=base, user_id=uid)
+    assert nib.shape == (2, 3, 64) and qjl.shape == (2, 3, 8) and nrm.shape == (2, 3)
+    flat = x.reshape(6, 128).numpy()
+    codes = exact.argmin_first(flat, cb.numpy())
+    assert np.array_equal(restate.unpack_nibbles(nib.reshape(6, 64)).numpy(), codes)
+    e = (flat - cb.numpy()[codes]).astype(np.float32)
+    for i in range(6):
+        seed = (uid % 1024) ^ (base + i)
+        G = exact.g_from_mt(seed)
+        want = exact.pack_bits_lsb(exact.projection_signs_exact(e[i:i + 1], G).astype(np.uint8))
+        diff = np.unpackbits(qjl.reshape(6, 8)[i:i + 1].numpy() ^ want, axis=1, bitorder="little").astype(bool)
+        rel = np.abs(exact.projections_fp64(e[i:i + 1], G)) / np.linalg.norm(e[i].astype(np.float64))
+        assert (rel[diff] < 1e-6).all()
+    assert exact.ulp_distance_f32(nrm.reshape(6).numpy(), exact.residual_norm(e)).max() <= 2
+
+
+def test_dequantize_rows_is_exact_integer_reconstruction():
+    """restate.dequantize_rows (quantize.py:502-537): c[code] + (b+- . G_i) *
+    fl(norm * sqrt(2/pi) / D) with row i's own seed; b . G is an exact
+    integer, so the result is determined to the last bit."""
+    g = torch.Generator().manual_seed(32)
+    N, base, uid = 5, 9, 3
+    nib = torch.randint(0, 256, (N, 64), generator=g, dtype=torch.uint8)
+    qjl = torch.randint(0, 256, (N, 8), generator=g, dtype=torch.uint8)
+    nrm = torch.rand(N, generator=g) * 3
+    cb = torch.linspace(-2.5, 2.5, 16)
+    out = restate.dequantize_rows(nib, qjl, nrm, cb, base_head_idx=base, user_id=uid).numpy()
+    codes = np.stack([np.asarray([(int(b) >> (4 * k)) & 0xF for b in row for k in (0, 1)]) for row in nib.numpy()])
+    for i in range(N):
+        G = exact.g_from_mt((uid % 1024) ^ (base + i))
+        b = np.unpackbits(qjl[i:i + 1].numpy(), axis=1, bitorder="little").astype(np.float64)[0] * 2 - 1
+        s = (b @ G).astype(np.float32)
+        # torch forms (b @ G) * (norm * c) with the Python float norm * c in
+        # double, then rounds that scalar to fp32
+        sc = np.float32(float(nrm[i]) * math.sqrt(2.0 / math.pi) / 128)
+        want = (cb.numpy()[codes[i]] + (s * sc).astype(np.float32)).astype(np.float32)
+        assert np.array_equal(out[i], want), i
+    # without QJL: the centroids alone
+    out0 = restate.dequantize_rows(nib, qjl, nrm, cb, base_head_idx=base, user_id=uid, with_qjl=False).numpy()
+    assert np.array_equal(out0, cb.numpy()[codes])
+
+
+def test_qjl_reconstruct_batch_is_signed_sum_of_g_rows():
+    """restate.qjl_reconstruct_batch (quantize.py:426-451): row n is
+    sum_i b_i G_i (an exact integer vector) times fl(norm_n * fl(sqrt(2/pi)/D))."""
+    g = torch.Generator().manual_seed(33)
+    qjl = torch.randint(0, 256, (7, 8), generator=g, dtype=torch.uint8)
+    nrm = torch.rand(7, generator=g) * 2
+    seed = 42 ^ 5
+    got = restate.qjl_reconstruct_batch(qjl, nrm, seed).numpy()
+    G = exact.g_from_mt(seed)
+    b = np.unpackbits(qjl.numpy(), axis=1, bitorder="little").astype(np.float64) * 2 - 1
+    s = (b @ G).astype(np.float32)
+    sc = (nrm.numpy() * np.float32(math.sqrt(2 / math.pi) / 128)).astype(np.float32)
+    assert np.array_equal(got, (s * sc[:, None]).astype(np.float32))
+
+
+def _exact_deq(nib, qjl, nrm, cb, uid, with_qjl):
+    """(B, H, S, D) f64 reconstruction built from textbook pieces: nibble
+    unpacking by shifts, exact signed sums of MT19937 G rows, per-head seed."""
+    B, H, S, nb = nib.shape
+    D = 2 * nb
+    out = np.zeros((B, H, S, D))
+    for h in range(H):
+        c = cb[h].numpy() if cb.dim() == 2 else cb.numpy()
+        n = nib[:, h].reshape(-1, nb).numpy().astype(np.int64)
+        codes = np.stack([(n >> 0) & 0xF, (n >> 4) & 0xF], axis=-1).reshape(-1, D)
+        x = c[codes].astype(np.float64)
+        if with_qjl:
+            G = exact.g_from_mt((uid % 1024) ^ h, D)
+            b = np.unpackbits(qjl[:, h].reshape(-1, D // 16).numpy(), axis=1, bitorder="little").astype(np.float64) * 2 - 1
+            a = nrm[:, h].reshape(-1).numpy().astype(np.float64) * math.sqrt(2 / math.pi) / D
+            x = x + (b @ G) * a[:, None]
+        out[:, h] = x.reshape(B, S, D)
+    return torch.from_numpy(out)
+
+
+@pytest.mark.parametrize("D", [128, 32])
+def test_fused_attn_python_against_fp64_on_exact_reconstruction(D):
+    """restate.fused_attn_python (fused_attention.py:435-466): K with its
+    QJL reconstruction, V as centroids only (the same codebooks), then the
+    softmax attention.  Checked against fp64 brute force on a K / V
+    reconstruction built independently, with and without a causal mask."""
+    g = torch.Generator().manual_seed(34 + D)
+    B, Hq, Hkv, T, S, uid = 2, 8, 2, 3, 150, 77
+    kn = torch.randint(0, 256, (B, Hkv, S, D // 2), generator=g, dtype=torch.uint8)
+    vn = torch.randint(0, 256, (B, Hkv, S, D // 2), generator=g, dtype=torch.uint8)
+    kq = torch.randint(0, 256, (B, Hkv, S, D // 16), generator=g, dtype=torch.uint8)
+    kr = torch.rand(B, Hkv, S, generator=g)
+    cb = torch.randn(Hkv, 16, generator=g).sort(dim=1).values
+    q = torch.randn(B, Hq, T, D, generator=g)
+    off = S - T
+    mask = torch.zeros(1, 1, T, S)
+    for t in range(T):
+        mask[..., t, off + t + 1:] = float("-inf")
+    for with_qjl in (True, False):
+        kd = _exact_deq(kn, kq, kr, cb, uid, with_qjl)
+        vd = _exact_deq(vn, kq, kr, cb, uid, False)
+        for m in (None, mask):
+            got = restate.fused_attn_python(q, kn, kq, kr, vn, cb, uid, 1 / math.sqrt(D), with_qjl, mask=m)
+            want = exact.attention(q, kd, vd, 1 / math.sqrt(D), m)
+            assert (got.double() - want).abs().max().item() < 2e-5, (with_qjl, m is None)
+
+
+def test_omni_attn_cpu_lora_and_default_scale():
+    """restate.omni_attn_cpu (fused_attention.py:497-523): the LoRA update of
+    q (merged-weight closed form in fp64) and scale None = 1/sqrt(128), then
+    the attention; fp64 brute force on the exact reconstruction."""
+    g = torch.Generator().manual_seed(35)
+    B, Hq, Hkv, T, S, uid, hid, r, L = 3, 8, 2, 1, 70, 5, 64, 4, 6
+    kn = torch.randint(0, 256, (B, Hkv, S, 64), generator=g, dtype=torch.uint8)
+    vn = torch.randint(0, 256, (B, Hkv, S, 64), generator=g, dtype=torch.uint8)
+    kq = torch.randint(0, 256, (B, Hkv, S, 8), generator=g, dtype=torch.uint8)
+    kr = torch.rand(B, Hkv, S, generator=g)
+    cb = torch.randn(16, generator=g).sort().values
+    q = torch.randn(B, Hq, T, 128, generator=g)
+    x = torch.randn(B, T, hid, generator=g)
+    A = torch.randn(L, r, hid, generator=g) * 0.05
+    Bw = torch.randn(L, Hq * 128, r, generator=g) * 0.05
+    idx = torch.tensor([4, -1, 0], dtype=torch.int32)
+    got = restate.omni_attn_cpu(q, kn, kq, kr, vn, cb, user_id=uid, x=x, lora_a=A, lora_b=Bw,
+                                lora_indices=idx, lora_alpha=0.7)
+    q_eff = q.double().clone()
+    for b in range(B):
+        if idx[b] >= 0:
+            W = Bw[idx[b]].double() @ A[idx[b]].double()
+            q_eff[b] += (x[b].double() @ W.T).reshape(T, Hq, 128).permute(1, 0, 2) * 0.7
+    want = exact.attention(q_eff, _exact_deq(kn, kq, kr, cb, uid, True), _exact_deq(vn, kq, kr, cb, uid, False),
+                           1 / math.sqrt(128))
+    assert (got.double() - want).abs().max().item() < 2e-5
+
+
+# ── the fp64 / exact helpers themselves ─────────────────────────────────
+
+def test_exact_helpers_known_answers():
+    # argmin_first: explicit cases (tie -> first index, NaN distance wins)
+    cb = np.array([0.0, 1.0, 1.0, 3.0] + [10.0] * 12, dtype=np.float32)
+    x = np.array([0.4, 0.5, 1.0, 2.0, 2.6, np.nan, -np.inf], dtype=np.float32)
+    assert exact.argmin_first(x, cb).tolist() == [0, 0, 1, 1, 3, 0, 0]
+    # pack_bits_lsb: bit b of byte m = bits[8m + b]
+    bits = np.zeros((1, 16), dtype=np.uint8)
+    bits[0, [0, 3, 8, 15]] = 1
+    assert exact.pack_bits_lsb(bits).tolist() == [[0b1001, 0b10000001]]
+    # ulp_distance_f32: adjacent floats are 1 apart
+    a = np.float32(1.0)
+    assert exact.ulp_distance_f32(np.array([a]), np.array([np.nextafter(a, np.float32(2))])).tolist() == [1]
+    # residual_norm: 3-4-5 exactly, and rounding of an fp64 norm to fp32
+    assert exact.residual_norm(np.array([[3.0, 4.0] + [0.0] * 126], dtype=np.float32)).tolist() == [5.0]
+    # projections_fp64 / exact_dot agree where fp64 is exact
+    e = np.array([[1.5, -2.25, 0.125] + [0.0] * 125], dtype=np.float32)
+    G = np.ones((1, 128))
+    G[0, 1] = -1
+    assert exact.projections_fp64(e, G)[0, 0] == 1.5 + 2.25 + 0.125 == float(exact.exact_dot(e[0], G[0]))
+    # g_from_mt: +-1 in draw order of the textbook generator's low bits
+    raw = mt19937.raw(42, 256)
+    assert np.array_equal(exact.g_from_mt(42).reshape(-1)[:256], 2.0 * (raw & 1) - 1)
+    # attention: uniform scores give the mean of V
+    q = torch.zeros(1, 1, 1, 4)
+    k = torch.randn(1, 1, 5, 4)
+    v = torch.randn(1, 1, 5, 4)
+    assert torch.allclose(exact.attention(q, k, v, 1.0), v.double().mean(dim=2, keepdim=True))
+
+
+def test_every_oracle_function_has_a_pin():
+    """oracle.PINS names the check of every public function of
+    oracle.restate and oracle.exact."""
+    import inspect
+    import oracle
+    from oracle import exact as ex
+    keys = " ".join(oracle.PINS)
+    for mod, prefix in ((restate, "restate."), (ex, "exact.")):
+        for name, fn in inspect.getmembers(mod, inspect.isfunction):
+            if fn.__module__ != mod.__name__ or name.startswith("_"):
+                continue
+            assert (prefix + name) in keys or (prefix in keys and name in keys), prefix + name
