@@ -1382,8 +1382,13 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     const int full_end = nseq > 1 ? s_begin : (int)imin64((int64_t)s_end, min_limit64 + 1);
     const uint32_t laneoff = (uint32_t)(lane & 31) * 8u;
     const uint32_t slane = (uint32_t)kSlutOff | laneoff;
-    // ones on the hi slots of each (hi, lo) pair: sums every token's P once
-    const half8_t ones = as_half8(0x3C003C00u, 0u, 0x3C003C00u, 0u);
+    // ones on the hi slots of each (hi, lo) pair: sums every token's P once.
+    // Only output row 0 of that MFMA is read (lanes with n == 0 hold A row
+    // 0): the other rows get zeros.  The matrix cores run at a power-limited
+    // clock under sustained load, and operands that only feed discarded
+    // outputs still cost power when nonzero.
+    const uint32_t one2 = n == 0 ? 0x3C003C00u : 0u;
+    const half8_t ones = as_half8(one2, 0u, one2, 0u);
     const unsigned char *lut = smem + kLutOff;
 
     float4_t oacc[8], lacc_sum;
@@ -1394,7 +1399,10 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     // exponent offset directly: a tile whose keys are all masked (-inf)
     // still gives exp2(-inf - m) = 0, and the first finite maximum replaces
     // it (scaling the empty accumulators by exp2(-FLT_MAX - mt) = 0)
-    float m_run = -__FLT_MAX__;
+    // Padding row slots (no query row) start at +FLT_MAX instead, so every
+    // probability of their columns is exp2(-FLT_MAX) = 0 and the PV operand
+    // columns they feed stay zero (their outputs are never read).
+    float m_run = row_valid(rn) ? -__FLT_MAX__ : __FLT_MAX__;
     // Exponents are fma(raw, csc, -m_run): exact products against a rounded
     // maximum, which keeps relative weights exact but puts an error of up to
     // half an ulp of m_run on every exponent.  Once any row's |m_run| reaches
@@ -1464,7 +1472,8 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
             for (int k = 0; k < 8; ++k) oacc[k] *= f;
             lacc_sum *= f;
             m_run = need ? mt : m_run;
-            round_first = round_first || __builtin_amdgcn_ballot_w64(fabsf(m_run) >= 8192.0f && m_run > -__FLT_MAX__);
+            round_first = round_first ||
+                          __builtin_amdgcn_ballot_w64(fabsf(m_run) >= 8192.0f && m_run > -__FLT_MAX__ && m_run < __FLT_MAX__);
         }
         const float nm = -m_run;
         // lanes n and n + 8 hold the same scores: columns 0-7 exponentiate the
@@ -1485,9 +1494,15 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
         const uint32_t my01 = cvt_pk_h2(__builtin_amdgcn_exp2f(ex[0]), __builtin_amdgcn_exp2f(ex[1]));
         const uint32_t my23 = cvt_pk_h2(__builtin_amdgcn_exp2f(ex[2]), __builtin_amdgcn_exp2f(ex[3]));
         const uint32_t ot01 = dpp_row_ror8(my01), ot23 = dpp_row_ror8(my23);
+        // B columns 8-15 of PV feed output columns that are never read: zero
+        // (power, as for the denominator's ones)
         half8_t pb[2];
-        pb[0] = as_half8(my01, my01, my23, my23);
-        pb[1] = as_half8(ot01, ot01, ot23, ot23);
+        {
+            const uint32_t a01 = lo_col ? 0u : my01, a23 = lo_col ? 0u : my23;
+            const uint32_t b01 = lo_col ? 0u : ot01, b23 = lo_col ? 0u : ot23;
+            pb[0] = as_half8(a01, a01, a23, a23);
+            pb[1] = as_half8(b01, b01, b23, b23);
+        }
 #pragma unroll
         for (int u = 0; u < 2; ++u) lacc_sum = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb[u], lacc_sum, 0, 0, 0);
 
@@ -1942,7 +1957,10 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
     };
     const uint32_t laneoff = (uint32_t)(lane & 31) * 8u;
     const uint32_t slane = (uint32_t)kSlutOff | laneoff;
-    const half8_t ones = as_half8(0x3C003C00u, 0u, 0x3C003C00u, 0u);
+    // lane (ne, ge) reads denominator row 4 ge: only A rows 0, 4, 8 and 12
+    // need the ones (zeros elsewhere save matrix-core power)
+    const uint32_t one2 = (n & 3) == 0 ? 0x3C003C00u : 0u;
+    const half8_t ones = as_half8(one2, 0u, one2, 0u);
     const unsigned char *lut = smem + kLutOff;
 
     float4_t oacc[NCB][8], lacc[NCB];
@@ -2387,7 +2405,10 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
                                              QJL ? s_end * 4 : 0, kBufWord3);
     const uint32_t laneoff = (uint32_t)(lane & 31) * 8u;
     const uint32_t slane = (uint32_t)kSlutOff | laneoff;
-    const half8_t ones = as_half8(0x3C003C00u, 0u, 0x3C003C00u, 0u);
+    // lane (ne, ge) reads denominator row 4 ge: only A rows 0, 4, 8 and 12
+    // need the ones (zeros elsewhere save matrix-core power)
+    const uint32_t one2 = (n & 3) == 0 ? 0x3C003C00u : 0u;
+    const half8_t ones = as_half8(one2, 0u, one2, 0u);
     const unsigned char *lut = smem + kLutOff;
 
     float4_t oacc[NCB][2], lacc[NCB];
