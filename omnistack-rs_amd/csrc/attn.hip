@@ -1382,13 +1382,14 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     const int full_end = nseq > 1 ? s_begin : (int)imin64((int64_t)s_end, min_limit64 + 1);
     const uint32_t laneoff = (uint32_t)(lane & 31) * 8u;
     const uint32_t slane = (uint32_t)kSlutOff | laneoff;
-    // ones on the hi slots of each (hi, lo) pair: sums every token's P once.
-    // Only output row 0 of that MFMA is read (lanes with n == 0 hold A row
-    // 0): the other rows get zeros.  The matrix cores run at a power-limited
-    // clock under sustained load, and operands that only feed discarded
-    // outputs still cost power when nonzero.
+    // ones in every slot of A row 0: one MFMA sums the P of all 32 tokens of
+    // a tile (B holds the two halves' P side by side).  Only output row 0 of
+    // that MFMA is read (lanes with n == 0 hold A row 0): the other rows get
+    // zeros.  The matrix cores run at a power-limited clock under sustained
+    // load, and operands that only feed discarded outputs still cost power
+    // when nonzero.
     const uint32_t one2 = n == 0 ? 0x3C003C00u : 0u;
-    const half8_t ones = as_half8(one2, 0u, one2, 0u);
+    const half8_t ones = as_half8(one2, one2, one2, one2);
     const unsigned char *lut = smem + kLutOff;
 
     float4_t oacc[8], lacc_sum;
@@ -1502,9 +1503,9 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
             const uint32_t b01 = lo_col ? 0u : ot01, b23 = lo_col ? 0u : ot23;
             pb[0] = as_half8(a01, a01, a23, a23);
             pb[1] = as_half8(b01, b01, b23, b23);
+            // the denominator: tokens 4g .. 4g + 3 of both halves in one operand
+            lacc_sum = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, as_half8(a01, a23, b01, b23), lacc_sum, 0, 0, 0);
         }
-#pragma unroll
-        for (int u = 0; u < 2; ++u) lacc_sum = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb[u], lacc_sum, 0, 0, 0);
 
         // PV: pair bytes interleave the nibbles of two tokens at one d, so
         // each LUT entry is an MFMA-ready (hi pair, lo pair) for that d.
