@@ -547,15 +547,19 @@ __device__ __forceinline__ int dec_chunk(int row, int c) { return c ^ (2 * (row 
 constexpr int kDecCntOff = kDecCscOff + kDecRows * 4;                // next unclaimed tile of the block
 constexpr int kDecLrOff = kDecCntOff + 16;                           // fused LoRA: x A^T of two row groups
 constexpr int kDecLdsBytes = kDecLrOff + 2 * 16 * 4;
-// Paged cache: the pool row of each page of the split (page p of the split
-// at kDecPtOff + 4 p), staged in the prologue when the split spans at most
-// kDecPtMax pages, so a claimed tile's rows are one LDS read away; longer
-// splits read the page table per tile.
+// Paged cache: the pool row of each 16-token half of the split (half h at
+// kDecPtOff + 4 h, the row of token s_begin + 16 h), staged in the prologue
+// when the split has at most kDecPtMax halves, so a claimed tile's two rows
+// are one 8-byte LDS read away; longer splits (fused LoRA, two sequences per
+// block) read the page table per tile.  Each wave also records whether its
+// staged halves met a page id outside the pool (one word per wave at
+// kDecPtFlagOff).
 constexpr int kDecPtOff = (kDecLdsBytes + 15) & ~15;
-constexpr int kDecPtMax = 3072;
+constexpr int kDecPtMax = 6144;
 constexpr int kDecPtLoads = kDecPtMax / (64 * kDecWaves);
 static_assert(kDecPtLoads * 64 * kDecWaves == kDecPtMax, "page rows staged by a fixed number of loads per thread");
-constexpr uint32_t kDecPtBad = 0xFFFFFFFFu;                          // staged row of a page id outside the pool
+constexpr int kDecPtFlagOff = kDecPtOff + 4 * kDecPtMax;
+constexpr int kDecPtLdsBytes = kDecPtFlagOff + 4 * kDecWaves;
 // epilogue reuse of [0, 68K): per-wave O slabs (rows padded to 132 floats),
 // then per-wave running max and denominator
 constexpr int kObStride = 128 + 4;
@@ -986,7 +990,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     static_assert(SPB == 1 || SPB == 2, "one or two sequences per block");
     constexpr int D = 128, QD = 64;
     constexpr int nw = kDecWaves;
-    __shared__ __attribute__((aligned(16))) unsigned char smem[PAGED && !LORA && SPB == 1 ? kDecPtOff + 4 * kDecPtMax : kDecLdsBytes];
+    __shared__ __attribute__((aligned(16))) unsigned char smem[PAGED && !LORA && SPB == 1 ? kDecPtLdsBytes : kDecLdsBytes];
     float *qs = reinterpret_cast<float *>(smem + kDecQsOff);
     float *gq = qs + kDecRows * D;
 
@@ -1081,24 +1085,31 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
         if (SPB > 1 && sq) paged_half_rows(a, pt_row1, hk, t, s_end1, page_bad1, rb);
         else paged_half_rows(a, pt_row, hk, t, s_end, page_bad, rb);
     };
-    // the split's page ids (pages pg0 .. pg0 + npg - 1), requested before
-    // the cache prefetch so that waiting for them does not wait for it;
-    // converted to pool rows and staged in LDS before the first barrier
-    // (not with the fused LoRA prologue, whose scalar registers are full)
+    // the page id of each half of the split (pages pg0 .. pg0 + npg - 1;
+    // halves past the split end take its last page, as the page-table path
+    // does), requested before the cache prefetch so that waiting for them
+    // does not wait for it; converted to pool rows and staged in LDS before
+    // the first barrier (not with the fused LoRA prologue, whose scalar
+    // registers are full)
     constexpr bool kStage = PAGED && !LORA && SPB == 1;
     const int pg0 = kStage ? (s_begin >> a.page_shift) : 0;
     const int npg = kStage && s_end > s_begin ? ((s_end - 1) >> a.page_shift) - pg0 + 1 : 0;
-    const bool pt_lds = kStage && npg <= kDecPtMax;
+    const int nh = 2 * tps;
+    const bool pt_lds = kStage && nh <= kDecPtMax;
     uint32_t ptv[kStage ? kDecPtLoads : 1];
     if constexpr (kStage) {
         const __amdgpu_buffer_rsrc_t PT = __builtin_amdgcn_make_buffer_rsrc(
             (void *)(pt_row + pg0), (short)0, pt_lds ? npg * 4 : 0, kBufWord3);
 #pragma unroll
-        for (int k = 0; k < kDecPtLoads; ++k)
-            ptv[k] = __builtin_amdgcn_raw_buffer_load_b32(PT, 4u * (uint32_t)(tid + 64 * nw * k), 0, 0);
+        for (int k = 0; k < kDecPtLoads; ++k) {
+            // halves past the staged count read out of range (0, no memory access)
+            const int h = tid + 64 * nw * k;
+            const int q = imax(imin(((s_begin + 16 * h) >> a.page_shift) - pg0, npg - 1), 0);
+            ptv[k] = __builtin_amdgcn_raw_buffer_load_b32(PT, h < nh ? 4u * (uint32_t)q : 0x80000000u, 0, 0);
+        }
     }
     // rows of the two 16-token halves of the tile at token t: from the
-    // staged rows when the split's pages fit, else from the page table
+    // staged rows when the split's halves fit, else from the page table
     auto claim_rows = [&](int t, int sq, uint32_t (&rb)[2]) {
         if (!kStage || !pt_lds) {
             // page-table path: the scalar loads are waited for here, before
@@ -1109,16 +1120,12 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
             __builtin_amdgcn_sched_barrier(0);
             return;
         }
-        const uint32_t *ptl = reinterpret_cast<const uint32_t *>(smem + kDecPtOff);
-        const uint32_t pmask = (1u << a.page_shift) - 1u;
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int th = t + 16 * u;
-            const uint32_t base = ptl[imax(imin((th >> a.page_shift) - pg0, npg - 1), 0)];
-            const bool ok = base != kDecPtBad;
-            page_bad = page_bad || (!ok && th < s_end);
-            rb[u] = (ok ? base : 0u) + ((uint32_t)th & pmask);
-        }
+        // claims past the split end (prefetched, never consumed) read the
+        // last tile's rows
+        const int i = imin((t - s_begin) / kDecTile, tps - 1);
+        const uint2 r = *reinterpret_cast<const uint2 *>(smem + kDecPtOff + 8 * i);
+        rb[0] = __builtin_amdgcn_readfirstlane(r.x);
+        rb[1] = __builtin_amdgcn_readfirstlane(r.y);
     };
 
     // ── prologue loads: branch-free buffer loads (an absent input gets a
@@ -1290,17 +1297,38 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
         }
     }
     if constexpr (kStage) {
-        // pool row of each staged page (kDecPtBad for an id outside the pool)
+        // pool row of each staged half: (page * Hkv + hk) * page_size + slot;
+        // a page id outside the pool reads page 0 and, for a half that holds
+        // tokens of the sequence, flags the wave (rows come out NaN)
         uint32_t *ptl = reinterpret_cast<uint32_t *>(smem + kDecPtOff);
-        const uint32_t np = (uint32_t)a.n_pages;
+        const uint32_t np = (uint32_t)a.n_pages;                  // < 2^26 (host check)
+        const uint32_t pmask = (1u << a.page_shift) - 1u;
+        bool bad = false;
 #pragma unroll
         for (int k = 0; k < kDecPtLoads; ++k) {
-            const int j = tid + 64 * nw * k;
-            if (pt_lds && j < npg)
-                ptl[j] = ptv[k] < np ? (ptv[k] * (uint32_t)a.Hkv + (uint32_t)hk) << a.page_shift : kDecPtBad;
+            const int h = tid + 64 * nw * k;
+            const int th = s_begin + 16 * h;
+            const bool ok = ptv[k] < np;                          // negative ids wrap past np
+            bad = bad || (pt_lds && h < nh && !ok && th < s_end);
+            if (pt_lds && h < nh)
+                ptl[h] = (((ok ? ptv[k] : 0u) * (uint32_t)a.Hkv + (uint32_t)hk) << a.page_shift) +
+                         ((uint32_t)th & pmask);
         }
+        const bool wbad = __builtin_amdgcn_ballot_w64(bad) != 0;
+        if (lane == 0) reinterpret_cast<uint32_t *>(smem + kDecPtFlagOff)[wave] = wbad ? 1u : 0u;
     }
     __syncthreads();
+    if constexpr (kStage) {
+        // the split's bad pages poison every wave's denominator (the block
+        // merges them all, so this is the sequence's result either way)
+        if (pt_lds) {
+            const uint32_t *fl = reinterpret_cast<const uint32_t *>(smem + kDecPtFlagOff);
+            uint32_t any = 0u;
+#pragma unroll
+            for (int w = 0; w < kDecWaves; ++w) any |= w < nw ? fl[w] : 0u;
+            page_bad = any != 0u;
+        }
+    }
 
 
     if (QJL && wave < QD / 16) {
@@ -2628,6 +2656,11 @@ static Plan make_plan(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int D, b
         const int64_t tiles = (S + kDecTile - 1) / kDecTile;
         int64_t splits = clamp64((cus + units - 1) / (units > 0 ? units : 1), 1, (tiles / 16) > 1 ? tiles / 16 : 1);
         if (p.spb > 1) splits = 1;
+        // paged: splits short enough for every half's pool row to be staged
+        if (paged && p.spb == 1) {
+            const int64_t cap = kDecPtMax / 2;
+            if (tiles > splits * cap) splits = (tiles + cap - 1) / cap;
+        }
         const int64_t tps = (tiles + splits - 1) / splits;
         p.splits = (int)splits;
         p.split_len = tps * kDecTile;

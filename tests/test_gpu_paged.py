@@ -279,15 +279,16 @@ def test_paged_decode_dynamic_claims_and_bad_page(device):
 
 
 def test_paged_decode_split_longer_than_staged_pages(device):
-    """32 sequences x 8 kv heads x 49600 tokens in 16-token pages: one split
-    per (sequence, kv head) spans 3100 pages, more than the prologue stages,
-    so claimed tiles read their page ids from the page table.  Equal to the
-    contiguous kernel on the same bytes within the parity bar (the dynamic
-    tile claims sum in run-dependent order); a page id outside the pool in
-    the dynamically claimed range gives NaN rows for that sequence only."""
+    """32 sequences x 8 kv heads x 100000 tokens in 16-token pages: one split
+    per (sequence, kv head), the contiguous plan, would hold 6250 16-token
+    halves, more than the prologue stages (6144), so the paged plan splits
+    each sequence in two.  Equal to the contiguous kernel on the same bytes
+    within the parity bar (different splits, and the dynamic tile claims sum
+    in run-dependent order); a page id outside the pool in the dynamically
+    claimed range gives NaN rows for that sequence only."""
     from omnistack_rs.cache import paged_attention
     from omnistack_rs.kernels.fused_attention import omni_attn
-    B, Hq, Hkv, T, S, uid = 32, 32, 8, 1, 49600, 13
+    B, Hq, Hkv, T, S, uid = 32, 32, 8, 1, 100000, 13
     kn, kq, kr, vn = _random_cache(device, B, Hkv, S, seed=411)
     cb = _data.gaussian_codebook(Hkv).to(device)
     q = _data.query((B, Hq, T, 128), seed=412).to(device)
@@ -295,9 +296,9 @@ def test_paged_decode_split_longer_than_staged_pages(device):
     cache, pt, lt = _paged(device, kn, kq, kr, vn, 16, spare=0, seed=41)
     del kn, kq, kr, vn
     got = paged_attention(q, cache, pt, lt, cb, user_id=uid)
-    _assert_close(got.cpu(), ref.cpu(), "paged split of 3100 pages vs contiguous")
+    _assert_close(got.cpu(), ref.cpu(), "paged splits of 6250 halves vs contiguous")
     pt_bad = pt.clone()
-    pt_bad[7, 40000 // 16] = cache.n_pages
+    pt_bad[7, 90000 // 16] = cache.n_pages
     bad = paged_attention(q, cache, pt_bad, lt, cb, user_id=uid, validate=False)
     assert torch.isnan(bad[7]).all()
     keep = [b for b in range(B) if b != 7]
