@@ -2435,9 +2435,10 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
     const uint32_t laneoff = (uint32_t)(lane & 31) * 8u;
     const uint32_t slane = (uint32_t)kSlutOff | laneoff;
     // lane (ne, ge) reads denominator row 4 ge: only A rows 0, 4, 8 and 12
-    // need the ones (zeros elsewhere save matrix-core power)
+    // need the ones (zeros elsewhere save matrix-core power); every k slot
+    // of the P operand is a distinct token, so those rows are all ones
     const uint32_t one2 = (n & 3) == 0 ? 0x3C003C00u : 0u;
-    const half8_t ones = as_half8(one2, 0u, one2, 0u);
+    const half8_t ones = as_half8(one2, one2, one2, one2);
     const unsigned char *lut = smem + kLutOff;
 
     float4_t oacc[NCB][2], lacc[NCB];
@@ -2484,7 +2485,9 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
                 }
             }
         }
-        half8_t pb[NCB][2];
+        // P of the lane's eight tokens (4g .. 4g + 3 of each half) as one
+        // B operand: k slot 8g + j holds token 16 (j / 4) + 4g + j % 4
+        half8_t pb[NCB];
 #pragma unroll
         for (int c = 0; c < NCB; ++c) {
             // raw scores; the row scale qsr >= 0 enters each exponent's fma
@@ -2536,31 +2539,41 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
 #pragma unroll
                 for (int k = 0; k < 8; ++k) ex[k] = (dead >> k) & 1u ? -INFINITY : ex[k];
             }
+            uint32_t pw[4];
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const uint32_t p01 = cvt_pk_h2(__builtin_amdgcn_exp2f(ex[4 * u]), __builtin_amdgcn_exp2f(ex[4 * u + 1]));
-                const uint32_t p23 = cvt_pk_h2(__builtin_amdgcn_exp2f(ex[4 * u + 2]), __builtin_amdgcn_exp2f(ex[4 * u + 3]));
-                pb[c][u] = as_half8(p01, p01, p23, p23);
-                lacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb[c][u], lacc[c], 0, 0, 0);
-            }
+            for (int j = 0; j < 4; ++j)
+                pw[j] = cvt_pk_h2(__builtin_amdgcn_exp2f(ex[2 * j]), __builtin_amdgcn_exp2f(ex[2 * j + 1]));
+            pb[c] = as_half8(pw[0], pw[1], pw[2], pw[3]);
+            lacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb[c], lacc[c], 0, 0, 0);
         }
-        // PV: pair bytes of tokens (4g, 4g + 1) and (4g + 2, 4g + 3) at dims
-        // 2n (low nibbles) and 2n + 1 (high nibbles)
+        // PV: pair bytes of tokens (4g, 4g + 1) and (4g + 2, 4g + 3) of each
+        // half at dims 2n (low nibbles) and 2n + 1 (high nibbles); a LUT
+        // entry is (fp16 hi pair, remainder pair), read as two dwords so the
+        // hi and remainder planes are two A operands over the same P
+        uint32_t ph[2][4], pl[2][4];      // [dim parity][pair byte]
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const uint32_t b0 = R.v[4 * u], b1 = R.v[4 * u + 1], b2 = R.v[4 * u + 2], b3 = R.v[4 * u + 3];
-            const uint32_t ev01 = __builtin_amdgcn_ubfe(b0, 0, 4) | ((b1 & 0x0Fu) << 4);
-            const uint32_t ev23 = __builtin_amdgcn_ubfe(b2, 0, 4) | ((b3 & 0x0Fu) << 4);
-            const uint32_t od01 = (b0 >> 4) | (b1 & 0xF0u);
-            const uint32_t od23 = (b2 >> 4) | (b3 & 0xF0u);
-            const half8_t ae = pair_half8(*reinterpret_cast<const uint2 *>(lut + lut_addr(ev01, laneoff, 0)),
-                                          *reinterpret_cast<const uint2 *>(lut + lut_addr(ev23, laneoff, 0)));
-            const half8_t ao = pair_half8(*reinterpret_cast<const uint2 *>(lut + lut_addr(od01, laneoff, 0)),
-                                          *reinterpret_cast<const uint2 *>(lut + lut_addr(od23, laneoff, 0)));
+            const uint32_t pe[2] = {__builtin_amdgcn_ubfe(b0, 0, 4) | ((b1 & 0x0Fu) << 4),
+                                    __builtin_amdgcn_ubfe(b2, 0, 4) | ((b3 & 0x0Fu) << 4)};
+            const uint32_t po[2] = {(b0 >> 4) | (b1 & 0xF0u), (b2 >> 4) | (b3 & 0xF0u)};
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t ae = lut_addr(pe[h], laneoff, 0), ao = lut_addr(po[h], laneoff, 0);
+                ph[0][2 * u + h] = *reinterpret_cast<const uint32_t *>(lut + ae);
+                pl[0][2 * u + h] = *reinterpret_cast<const uint32_t *>(lut + ae + 4);
+                ph[1][2 * u + h] = *reinterpret_cast<const uint32_t *>(lut + ao);
+                pl[1][2 * u + h] = *reinterpret_cast<const uint32_t *>(lut + ao + 4);
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const half8_t ah = as_half8(ph[p][0], ph[p][1], ph[p][2], ph[p][3]);
+            const half8_t al = as_half8(pl[p][0], pl[p][1], pl[p][2], pl[p][3]);
 #pragma unroll
             for (int c = 0; c < NCB; ++c) {
-                oacc[c][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ae, pb[c][u], oacc[c][0], 0, 0, 0);
-                oacc[c][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ao, pb[c][u], oacc[c][1], 0, 0, 0);
+                oacc[c][p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, pb[c], oacc[c][p], 0, 0, 0);
+                oacc[c][p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, pb[c], oacc[c][p], 0, 0, 0);
             }
         }
     };
