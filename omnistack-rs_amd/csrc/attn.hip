@@ -2498,11 +2498,15 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
                 for (int i = 0; i < 4; ++i) sc[4 * u + i] = acc[c][u][i];
             uint32_t dead = 0u;
             if (!full) {
+                // the tile's token, opaque here: the compares stay on this
+                // (rare) path instead of being hoisted into every tile
+                int tb = tt;
+                asm volatile("" : "+s"(tb));
 #pragma unroll
                 for (int u = 0; u < 2; ++u)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const int tn = tt + 16 * u + 4 * g + i;
+                        const int tn = tb + 16 * u + 4 * g + i;
                         if (tn >= s_end || tn > lim[c]) {
                             sc[4 * u + i] = -INFINITY;
                             dead |= 1u << (4 * u + i);
