@@ -2239,7 +2239,7 @@ constexpr int kP32LdsBytes = kP32QsrOff + kP32Waves * 64 * 4;
 struct TileRaw32 {
     uint32_t k[2];     // K dword g of token 16u + (lane % 16)
     uint32_t sg[2];    // the 2 sign bytes of the same token
-    float nr[2];       // norm of token 16u + 4g + lane % 4
+    float4_t nr[2];    // norms of tokens 16u + 4g .. 16u + 4g + 3
     uint32_t v[8];     // V byte (lane % 16) of token 16(i / 4) + 4g + i % 4 (low byte)
 };
 
@@ -2252,8 +2252,8 @@ __device__ __forceinline__ void tile_load32(TileRaw32 &R, const DecBufs &P, int 
         R.k[u] = __builtin_amdgcn_raw_buffer_load_b32(P.kn, tk * 16u + 4u * g, 0, 0);
         if (QJL) {
             R.sg[u] = __builtin_amdgcn_raw_buffer_load_b16(P.kq, tk * 2u, 0, 0);
-            R.nr[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-                P.kr, (t + 16u * u + 4u * g + ((uint32_t)n & 3u)) * 4u, 0, 0));
+            const u32x4_t nv = __builtin_amdgcn_raw_buffer_load_b128(P.kr, (t + 16u * u + 4u * g) * 4u, 0, 0);
+            R.nr[u] = float4_t{__uint_as_float(nv.x), __uint_as_float(nv.y), __uint_as_float(nv.z), __uint_as_float(nv.w)};
         }
     }
 #pragma unroll
@@ -2329,7 +2329,11 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
             const uint16_t x16 = f32_to_f16_rne(xs);
             stage[rr * D + e] = x16;
             if constexpr (QLO) stage[RW * D + rr * D + e] = f32_to_f16_rne(xs - f16_to_f32(x16));
-            if (e == 0) qsr_l[rr] = fabsf(a.qscale) / sr;
+            // kept >= FLT_MIN (a positive scale that underflows here leaves
+            // every score as good as 0 either way): the softmax below
+            // relies on -inf x qsr = -inf.  A zero scale runs elsewhere.
+            const float q0 = fabsf(a.qscale) / sr;
+            if (e == 0) qsr_l[rr] = q0 < __FLT_MIN__ ? __FLT_MIN__ : q0;
         }
     }
     __syncthreads();
@@ -2444,12 +2448,13 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
     float4_t oacc[NCB][2], lacc[NCB];
     // running maximum (scaled, log2 domain) from -FLT_MAX: it serves as the
     // exponent offset as is (the first finite maximum replaces it)
-    float m_run[NCB];
+    float m_run[NCB], m_thr[NCB];     // m_thr = m_run + 8, the rescale threshold
 #pragma unroll
     for (int c = 0; c < NCB; ++c) {
         oacc[c][0] = oacc[c][1] = float4_t{0.f, 0.f, 0.f, 0.f};
         lacc[c] = float4_t{0.f, 0.f, 0.f, 0.f};
         m_run[c] = -__FLT_MAX__;
+        m_thr[c] = -__FLT_MAX__ + 8.0f;
     }
     // exponents are fma(raw, qsr, -m_run): exact products against a rounded
     // maximum, so each carries up to half an ulp of m_run; once any row's
@@ -2481,7 +2486,7 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
                 for (int c = 0; c < NCB; ++c) {
                     const float4_t qacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(s8, bgq[c], float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) acc[c][u][i] = __builtin_fmaf(dpp_quad_bcast(R.nr[u], i), qacc[i], acc[c][u][i]);
+                    for (int i = 0; i < 4; ++i) acc[c][u][i] = __builtin_fmaf(R.nr[u][i], qacc[i], acc[c][u][i]);
                 }
             }
         }
@@ -2496,7 +2501,6 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
             for (int u = 0; u < 2; ++u)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) sc[4 * u + i] = acc[c][u][i];
-            uint32_t dead = 0u;
             if (!full) {
                 // the tile's token, opaque here: the compares stay on this
                 // (rare) path instead of being hoisted into every tile
@@ -2507,26 +2511,25 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int tn = tb + 16 * u + 4 * g + i;
-                        if (tn >= s_end || tn > lim[c]) {
-                            sc[4 * u + i] = -INFINITY;
-                            dead |= 1u << (4 * u + i);
-                        }
+                        if (tn >= s_end || tn > lim[c]) sc[4 * u + i] = -INFINITY;
                     }
             }
             // the scaled maximum of a row is the scale times its raw maximum
-            // (rounding is monotonic and qsr >= 0); m_run is the same in the
-            // four lane groups of a row, so each lane tests its own maximum
-            // and the cross-group maximum is formed only when a lane rescales
+            // (rounding is monotonic and qsr > 0, so a fully masked lane
+            // gives -inf); m_run is the same in the four lane groups of a
+            // row, so each lane tests its own maximum against m_run + 8 and
+            // the cross-group maximum is formed only when a lane rescales
             const float mr = vmax3(vmax3(sc[0], sc[1], sc[2]), vmax3(sc[3], sc[4], sc[5]), vmax2(sc[6], sc[7]));
-            float mt = mr == -INFINITY ? -INFINITY : mr * qsr[c];
-            if (__builtin_amdgcn_ballot_w64(mt > m_run[c] + 8.0f)) {
+            float mt = mr * qsr[c];
+            if (__builtin_amdgcn_ballot_w64(mt > m_thr[c])) {
                 mt = max_over_groups(mt);
-                const bool need = mt > m_run[c] + 8.0f;
+                const bool need = mt > m_thr[c];
                 const float f = need ? __builtin_amdgcn_exp2f(m_run[c] - mt) : 1.0f;
                 oacc[c][0] *= f;
                 oacc[c][1] *= f;
                 lacc[c] *= f;
                 m_run[c] = need ? mt : m_run[c];
+                m_thr[c] = m_run[c] + 8.0f;
                 round_first = round_first ||
                               __builtin_amdgcn_ballot_w64(fabsf(m_run[c]) >= 8192.0f && m_run[c] > -__FLT_MAX__);
             }
@@ -2536,13 +2539,10 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
                 for (int k = 0; k < 8; ++k) sc[k] = sc[k] * qsr[c];
             }
             const float qm = round_first ? 1.0f : qsr[c];
+            // a masked score (-inf) gives -inf here: qm > 0
             float ex[8];
 #pragma unroll
             for (int k = 0; k < 8; ++k) ex[k] = __builtin_fmaf(sc[k], qm, nm);
-            if (!full) {
-#pragma unroll
-                for (int k = 0; k < 8; ++k) ex[k] = (dead >> k) & 1u ? -INFINITY : ex[k];
-            }
             uint32_t pw[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j)
@@ -2644,12 +2644,17 @@ struct Plan {
 
 static int64_t clamp64(int64_t v, int64_t lo, int64_t hi) { return v < lo ? lo : (v > hi ? hi : v); }
 
-static Plan make_plan(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int D, bool q32, bool paged = false) {
+// `zero_scale`: a score scale of exactly 0, which the head_dim-32 prefill
+// kernel leaves to the generic one (its exponents need a positive scale;
+// the generic kernel forms scale x score as the reference does, so an
+// infinite score gives NaN there)
+static Plan make_plan(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int D, bool q32, bool paged = false,
+                      bool zero_scale = false) {
     Plan p;
     const int G = Hq / Hkv;
     const int cus = device_cus();
     p.prefill = (D == 128) && T * G > kPrefillMinRows;
-    p.prefill32 = (D == 32) && T * G > kPrefillMinRows;
+    p.prefill32 = (D == 32) && T * G > kPrefillMinRows && !zero_scale;
     p.dec128 = (D == 128) && !p.prefill;
     p.rows = p.prefill ? kPreWaves * 16 * (q32 ? 1 : kPreNcb)
                        : (p.prefill32 ? kP32Waves * 16 * (q32 ? 2 : kP32Ncb) : (p.dec128 ? kDecRows : kRows));
@@ -2699,6 +2704,14 @@ static Plan make_plan(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int D, b
     return p;
 }
 
+// Split-K workspace of a contiguous-cache call, whatever its score scale
+// (a zero scale may take another kernel).
+static size_t plan_ws_bytes(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int D, bool q32) {
+    const size_t a = make_plan(B, Hq, Hkv, T, S, D, q32).ws_bytes;
+    const size_t b = make_plan(B, Hq, Hkv, T, S, D, q32, false, true).ws_bytes;
+    return a > b ? a : b;
+}
+
 }  // namespace omni
 
 using namespace omni;
@@ -2706,8 +2719,8 @@ using namespace omni;
 extern "C" size_t omni_attn_workspace_size(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int head_dim) {
     if (B <= 0 || Hq <= 0 || Hkv <= 0 || T <= 0 || S <= 0 || Hq % Hkv || !head_dim_ok(head_dim)) return 0;
     // the prefill plan differs for f32 queries: size for either
-    const size_t a = make_plan(B, Hq, Hkv, T, S, head_dim, false).ws_bytes;
-    const size_t b = make_plan(B, Hq, Hkv, T, S, head_dim, true).ws_bytes;
+    const size_t a = plan_ws_bytes(B, Hq, Hkv, T, S, head_dim, false);
+    const size_t b = plan_ws_bytes(B, Hq, Hkv, T, S, head_dim, true);
     return a > b ? a : b;
 }
 
@@ -2756,7 +2769,7 @@ static int attn_run(const void *q, int q_dtype, const uint8_t *k_nib, const uint
     OMNI_CHECK_ARG(S < (int64_t(1) << 25), "omni_attn: S must be < 2^25 tokens per sequence");
     OMNI_CHECK_ARG(T * (Hq / Hkv) < (int64_t(1) << 31), "omni_attn: T * (n_heads / n_kv_heads) must be < 2^31");
     OMNI_CHECK_ARG(seq_index == nullptr || n_seqs >= 1, "omni_attn: a cache index needs a pool of >= 1 sequences");
-    Plan p = make_plan(B, Hq, Hkv, T, S, head_dim, q_dtype == OMNI_F32, paged != nullptr);
+    Plan p = make_plan(B, Hq, Hkv, T, S, head_dim, q_dtype == OMNI_F32, paged != nullptr, scale == 0.0f);
     OMNI_CHECK_ARG(paged == nullptr || head_dim == 128, "omni_attn_paged: needs head_dim 128");
     OMNI_CHECK_ARG(Hkv <= 65535 && ((B + p.spb - 1) / p.spb) * p.n_rchunks <= 65535 && p.splits <= 2147483647,
                    "omni_attn: grid too large (batch x row chunks must be <= 65535)");
@@ -2884,11 +2897,11 @@ extern "C" size_t omni_attn_lora_workspace_size(int64_t B, int Hq, int Hkv, int6
                                                 int q_dtype) {
     if (B <= 0 || Hq <= 0 || Hkv <= 0 || T <= 0 || S <= 0 || Hq % Hkv || !head_dim_ok(head_dim) || !dtype_ok(q_dtype))
         return 0;
-    const Plan p = make_plan(B, Hq, Hkv, T, S, head_dim, q_dtype == OMNI_F32);
+    const size_t ws = plan_ws_bytes(B, Hq, Hkv, T, S, head_dim, q_dtype == OMNI_F32);
     // room for the gather-apply fallback's q_eff: the adapter's rank and
     // hidden size, which decide between it and the fused path, are not
     // arguments here
-    return align256(p.ws_bytes) + (size_t)B * Hq * T * head_dim * (q_dtype == OMNI_F32 ? 4 : 2);
+    return align256(ws) + (size_t)B * Hq * T * head_dim * (q_dtype == OMNI_F32 ? 4 : 2);
 }
 
 extern "C" int omni_attn_lora(const void *q, int q_dtype, const void *x, const void *lora_a, const void *lora_b,

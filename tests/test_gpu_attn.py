@@ -255,10 +255,12 @@ def test_prefill_d32_rotate_q_and_extreme_rows(device):
     _assert_close(got, want, "prefill d32 extreme rows")
 
 
-@pytest.mark.parametrize("scale", [-0.3, 0.0])
+@pytest.mark.parametrize("scale", [-0.3, 0.0, 1e-36])
 def test_prefill_d32_negative_and_zero_scale(device, scale):
     """The head_dim-32 prefill kernel folds the score scale's sign into the
-    query rows; a zero scale is a uniform softmax over the visible keys."""
+    query rows; a zero scale (left to the generic kernel) is a uniform
+    softmax over the visible keys, and so, to within the bar, is a scale so
+    small that the kernel's per-row factor would underflow."""
     B, Hq, Hkv, T, S, uid = 1, 16, 4, 40, 300, 4
     kn, kq, kr, vn, cb, P = _proj32_cache(B, Hkv, S, seed=97, uid=uid)
     q = (_data.query((B, Hq, T, 128), seed=98, dtype=torch.float32) @ P).to(torch.bfloat16)
@@ -267,6 +269,22 @@ def test_prefill_d32_negative_and_zero_scale(device, scale):
     want = restate.fused_attn_python(q.float(), kn, kq, kr, vn, cb, uid, scale, True, mask=_causal_mask(T, S, off))
     assert torch.isfinite(got).all()
     _assert_close(got, want, f"prefill d32 scale {scale}")
+
+
+def test_prefill_d32_zero_scale_infinite_query(device):
+    """Score scale 0 with an infinite query element: the reference forms
+    scale x score, so that row's scores are NaN (inf x 0) and so is its
+    output; every other row is the uniform average."""
+    B, Hq, Hkv, T, S, uid = 1, 16, 4, 40, 300, 4
+    kn, kq, kr, vn, cb, P = _proj32_cache(B, Hkv, S, seed=99, uid=uid)
+    q = (_data.query((B, Hq, T, 128), seed=100, dtype=torch.float32) @ P).to(torch.bfloat16)
+    q[0, 3, 5, 7] = float("inf")
+    got = _run(device, q, kn, kq, kr, vn, cb, uid, scale=0.0)
+    want = restate.fused_attn_python(q.float(), kn, kq, kr, vn, cb, uid, 0.0, True)
+    nan_got, nan_want = torch.isnan(got.cpu()), torch.isnan(want)
+    assert nan_want[0, 3, 5].all() and torch.equal(nan_got, nan_want)
+    keep = ~nan_want
+    _assert_close(got.cpu()[keep], want[keep], "prefill d32 scale 0 with an infinite query")
 
 
 def test_attn_shared_codebook(device):
