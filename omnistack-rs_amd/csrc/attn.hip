@@ -1790,7 +1790,13 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
                 lop[rr * D + lane] = f32_to_f16_rne(los - f16_to_f32(l16));
                 lop[rr * D + 64 + lane] = f32_to_f16_rne(his - f16_to_f32(h16));
             }
-            if (lane == 0) qsr_l[rr] = fabsf(a.qscale) / sr;
+            // a positive factor is kept >= FLT_MIN (one that underflows
+            // leaves every score as good as 0 either way), so a masked
+            // score's -inf stays -inf through the maximum and the exponent;
+            // a zero scale keeps 0 (inf x 0 = NaN, as the reference forms
+            // scale x score) and re-masks the exponents below
+            const float q0 = fabsf(a.qscale) / sr;
+            if (lane == 0) qsr_l[rr] = (q0 < __FLT_MIN__ && a.qscale != 0.0f) ? __FLT_MIN__ : q0;
         }
     }
     __syncthreads();
@@ -1995,14 +2001,16 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
     float4_t oacc[NCB][8], lacc[NCB];
     // running maximum (scaled, log2 domain) from -FLT_MAX: it serves as the
     // exponent offset as is (the first finite maximum replaces it)
-    float m_run[NCB];
+    float m_run[NCB], m_thr[NCB];     // m_thr = m_run + 8, the rescale threshold
 #pragma unroll
     for (int c = 0; c < NCB; ++c) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) oacc[c][k] = float4_t{0.f, 0.f, 0.f, 0.f};
         lacc[c] = float4_t{0.f, 0.f, 0.f, 0.f};
         m_run[c] = -__FLT_MAX__;
+        m_thr[c] = -__FLT_MAX__ + 8.0f;
     }
+    const bool zero_scale = a.qscale == 0.0f;
     // exponents are fma(raw, qsr, -m_run): exact products against a rounded
     // maximum, so each carries up to half an ulp of m_run; once any row's
     // |m_run| reaches 2^13 the wave rounds each logit first (wave-uniform)
@@ -2069,11 +2077,15 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
                 for (int i = 0; i < 4; ++i) sc[4 * u + i] = acc[c][u][i];
             uint32_t dead = 0u;
             if (!full) {
+                // the tile's token, opaque here: the compares stay on this
+                // (rare) path instead of being hoisted into every tile
+                int tb = tt;
+                asm volatile("" : "+s"(tb));
 #pragma unroll
                 for (int u = 0; u < 2; ++u)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const int tn = tt + 16 * u + 4 * g + i;
+                        const int tn = tb + 16 * u + 4 * g + i;
                         if (tn >= s_end || tn > lim[c]) {
                             sc[4 * u + i] = -INFINITY;
                             dead |= 1u << (4 * u + i);
@@ -2081,19 +2093,22 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
                     }
             }
             // the scaled maximum of a row is the scale times its raw maximum
-            // (rounding is monotonic and qsr >= 0); m_run is the same in the
-            // four lane groups of a row, so each lane tests its own maximum
-            // and the cross-group maximum is formed only when a lane rescales
+            // (rounding is monotonic and qsr >= 0; a fully masked lane gives
+            // -inf, or NaN at a zero scale, and neither rescales); m_run is
+            // the same in the four lane groups of a row, so each lane tests
+            // its own maximum against m_run + 8 and the cross-group maximum
+            // is formed only when a lane rescales
             const float mr = vmax3(vmax3(sc[0], sc[1], sc[2]), vmax3(sc[3], sc[4], sc[5]), vmax2(sc[6], sc[7]));
-            float mt = mr == -INFINITY ? -INFINITY : mr * qsr[c];
-            if (__builtin_amdgcn_ballot_w64(mt > m_run[c] + 8.0f)) {
+            float mt = mr * qsr[c];
+            if (__builtin_amdgcn_ballot_w64(mt > m_thr[c])) {
                 mt = max_over_groups(mt);
-                const bool need = mt > m_run[c] + 8.0f;
+                const bool need = mt > m_thr[c];
                 const float f = need ? __builtin_amdgcn_exp2f(m_run[c] - mt) : 1.0f;
 #pragma unroll
                 for (int k = 0; k < 8; ++k) oacc[c][k] *= f;
                 lacc[c] *= f;
                 m_run[c] = need ? mt : m_run[c];
+                m_thr[c] = m_run[c] + 8.0f;
                 round_first = round_first ||
                               __builtin_amdgcn_ballot_w64(fabsf(m_run[c]) >= 8192.0f && m_run[c] > -__FLT_MAX__);
             }
@@ -2106,7 +2121,8 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
             float ex[8];
 #pragma unroll
             for (int k = 0; k < 8; ++k) ex[k] = __builtin_fmaf(sc[k], qm, nm);
-            if (!full) {
+            // -inf x qm is -inf unless the scale is 0
+            if (zero_scale && !full) {
 #pragma unroll
                 for (int k = 0; k < 8; ++k) ex[k] = (dead >> k) & 1u ? -INFINITY : ex[k];
             }

@@ -547,6 +547,26 @@ def test_prefill_extreme_q_no_overflow(device, dtype):
     _assert_close(got, want, f"prefill q x200 {dtype}")
 
 
+@pytest.mark.parametrize("scale", [0.0, 1e-40])
+def test_prefill_zero_and_tiny_scale_causal(device, scale):
+    """The head_dim-128 prefill kernel at a score scale of 0 (a uniform
+    softmax over each row's visible keys; a query with an infinite element
+    gives that row NaN, inf x 0, as the reference's scale x score does) and
+    at a scale whose per-row factor underflows (uniform to within the bar)."""
+    B, Hq, Hkv, T, S, uid = 1, 16, 4, 40, 300, 5
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=31, user_id=uid)
+    q = _data.query((B, Hq, T, 128), seed=32, dtype=torch.float32).to(torch.bfloat16)
+    if scale == 0.0:
+        q[0, 3, 5, 7] = float("inf")
+    off = S - T
+    got = _run(device, q, kn, kq, kr, vn, cb, uid, scale=scale, causal_offset=off).cpu()
+    want = restate.fused_attn_python(q.float(), kn, kq, kr, vn, cb, uid, scale, True, mask=_causal_mask(T, S, off))
+    nan_got, nan_want = torch.isnan(got), torch.isnan(want)
+    assert torch.equal(nan_got, nan_want) and nan_want[0, 3, 5].all() == (scale == 0.0)
+    keep = ~nan_want
+    _assert_close(got[keep], want[keep], f"prefill scale {scale}")
+
+
 def test_prefill_large_and_tiny_query_rows(device):
     """Per-row power-of-two scaling keeps bf16 rows far outside fp16 range exact;
     rows whose logits pass 2^13 (log2 units) switch the exponents to rounded
