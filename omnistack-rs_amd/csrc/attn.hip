@@ -1257,9 +1257,11 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
             const float sr = ldexpf(1.0f, 15 - imax(ex, -100));     // 2^k stays finite for tiny rows
             // the score scale's sign goes into the staged row (exact), so the
             // row's factor |scale| log2(e) / 2^k >= 0 maps raw scores
-            // monotonically.  A factor below 2^-126 (zero included) is raised
-            // to it: raw scores stay below 2^40, so no exponent moves by more
-            // than 2^-86, and a masked key's -inf times the factor stays -inf.
+            // monotonically.  A factor below 2^-126 is raised to it: raw
+            // scores stay below 2^40, so no exponent moves by more than
+            // 2^-86, and a masked key's -inf times the factor stays -inf (a
+            // zero scale, whose inf x 0 = NaN this would hide, runs another
+            // kernel).
             const float ssr = a.qscale < 0.0f ? -sr : sr;
             qs[wave * D + lane] = row_ok ? lo * ssr : 0.0f;
             qs[wave * D + 64 + lane] = row_ok ? hi * ssr : 0.0f;
@@ -1486,13 +1488,14 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
 
         // online softmax (exp2 domain), lazy rescale.  The scaled maximum of
         // the lane's scores is csc times their raw maximum (rounding is
-        // monotonic and csc >= 0), so every exponent below is at most 8 plus
-        // the rounding of one product.  m_run is the same in the four lane
+        // monotonic and csc >= 2^-126, so a fully masked lane gives -inf),
+        // so every exponent below is at most 8 plus the rounding of one
+        // product.  m_run is the same in the four lane
         // groups of a row (it only ever takes a cross-group maximum), so each
         // lane tests its own maximum and the cross-group maximum is formed
         // only when some lane rescales.
         const float mr = vmax3(vmax3(sc[0], sc[1], sc[2]), vmax3(sc[3], sc[4], sc[5]), vmax2(sc[6], sc[7]));
-        float mt = mr == -INFINITY ? -INFINITY : mr * csc;
+        float mt = mr * csc;
         if (__builtin_amdgcn_ballot_w64(mt > m_run + 8.0f)) {
             mt = max_over_groups(mt);
             const bool need = mt > m_run + 8.0f;
@@ -2660,16 +2663,17 @@ struct Plan {
 
 static int64_t clamp64(int64_t v, int64_t lo, int64_t hi) { return v < lo ? lo : (v > hi ? hi : v); }
 
-// `zero_scale`: a score scale of exactly 0, which the head_dim-32 prefill
-// kernel leaves to the generic one (its exponents need a positive scale;
-// the generic kernel forms scale x score as the reference does, so an
-// infinite score gives NaN there)
+// `zero_scale`: a score scale of exactly 0.  The decode and head_dim-32
+// prefill kernels need a positive score factor (a masked key's -inf must
+// stay -inf through it); a zero scale, where an infinite score gives NaN
+// (inf x 0, as the reference forms scale x score), runs the head_dim-128
+// prefill kernel or the generic one instead, which keep the factor 0.
 static Plan make_plan(int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int D, bool q32, bool paged = false,
                       bool zero_scale = false) {
     Plan p;
     const int G = Hq / Hkv;
     const int cus = device_cus();
-    p.prefill = (D == 128) && T * G > kPrefillMinRows;
+    p.prefill = (D == 128) && (T * G > kPrefillMinRows || zero_scale);
     p.prefill32 = (D == 32) && T * G > kPrefillMinRows && !zero_scale;
     p.dec128 = (D == 128) && !p.prefill;
     p.rows = p.prefill ? kPreWaves * 16 * (q32 ? 1 : kPreNcb)
@@ -3002,9 +3006,12 @@ extern "C" size_t omni_attn_paged_workspace_size(int64_t B, int Hq, int Hkv, int
                                                  int page_size, int q_dtype) {
     if (B <= 0 || Hq <= 0 || Hkv <= 0 || T <= 0 || max_pages <= 0 || page_size <= 0 || Hq % Hkv || !dtype_ok(q_dtype))
         return 0;
-    const Plan p = make_plan(B, Hq, Hkv, T, max_pages * (int64_t)page_size, 128, q_dtype == OMNI_F32, true);
-    // plus room for the gather-apply LoRA fallback's q_eff
-    return align256(p.ws_bytes) + (size_t)B * Hq * T * 128 * (q_dtype == OMNI_F32 ? 4 : 2);
+    // either plan (a zero score scale runs another kernel), plus room for
+    // the gather-apply LoRA fallback's q_eff
+    const int64_t S = max_pages * (int64_t)page_size;
+    const size_t a = make_plan(B, Hq, Hkv, T, S, 128, q_dtype == OMNI_F32, true).ws_bytes;
+    const size_t z = make_plan(B, Hq, Hkv, T, S, 128, q_dtype == OMNI_F32, true, true).ws_bytes;
+    return align256(a > z ? a : z) + (size_t)B * Hq * T * 128 * (q_dtype == OMNI_F32 ? 4 : 2);
 }
 
 extern "C" int omni_attn_paged(const void *q, int q_dtype, const uint8_t *k_nib, const uint8_t *k_qjl,

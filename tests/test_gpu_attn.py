@@ -287,6 +287,36 @@ def test_prefill_d32_zero_scale_infinite_query(device):
     _assert_close(got.cpu()[keep], want[keep], "prefill d32 scale 0 with an infinite query")
 
 
+def test_decode_zero_scale_with_infinite_query(device):
+    """Decode-sized calls (at most 32 query rows per kv head) at a score scale
+    of 0: every row is the uniform average of its keys, and a query with an
+    infinite element gives NaN for its row (inf x 0, as the reference's
+    scale x score does), with and without a fused-size adapter bank and
+    through the prepared object (its workspace covers the plan a zero scale
+    takes)."""
+    from omnistack_rs.kernels.fused_attention import PackedKVAttention
+    B, Hq, Hkv, T, S, uid, L = 3, 16, 4, 1, 100, 6, 8
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=51, user_id=uid)
+    q = _data.query((B, Hq, T, 128), seed=52)
+    q[1, 5, 0, 9] = float("inf")
+    got = _run(device, q, kn, kq, kr, vn, cb, uid, scale=0.0, validate=False).cpu()
+    want = restate.fused_attn_python(q.float(), kn, kq, kr, vn, cb, uid, 0.0, True)
+    nan_got, nan_want = torch.isnan(got), torch.isnan(want)
+    assert nan_want[1, 5].all() and torch.equal(nan_got, nan_want)
+    _assert_close(got[~nan_want], want[~nan_want], "decode scale 0")
+    a, bw = _data.lora_bank(L, 8, 96, Hq * 128, seed=53)
+    a, bw = a.to(torch.bfloat16), bw.to(torch.bfloat16)
+    x = torch.randn(B, T, 96, generator=_data.gen(54)).to(torch.bfloat16)
+    ids = _data.lora_ids(B, L)
+    q2 = _data.query((B, Hq, T, 128), seed=55)
+    att = PackedKVAttention(*(t.to(device) for t in (kn, kq, kr, vn, cb)), n_heads=Hq, user_id=uid, scale=0.0,
+                            lora_a=a.to(device), lora_b=bw.to(device), lora_alpha=0.5)
+    got2 = att.run(q2.to(device), x.to(device), ids.to(device)).cpu()
+    q_eff = restate.apply_lora_to_q(q2, x, a, bw, ids, 0.5)
+    want2 = restate.fused_attn_python(q_eff.float(), kn, kq, kr, vn, cb, uid, 0.0, True)
+    _assert_close(got2, want2, "decode scale 0 with adapters")
+
+
 def test_attn_shared_codebook(device):
     kn, kq, kr, vn, cb = _cache(1, 2, 70, seed=24, user_id=0)
     cb1 = cb[0]
