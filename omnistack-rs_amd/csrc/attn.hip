@@ -2467,13 +2467,17 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
     float4_t oacc[NCB][2], lacc[NCB];
     // running maximum (scaled, log2 domain) from -FLT_MAX: it serves as the
     // exponent offset as is (the first finite maximum replaces it)
-    float m_run[NCB], m_thr[NCB];     // m_thr = m_run + 8, the rescale threshold
+    // m_thr: the rescale threshold m_run + 8 in raw score units, (m_run +
+    // 8) / qsr (approximate: it only decides when to rescale; a rescale
+    // missed by a rounding leaves exponents a hair above 8)
+    float m_run[NCB], m_thr[NCB], rqsr[NCB];
 #pragma unroll
     for (int c = 0; c < NCB; ++c) {
         oacc[c][0] = oacc[c][1] = float4_t{0.f, 0.f, 0.f, 0.f};
         lacc[c] = float4_t{0.f, 0.f, 0.f, 0.f};
         m_run[c] = -__FLT_MAX__;
-        m_thr[c] = -__FLT_MAX__ + 8.0f;
+        m_thr[c] = -INFINITY;
+        rqsr[c] = __builtin_amdgcn_rcpf(qsr[c]);
     }
     // exponents are fma(raw, qsr, -m_run): exact products against a rounded
     // maximum, so each carries up to half an ulp of m_run; once any row's
@@ -2536,19 +2540,19 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
             // the scaled maximum of a row is the scale times its raw maximum
             // (rounding is monotonic and qsr > 0, so a fully masked lane
             // gives -inf); m_run is the same in the four lane groups of a
-            // row, so each lane tests its own maximum against m_run + 8 and
-            // the cross-group maximum is formed only when a lane rescales
+            // row, so each lane tests its own raw maximum against the raw
+            // threshold and the cross-group maximum is formed only when a
+            // lane may rescale
             const float mr = vmax3(vmax3(sc[0], sc[1], sc[2]), vmax3(sc[3], sc[4], sc[5]), vmax2(sc[6], sc[7]));
-            float mt = mr * qsr[c];
-            if (__builtin_amdgcn_ballot_w64(mt > m_thr[c])) {
-                mt = max_over_groups(mt);
-                const bool need = mt > m_thr[c];
+            if (__builtin_amdgcn_ballot_w64(mr > m_thr[c])) {
+                const float mt = max_over_groups(mr * qsr[c]);
+                const bool need = mt > m_run[c] + 8.0f;
                 const float f = need ? __builtin_amdgcn_exp2f(m_run[c] - mt) : 1.0f;
                 oacc[c][0] *= f;
                 oacc[c][1] *= f;
                 lacc[c] *= f;
                 m_run[c] = need ? mt : m_run[c];
-                m_thr[c] = m_run[c] + 8.0f;
+                m_thr[c] = (m_run[c] + 8.0f) * rqsr[c];
                 round_first = round_first ||
                               __builtin_amdgcn_ballot_w64(fabsf(m_run[c]) >= 8192.0f && m_run[c] > -__FLT_MAX__);
             }
