@@ -1108,24 +1108,32 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
             ptv[k] = __builtin_amdgcn_raw_buffer_load_b32(PT, h < nh ? 4u * (uint32_t)q : 0x80000000u, 0, 0);
         }
     }
-    // rows of the two 16-token halves of the tile at token t: from the
-    // staged rows when the split's halves fit, else from the page table
-    auto claim_rows = [&](int t, int sq, uint32_t (&rb)[2]) {
+    // rows of the two 16-token halves of the tile at token t, in two steps:
+    // from the staged rows when the split's halves fit (an LDS read, then
+    // its scalar copies), else from the page table (scalar loads, waited for
+    // here, before the next claim is issued, so that wait does not also
+    // wait for the claim's atomic)
+    struct RowReq { uint2 r; uint32_t rb[2]; };
+    auto rows_request = [&](int t, int sq, RowReq &q) {
         if (!kStage || !pt_lds) {
-            // page-table path: the scalar loads are waited for here, before
-            // the next claim is issued, so that wait does not also wait for
-            // the claim's atomic
-            half_rows(t, sq, rb);
-            asm volatile("" ::"s"(rb[0]), "s"(rb[1]));
+            half_rows(t, sq, q.rb);
+            asm volatile("" ::"s"(q.rb[0]), "s"(q.rb[1]));
             __builtin_amdgcn_sched_barrier(0);
             return;
         }
         // claims past the split end (prefetched, never consumed) read the
         // last tile's rows
         const int i = imin((t - s_begin) / kDecTile, tps - 1);
-        const uint2 r = *reinterpret_cast<const uint2 *>(smem + kDecPtOff + 8 * i);
-        rb[0] = __builtin_amdgcn_readfirstlane(r.x);
-        rb[1] = __builtin_amdgcn_readfirstlane(r.y);
+        q.r = *reinterpret_cast<const uint2 *>(smem + kDecPtOff + 8 * i);
+    };
+    auto rows_resolve = [&](const RowReq &q, uint32_t (&rb)[2]) {
+        if (!kStage || !pt_lds) {
+            rb[0] = q.rb[0];
+            rb[1] = q.rb[1];
+            return;
+        }
+        rb[0] = __builtin_amdgcn_readfirstlane(q.r.x);
+        rb[1] = __builtin_amdgcn_readfirstlane(q.r.y);
     };
 
     // ── prologue loads: branch-free buffer loads (an absent input gets a
@@ -1442,7 +1450,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     bool round_first = false;
 
     // One 32-token tile: scores, online softmax, PV.
-    auto tile_step = [&](TileRaw &R, const int tt, const int tseq) {
+    auto tile_step = [&](TileRaw &R, const int tt, const int tseq, auto &&after_k) {
         const bool full = tt + kDecTile <= full_end;
 
         // scores: lane (n, g) holds tokens tt + 16u + 4g + i
@@ -1476,6 +1484,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
                 sc[4 * u + i] = v + __uint_as_float(dpp_row_ror8(__float_as_uint(v)));
             }
         }
+        after_k();
         if (!full) {
 #pragma unroll
             for (int u = 0; u < 2; ++u)
@@ -1577,36 +1586,46 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     int i_cur = wave;
     int c_raw = claim_issue(tile_cnt, lane);
     if (i_cur < ntiles) {
-        tile_step(ring[0], tile_tok(i_cur), tile_seq(i_cur));
+        tile_step(ring[0], tile_tok(i_cur), tile_seq(i_cur), [] {});
         const int i_pre = wave + nw;
         if (i_pre < ntiles && PAGED) {
-            // paged: a claimed tile's pool rows, then the next claim
-            uint32_t rb[2];
-            auto next_rows = [&](int i) { claim_rows(tile_tok(i), tile_seq(i), rb); };
+            // paged: the claimed tile's pool rows are requested before the
+            // current tile's K pass and its loads issued right after it, so
+            // the row read's latency hides behind the K pass
+            RowReq q;
             i_cur = claim_value(c_raw);
-            next_rows(i_cur);
+            rows_request(tile_tok(i_cur), tile_seq(i_cur), q);
             c_raw = claim_issue(tile_cnt, lane);
-            __builtin_amdgcn_sched_barrier(0);
-            tile_load_paged<QJL>(ring[0], P, OFS, rb);
-            __builtin_amdgcn_sched_barrier(0);
-            tile_step(ring[1], tile_tok(i_pre), tile_seq(i_pre));
-            for (;;) {
-                if (i_cur >= ntiles) break;
-                const int i_nxt = claim_value(c_raw);
-                next_rows(i_nxt);
-                c_raw = claim_issue(tile_cnt, lane);
-                __builtin_amdgcn_sched_barrier(0);
-                tile_load_paged<QJL>(ring[1], P, OFS, rb);
-                __builtin_amdgcn_sched_barrier(0);
-                tile_step(ring[0], tile_tok(i_cur), tile_seq(i_cur));
-                if (i_nxt >= ntiles) break;
-                i_cur = claim_value(c_raw);
-                next_rows(i_cur);
-                c_raw = claim_issue(tile_cnt, lane);
+            tile_step(ring[1], tile_tok(i_pre), tile_seq(i_pre), [&] {
+                uint32_t rb[2];
+                rows_resolve(q, rb);
                 __builtin_amdgcn_sched_barrier(0);
                 tile_load_paged<QJL>(ring[0], P, OFS, rb);
                 __builtin_amdgcn_sched_barrier(0);
-                tile_step(ring[1], tile_tok(i_nxt), tile_seq(i_nxt));
+            });
+            for (;;) {
+                if (i_cur >= ntiles) break;
+                const int i_nxt = claim_value(c_raw);
+                rows_request(tile_tok(i_nxt), tile_seq(i_nxt), q);
+                c_raw = claim_issue(tile_cnt, lane);
+                tile_step(ring[0], tile_tok(i_cur), tile_seq(i_cur), [&] {
+                    uint32_t rb[2];
+                    rows_resolve(q, rb);
+                    __builtin_amdgcn_sched_barrier(0);
+                    tile_load_paged<QJL>(ring[1], P, OFS, rb);
+                    __builtin_amdgcn_sched_barrier(0);
+                });
+                if (i_nxt >= ntiles) break;
+                i_cur = claim_value(c_raw);
+                rows_request(tile_tok(i_cur), tile_seq(i_cur), q);
+                c_raw = claim_issue(tile_cnt, lane);
+                tile_step(ring[1], tile_tok(i_nxt), tile_seq(i_nxt), [&] {
+                    uint32_t rb[2];
+                    rows_resolve(q, rb);
+                    __builtin_amdgcn_sched_barrier(0);
+                    tile_load_paged<QJL>(ring[0], P, OFS, rb);
+                    __builtin_amdgcn_sched_barrier(0);
+                });
             }
         } else if (i_pre < ntiles) {
             i_cur = claim_value(c_raw);
@@ -1614,7 +1633,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
             __builtin_amdgcn_sched_barrier(0);
             tile_load<QJL>(ring[0], tile_seq(i_cur) ? P1 : P, OFS, tile_tok(i_cur));
             __builtin_amdgcn_sched_barrier(0);
-            tile_step(ring[1], tile_tok(i_pre), tile_seq(i_pre));
+            tile_step(ring[1], tile_tok(i_pre), tile_seq(i_pre), [] {});
             for (;;) {
                 if (i_cur >= ntiles) break;
                 const int i_nxt = claim_value(c_raw);
@@ -1622,14 +1641,14 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
                 __builtin_amdgcn_sched_barrier(0);
                 tile_load<QJL>(ring[1], tile_seq(i_nxt) ? P1 : P, OFS, tile_tok(i_nxt));
                 __builtin_amdgcn_sched_barrier(0);
-                tile_step(ring[0], tile_tok(i_cur), tile_seq(i_cur));
+                tile_step(ring[0], tile_tok(i_cur), tile_seq(i_cur), [] {});
                 if (i_nxt >= ntiles) break;
                 i_cur = claim_value(c_raw);
                 c_raw = claim_issue(tile_cnt, lane);
                 __builtin_amdgcn_sched_barrier(0);
                 tile_load<QJL>(ring[0], tile_seq(i_cur) ? P1 : P, OFS, tile_tok(i_cur));
                 __builtin_amdgcn_sched_barrier(0);
-                tile_step(ring[1], tile_tok(i_nxt), tile_seq(i_nxt));
+                tile_step(ring[1], tile_tok(i_nxt), tile_seq(i_nxt), [] {});
             }
         }
     }
