@@ -549,10 +549,11 @@ constexpr int kDecLrOff = kDecCntOff + 16;                           // fused Lo
 constexpr int kDecLdsBytes = kDecLrOff + 2 * 16 * 4;
 // Paged cache: the pool row of each 16-token half of the split (half h at
 // kDecPtOff + 4 h, the row of token s_begin + 16 h), staged in the prologue
-// when the split has at most kDecPtMax halves, so a claimed tile's two rows
-// are one 8-byte LDS read away; longer splits (fused LoRA, two sequences per
-// block) read the page table per tile.  Each wave also records whether its
-// staged halves met a page id outside the pool (one word per wave at
+// when the split has at most kDecPtMax halves (the paged plan keeps every
+// split within that), so a claimed tile's two rows are one 8-byte LDS read
+// away; the variants with the fused LoRA prologue or two sequences per block
+// read the page table per tile.  Each wave also records whether its staged
+// halves met a page id outside the pool (one word per wave at
 // kDecPtFlagOff).
 constexpr int kDecPtOff = (kDecLdsBytes + 15) & ~15;
 constexpr int kDecPtMax = 6144;
