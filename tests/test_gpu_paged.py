@@ -63,6 +63,32 @@ def test_paged_ragged_lengths(device, page_size):
         _assert_close(got[sl], want, f"paged ragged ps{page_size} b{b} len{L}")
 
 
+def test_paged_zero_scale_ragged_with_infinite_query(device):
+    """Score scale 0 over pages (ragged lengths): each row is the uniform
+    average of its sequence's keys and a query with an infinite element gives
+    NaN for its row, as the reference's scale x score does; the prepared
+    object's workspace covers the plan a zero scale takes."""
+    from omnistack_rs.cache import PagedKVAttention, paged_attention
+    B, Hq, Hkv, T, S, uid = 4, 16, 4, 1, 200, 9
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=321, user_id=uid)
+    q = _data.query((B, Hq, T, 128), seed=322)
+    q[2, 7, 0, 3] = float("-inf")
+    lens = [200, 1, 77, 130]
+    cache, pt, lt = _paged(device, kn, kq, kr, vn, 16, lens=lens, seed=8)
+    got = paged_attention(q.to(device), cache, pt, lt, cb.to(device), user_id=uid, scale=0.0).cpu()
+    att = PagedKVAttention(cache, cb.to(device), n_heads=Hq, batch=B, max_pages=pt.shape[1], user_id=uid, scale=0.0)
+    got2 = att.run(q.to(device), pt, lt).cpu()
+    for b, L in enumerate(lens):
+        sl = slice(b, b + 1)
+        want = restate.fused_attn_python(q[sl].float(), kn[sl, :, :L], kq[sl, :, :L], kr[sl, :, :L],
+                                         vn[sl, :, :L], cb, uid, 0.0, True)
+        for g_, tag in ((got, "paged_attention"), (got2, "PagedKVAttention")):
+            nan_got, nan_want = torch.isnan(g_[sl]), torch.isnan(want)
+            assert torch.equal(nan_got, nan_want), f"{tag} b{b}: NaN pattern"
+            _assert_close(g_[sl][~nan_want], want[~nan_want], f"paged scale 0 {tag} b{b} len{L}")
+    assert torch.isnan(got[2, 7]).all()
+
+
 def test_paged_long_sequence_split_k(device):
     """One sequence of 6000 tokens over 2 kv heads: many splits per
     (sequence, kv head), each reading its own run of pages, merged by the
