@@ -254,9 +254,10 @@ int omni_attn(const void *q, int q_dtype,
  *   q_eff[b] = dtype(q[b] + ((x[b] A[idx[b]]^T) B[idx[b]]^T) * lora_alpha)
  * (idx < 0: q unchanged; idx >= n_loras: NaN rows), then attention on q_eff
  * exactly as omni_attn.  LoRA shapes and dtypes as omni_lora_apply.  At
- * head_dim 128 with <= 32 query rows per kv head and a 16-bit adapter of
- * rank 8 or 16, hidden <= 256 and a 16-byte aligned lora_b, the update runs inside the attention
- * kernel's prologue (one launch); otherwise the gather-apply kernel writes
+ * head_dim 128 with <= 32 query rows per kv head, a nonzero score scale and
+ * a 16-bit adapter of rank 8 or 16, hidden <= 256 and a 16-byte aligned
+ * lora_b, the update runs inside the attention kernel's prologue (one
+ * launch); otherwise the gather-apply kernel writes
  * q_eff into the workspace tail first.  q_eff is rounded
  * exactly as omni_lora_apply rounds it.  `workspace` must hold
  * omni_attn_lora_workspace_size(...) bytes.
