@@ -329,6 +329,36 @@ int omni_attn_serve(const void *q, int q_dtype, const int64_t *cache_index, int6
                     float *out, void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * Prepared attention: replaces the reference serving loop's per-step
+ * omni_attn call (scripts/run_criteo_benchmark.py:684), whose cache,
+ * codebooks, adapters and shapes stay fixed from step to step.
+ * omni_attn_plan_create stores those static arguments (the pointers are
+ * kept, not copied: the buffers must outlive the plan); omni_attn_plan_run
+ * then takes only what changes per step and is exactly
+ *   n_cache_seqs > 0:        omni_attn_serve(q, ..., cache_index, ..., x, ..., lora_idx, ...)
+ *   lora_a != NULL:          omni_attn_lora(q, ..., x, ..., lora_idx, ...)   (cache_index must be NULL)
+ *   otherwise:               omni_attn(q, ...)                               (x, lora_idx, cache_index NULL)
+ * with the stored arguments, including every argument check.  A plan is
+ * read-only once created (runs on several threads or streams may share it,
+ * but not its `out` and `workspace`); omni_attn_plan_destroy frees it.
+ */
+typedef struct omni_attn_plan omni_attn_plan;
+int omni_attn_plan_create(int q_dtype, int64_t n_cache_seqs,
+                          const void *lora_a, const void *lora_b, int w_dtype,
+                          int hidden, int rank, int n_loras, float lora_alpha,
+                          const uint8_t *k_nib, const uint8_t *k_qjl, const float *k_norms,
+                          const uint8_t *v_nib, const float *codebooks, int per_head_codebook,
+                          const uint32_t *g_bits,
+                          int64_t B, int Hq, int Hkv, int64_t T, int64_t S, int head_dim,
+                          float scale, int with_qjl, int64_t causal_offset,
+                          int rotate_q, const int8_t *sign_flip,
+                          float *out, void *workspace, size_t workspace_bytes,
+                          omni_attn_plan **plan);
+int omni_attn_plan_run(const omni_attn_plan *plan, const void *q, const void *x, const int32_t *lora_idx,
+                       const int64_t *cache_index, void *stream);
+void omni_attn_plan_destroy(omni_attn_plan *plan);
+
+/*
  * The serving step over a page-granular cache.  The reference plans a paged
  * KV cache (MANIFEST.md:211-215; page_size = 16 tokens, config.py:43) but
  * gathers whole sequences instead (scripts/run_criteo_benchmark.py:553-557);

@@ -27,6 +27,7 @@
 
 #include <atomic>
 #include <mutex>
+#include <new>
 #include <type_traits>
 
 #include "omni_common.h"
@@ -3138,3 +3139,86 @@ extern "C" int omni_attn_noalloc(const void *q, int q_dtype, const uint8_t *k_ni
                     S, head_dim, scale, with_qjl, causal_offset, rotate_q, sign_flip, out, ws, kScratchBytes,
                     stream, nullptr, nullptr, 0);
 }
+
+// ── prepared calls (omni_attn_plan_*) ──────────────────────────────────
+//
+// The static arguments of one attention configuration, stored once, so a
+// serving loop's per-step call passes only what changes (q, the LoRA inputs,
+// the cache index, the stream).  A run is exactly the omni_attn /
+// omni_attn_lora / omni_attn_serve call the stored arguments describe.
+struct omni_attn_plan {
+    int q_dtype;
+    int64_t n_cache_seqs;                 // > 0: a pool indexed per query (omni_attn_serve)
+    const void *lora_a, *lora_b;          // lora_a NULL: no adapters
+    int w_dtype, hidden, rank, n_loras;
+    float lora_alpha;
+    const uint8_t *k_nib, *k_qjl;
+    const float *k_norms;
+    const uint8_t *v_nib;
+    const float *codebooks;
+    int per_head_codebook;
+    const uint32_t *g_bits;
+    int64_t B;
+    int Hq, Hkv;
+    int64_t T, S;
+    int head_dim;
+    float scale;
+    int with_qjl;
+    int64_t causal_offset;
+    int rotate_q;
+    const int8_t *sign_flip;
+    float *out;
+    void *workspace;
+    size_t workspace_bytes;
+};
+
+extern "C" int omni_attn_plan_create(int q_dtype, int64_t n_cache_seqs, const void *lora_a, const void *lora_b,
+                                     int w_dtype, int hidden, int rank, int n_loras, float lora_alpha,
+                                     const uint8_t *k_nib, const uint8_t *k_qjl, const float *k_norms,
+                                     const uint8_t *v_nib, const float *codebooks, int per_head_codebook,
+                                     const uint32_t *g_bits, int64_t B, int Hq, int Hkv, int64_t T, int64_t S,
+                                     int head_dim, float scale, int with_qjl, int64_t causal_offset, int rotate_q,
+                                     const int8_t *sign_flip, float *out, void *workspace, size_t workspace_bytes,
+                                     omni_attn_plan **plan) {
+    OMNI_CHECK_ARG(plan != nullptr, "omni_attn_plan_create: NULL plan pointer");
+    *plan = nullptr;
+    OMNI_CHECK_ARG(dtype_ok(q_dtype), "omni_attn_plan_create: bad q dtype %d", q_dtype);
+    OMNI_CHECK_ARG(head_dim_ok(head_dim), "omni_attn_plan_create: head_dim must be 128 or 32, got %d", head_dim);
+    OMNI_CHECK_ARG(n_cache_seqs >= 0, "omni_attn_plan_create: n_cache_seqs must be >= 0");
+    OMNI_CHECK_ARG(lora_a == nullptr || dtype_ok(w_dtype), "omni_attn_plan_create: bad LoRA dtype %d", w_dtype);
+    omni_attn_plan *p = new (std::nothrow) omni_attn_plan;
+    if (p == nullptr) {
+        set_error("omni_attn_plan_create: out of host memory");
+        return OMNI_ERUNTIME;
+    }
+    *p = omni_attn_plan{q_dtype, n_cache_seqs, lora_a, lora_b, w_dtype, hidden, rank, n_loras, lora_alpha,
+                        k_nib, k_qjl, k_norms, v_nib, codebooks, per_head_codebook, g_bits, B, Hq, Hkv, T, S,
+                        head_dim, scale, with_qjl, causal_offset, rotate_q, sign_flip, out, workspace,
+                        workspace_bytes};
+    *plan = p;
+    return OMNI_OK;
+}
+
+extern "C" int omni_attn_plan_run(const omni_attn_plan *p, const void *q, const void *x, const int32_t *lora_idx,
+                                  const int64_t *cache_index, void *stream) {
+    OMNI_CHECK_ARG(p != nullptr, "omni_attn_plan_run: NULL plan");
+    if (p->n_cache_seqs > 0)
+        return omni_attn_serve(q, p->q_dtype, cache_index, p->n_cache_seqs, x, p->lora_a, p->lora_b, p->w_dtype,
+                               lora_idx, p->hidden, p->rank, p->n_loras, p->lora_alpha, p->k_nib, p->k_qjl,
+                               p->k_norms, p->v_nib, p->codebooks, p->per_head_codebook, p->g_bits, p->B, p->Hq,
+                               p->Hkv, p->T, p->S, p->head_dim, p->scale, p->with_qjl, p->causal_offset,
+                               p->rotate_q, p->sign_flip, p->out, p->workspace, p->workspace_bytes, stream);
+    OMNI_CHECK_ARG(cache_index == nullptr, "omni_attn_plan_run: a cache index needs a plan over a pool");
+    if (p->lora_a != nullptr)
+        return omni_attn_lora(q, p->q_dtype, x, p->lora_a, p->lora_b, p->w_dtype, lora_idx, p->hidden, p->rank,
+                              p->n_loras, p->lora_alpha, p->k_nib, p->k_qjl, p->k_norms, p->v_nib, p->codebooks,
+                              p->per_head_codebook, p->g_bits, p->B, p->Hq, p->Hkv, p->T, p->S, p->head_dim,
+                              p->scale, p->with_qjl, p->causal_offset, p->rotate_q, p->sign_flip, p->out,
+                              p->workspace, p->workspace_bytes, stream);
+    OMNI_CHECK_ARG(x == nullptr && lora_idx == nullptr, "omni_attn_plan_run: LoRA inputs need a plan with a bank");
+    return omni_attn(q, p->q_dtype, p->k_nib, p->k_qjl, p->k_norms, p->v_nib, p->codebooks, p->per_head_codebook,
+                     p->g_bits, p->B, p->Hq, p->Hkv, p->T, p->S, p->head_dim, p->scale, p->with_qjl,
+                     p->causal_offset, p->rotate_q, p->sign_flip, p->out, p->workspace, p->workspace_bytes, stream);
+}
+
+extern "C" void omni_attn_plan_destroy(omni_attn_plan *p) { delete p; }

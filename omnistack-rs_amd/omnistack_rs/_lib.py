@@ -60,6 +60,13 @@ SIGNATURES = {
                                  _vp, _vp, _vp, _vp, _vp, _c_int, _vp,
                                  _c_i64, _c_int, _c_int, _c_i64, _c_i64, _c_int,
                                  _c_f32, _c_int, _c_i64, _c_int, _vp, _vp, _vp, _c_sz, _vp]),
+    "omni_attn_plan_create": (_c_int, [_c_int, _c_i64, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_f32,
+                                       _vp, _vp, _vp, _vp, _vp, _c_int, _vp,
+                                       _c_i64, _c_int, _c_int, _c_i64, _c_i64, _c_int,
+                                       _c_f32, _c_int, _c_i64, _c_int, _vp, _vp, _vp, _c_sz,
+                                       ctypes.POINTER(_vp)]),
+    "omni_attn_plan_run": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp]),
+    "omni_attn_plan_destroy": (None, [_vp]),
     "omni_attn_paged_workspace_size": (_c_sz, [_c_i64, _c_int, _c_int, _c_i64, _c_i64, _c_int, _c_int]),
     "omni_attn_paged": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _vp, _c_i64, _c_int, _vp, _c_i64, _vp,
                                  _vp, _vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_f32,

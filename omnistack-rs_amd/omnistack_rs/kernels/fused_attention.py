@@ -29,6 +29,7 @@ path).
 """
 from __future__ import annotations
 
+import ctypes
 import math
 from typing import Optional
 
@@ -297,9 +298,17 @@ class PackedKVAttention:
             self.ws_bytes = L.omni_attn_workspace_size(B, n_heads, Hkv, q_tokens, S, D)
         self.ws = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device=dev)
         self._ws = (_lib.ptr(self.ws), self.ws_bytes)
-        self._fn = L.omni_attn
-        self._lora_fn = L.omni_attn_lora if self.lora is not None else None
-        self._serve_fn = L.omni_attn_serve if self.pool is not None else None
+        # the static arguments stored once in a native plan: run() passes only
+        # q, the LoRA inputs, the cache index and the stream
+        lora_static = ((*self._lora_head[:2], self._lora_head[2], *self._lora_mid) if self.lora is not None
+                       else (None, None, 0, 0, 0, 0, 0.0))
+        plan = ctypes.c_void_p()
+        _lib.check(L.omni_attn_plan_create(self._qcode, 0 if self.pool is None else N, *lora_static, *self._tail,
+                                           *self._ws, ctypes.byref(plan)))
+        self._plan = plan
+        self._run_fn = L.omni_attn_plan_run
+        self._destroy = L.omni_attn_plan_destroy
+        self._fn, self._serve_fn = L.omni_attn, L.omni_attn_serve      # runs without the bank's inputs
 
     def run(self, q: torch.Tensor, x: Optional[torch.Tensor] = None,
             lora_indices: Optional[torch.Tensor] = None,
@@ -316,8 +325,7 @@ class PackedKVAttention:
             raise ValueError(f"q, x, lora_indices and cache_index must be on {dev}")
         B, Hq, T, D = self.shape
         stream = _lib.stream_of(self.device)
-        qp = q.data_ptr()
-        lora_args = None
+        xp = ip = cp = None
         if x is not None:
             if self.lora is None:
                 raise ValueError("run(q, x, ...) needs a LoRA bank at construction")
@@ -327,22 +335,29 @@ class PackedKVAttention:
             if (lora_indices is None or lora_indices.dtype != torch.int32 or lora_indices.numel() != B
                     or not lora_indices.is_contiguous()):
                 raise ValueError(f"lora_indices must be a contiguous int32 tensor of {B} entries")
-            la, lb, wcode = self._lora_head
-            lora_args = (x.data_ptr(), la, lb, wcode, lora_indices.data_ptr(), *self._lora_mid)
+            xp, ip = x.data_ptr(), lora_indices.data_ptr()
         if self.pool is not None:
             if (cache_index is None or cache_index.dtype != torch.int64 or cache_index.numel() != B
                     or not cache_index.is_contiguous()):
                 raise ValueError(f"cache_index must be a contiguous int64 tensor of {B} entries")
-            if lora_args is None:
-                lora_args = (None, None, None, 0, None, 0, 0, 0, 0.0)
-            rc = self._serve_fn(qp, self._qcode, cache_index.data_ptr(), self.pool, *lora_args, *self._tail,
-                                *self._ws, stream)
+            cp = cache_index.data_ptr()
         elif cache_index is not None:
             raise ValueError("run(..., cache_index=...) needs batch= at construction")
-        elif lora_args is not None:
-            rc = self._lora_fn(qp, self._qcode, *lora_args, *self._tail, *self._ws, stream)
+        if x is None and self.lora is not None:
+            # a bank was given but no adapter inputs this step: plain attention
+            if cp is not None:
+                rc = self._serve_fn(q.data_ptr(), self._qcode, cp, self.pool, None, None, None, 0, None, 0, 0, 0,
+                                    0.0, *self._tail, *self._ws, stream)
+            else:
+                rc = self._fn(q.data_ptr(), self._qcode, *self._tail, *self._ws, stream)
         else:
-            rc = self._fn(qp, self._qcode, *self._tail, *self._ws, stream)
+            rc = self._run_fn(self._plan, q.data_ptr(), xp, ip, cp, stream)
         if rc:
             _lib.check(rc)
         return self.out
+
+    def __del__(self):
+        plan = getattr(self, "_plan", None)
+        if plan is not None and plan.value:
+            self._destroy(plan)
+            self._plan = None

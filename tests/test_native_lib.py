@@ -408,3 +408,26 @@ def test_prepared_paged_attention_run_refusals():
     pool = PagedKVCache(4, 2, page_size=16, device="cpu")
     with pytest.raises(RuntimeError):
         PagedKVAttention(pool, torch.zeros(16), n_heads=4, batch=1, max_pages=2)
+
+
+def test_attn_plan_create_checks_and_lifetime(L):
+    """omni_attn_plan_create refuses a bad q dtype, head_dim or LoRA dtype
+    and a NULL result pointer (no device work: host-only checks); a valid
+    plan is created and destroyed; a run of a NULL plan is refused."""
+    import ctypes
+    from omnistack_rs import _lib
+
+    def create(qd=2, D=128, lora_a=None, wd=2, out=True):
+        plan = ctypes.c_void_p()
+        rc = L.omni_attn_plan_create(qd, 0, lora_a, None, wd, 96, 8, 4, 1.0, None, None, None, None, None, 1,
+                                     None, 2, 8, 2, 1, 64, D, 0.1, 1, -1, 0, None, None, None, 0,
+                                     ctypes.byref(plan) if out else None)
+        return rc, plan
+    for kw in (dict(qd=7), dict(D=64), dict(lora_a=1, wd=9), dict(out=False)):
+        rc, _ = create(**kw)
+        assert rc == _lib.OMNI_EINVAL, kw
+    rc, plan = create()
+    assert rc == _lib.OMNI_OK and plan.value
+    L.omni_attn_plan_destroy(plan)
+    assert L.omni_attn_plan_run(None, None, None, None, None, None) == _lib.OMNI_EINVAL
+    assert "NULL plan" in _lib.last_error()
