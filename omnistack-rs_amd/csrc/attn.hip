@@ -2025,23 +2025,31 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
     float4_t oacc[NCB][8], lacc[NCB];
     // running maximum (scaled, log2 domain) from -FLT_MAX: it serves as the
     // exponent offset as is (the first finite maximum replaces it)
-    float m_run[NCB], m_thr[NCB];     // m_thr = m_run + 8, the rescale threshold
+    // m_thr: the rescale threshold m_run + 8 in raw score units, (m_run + 8)
+    // / qsr (approximate: it only decides when to rescale; a rescale missed
+    // by a rounding leaves exponents a hair above 8; at a zero scale it is
+    // -inf until the first rescale, then +inf)
+    float m_run[NCB], m_thr[NCB], rqsr[NCB], qmul[NCB];
 #pragma unroll
     for (int c = 0; c < NCB; ++c) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) oacc[c][k] = float4_t{0.f, 0.f, 0.f, 0.f};
         lacc[c] = float4_t{0.f, 0.f, 0.f, 0.f};
         m_run[c] = -__FLT_MAX__;
-        m_thr[c] = -__FLT_MAX__ + 8.0f;
+        m_thr[c] = -INFINITY;
+        rqsr[c] = __builtin_amdgcn_rcpf(qsr[c]);
+        qmul[c] = qsr[c];
     }
-    const bool zero_scale = a.qscale == 0.0f;
-    // exponents are fma(raw, qsr, -m_run): exact products against a rounded
-    // maximum, so each carries up to half an ulp of m_run; once any row's
-    // |m_run| reaches 2^13 the wave rounds each logit first (wave-uniform)
-    bool round_first = false;
+    const int zero_scale = __builtin_amdgcn_readfirstlane(a.qscale == 0.0f ? 1 : 0);
+    // exponents are fma(raw, qmul, -m_run) with qmul = qsr: exact products
+    // against a rounded maximum, so each carries up to half an ulp of m_run;
+    // once any row's |m_run| reaches 2^13 the wave rounds each logit first
+    // and qmul becomes 1 (wave-uniform; an int, so it stays a scalar)
+    int round_first = 0;
 
     auto tile_step = [&](TileRaw &R, const int tt) {
-        const bool full = tt + kDecTile <= full_end;
+        // wave-uniform flags as ints (scalar compares, no lane masks)
+        const int full = __builtin_amdgcn_readfirstlane(tt + kDecTile <= full_end ? 1 : 0);
         float4_t acc[NCB][2];
 #pragma unroll
         for (int c = 0; c < NCB; ++c)
@@ -2099,8 +2107,12 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
             for (int u = 0; u < 2; ++u)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) sc[4 * u + i] = acc[c][u][i];
-            uint32_t dead = 0u;
-            if (!full) {
+            // the flag copied through a scalar register per column block, so
+            // each test is a scalar compare rather than a lane mask kept
+            // across the blocks
+            int fu = full;
+            asm volatile("" : "+s"(fu));
+            if (fu == 0) {
                 // the tile's token, opaque here: the compares stay on this
                 // (rare) path instead of being hoisted into every tile
                 int tb = tt;
@@ -2110,45 +2122,54 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int tn = tb + 16 * u + 4 * g + i;
-                        if (tn >= s_end || tn > lim[c]) {
-                            sc[4 * u + i] = -INFINITY;
-                            dead |= 1u << (4 * u + i);
-                        }
+                        if (tn >= s_end || tn > lim[c]) sc[4 * u + i] = -INFINITY;
                     }
             }
             // the scaled maximum of a row is the scale times its raw maximum
             // (rounding is monotonic and qsr >= 0; a fully masked lane gives
             // -inf, or NaN at a zero scale, and neither rescales); m_run is
             // the same in the four lane groups of a row, so each lane tests
-            // its own maximum against m_run + 8 and the cross-group maximum
-            // is formed only when a lane rescales
+            // its own raw maximum against the raw threshold and the
+            // cross-group maximum is formed only when a lane may rescale
             const float mr = vmax3(vmax3(sc[0], sc[1], sc[2]), vmax3(sc[3], sc[4], sc[5]), vmax2(sc[6], sc[7]));
-            float mt = mr * qsr[c];
-            if (__builtin_amdgcn_ballot_w64(mt > m_thr[c])) {
-                mt = max_over_groups(mt);
-                const bool need = mt > m_thr[c];
+            if (__builtin_amdgcn_ballot_w64(mr > m_thr[c])) {
+                const float mt = max_over_groups(mr * qsr[c]);
+                const bool need = mt > m_run[c] + 8.0f;
                 const float f = need ? __builtin_amdgcn_exp2f(m_run[c] - mt) : 1.0f;
+                // the old maximum's last use before the new one is formed
+                // (one register for both: no copy on the path without a rescale)
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int k = 0; k < 8; ++k) oacc[c][k] *= f;
                 lacc[c] *= f;
                 m_run[c] = need ? mt : m_run[c];
-                m_thr[c] = m_run[c] + 8.0f;
-                round_first = round_first ||
-                              __builtin_amdgcn_ballot_w64(fabsf(m_run[c]) >= 8192.0f && m_run[c] > -__FLT_MAX__);
+                m_thr[c] = (m_run[c] + 8.0f) * rqsr[c];
+                round_first |= __builtin_amdgcn_ballot_w64(fabsf(m_run[c]) >= 8192.0f && m_run[c] > -__FLT_MAX__) ? 1 : 0;
+#pragma unroll
+                for (int k = 0; k < NCB; ++k) qmul[k] = round_first ? 1.0f : qmul[k];
             }
             const float nm = -m_run[c];
             if (round_first) {
 #pragma unroll
                 for (int k = 0; k < 8; ++k) sc[k] = sc[k] * qsr[c];
             }
-            const float qm = round_first ? 1.0f : qsr[c];
             float ex[8];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) ex[k] = __builtin_fmaf(sc[k], qm, nm);
-            // -inf x qm is -inf unless the scale is 0
-            if (zero_scale && !full) {
+            for (int k = 0; k < 8; ++k) ex[k] = __builtin_fmaf(sc[k], qmul[c], nm);
+            // -inf x qmul is -inf unless the scale is 0: then the masked
+            // keys' exponents are set again (their tokens tested as above)
+            int zr = zero_scale & (full ^ 1);
+            asm volatile("" : "+s"(zr));
+            if (zr != 0) {
+                int tb = tt;
+                asm volatile("" : "+s"(tb));
 #pragma unroll
-                for (int k = 0; k < 8; ++k) ex[k] = (dead >> k) & 1u ? -INFINITY : ex[k];
+                for (int u = 0; u < 2; ++u)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int tn = tb + 16 * u + 4 * g + i;
+                        if (tn >= s_end || tn > lim[c]) ex[4 * u + i] = -INFINITY;
+                    }
             }
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
@@ -2500,13 +2521,18 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
         m_thr[c] = -INFINITY;
         rqsr[c] = __builtin_amdgcn_rcpf(qsr[c]);
     }
-    // exponents are fma(raw, qsr, -m_run): exact products against a rounded
-    // maximum, so each carries up to half an ulp of m_run; once any row's
-    // |m_run| reaches 2^13 the wave rounds each logit first (wave-uniform)
-    bool round_first = false;
+    // exponents are fma(raw, qmul, -m_run) with qmul = qsr: exact products
+    // against a rounded maximum, so each carries up to half an ulp of m_run;
+    // once any row's |m_run| reaches 2^13 the wave rounds each logit first
+    // and qmul becomes 1 (wave-uniform; an int, so it stays a scalar)
+    int round_first = 0;
+    float qmul[NCB];
+#pragma unroll
+    for (int c = 0; c < NCB; ++c) qmul[c] = qsr[c];
 
     auto tile_step = [&](TileRaw32 &R, const int tt) {
-        const bool full = tt + kDecTile <= full_end;
+        // wave-uniform as an int (a scalar compare per use, no lane mask)
+        const int full = __builtin_amdgcn_readfirstlane(tt + kDecTile <= full_end ? 1 : 0);
         float4_t acc[NCB][2];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
@@ -2534,6 +2560,37 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
                 }
             }
         }
+        // PV operands, read before the softmax so that each column block's
+        // PV runs on the matrix cores while the next one's softmax runs:
+        // pair bytes of tokens (4g, 4g + 1) and (4g + 2, 4g + 3) of each
+        // half at dims 2n (low nibbles) and 2n + 1 (high nibbles); a LUT
+        // entry is (fp16 hi pair, remainder pair), read as two dwords so the
+        // hi and remainder planes are two A operands over the same P
+        uint32_t ph[2][4], pl[2][4];      // [dim parity][pair byte]
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const uint32_t b0 = R.v[4 * u], b1 = R.v[4 * u + 1], b2 = R.v[4 * u + 2], b3 = R.v[4 * u + 3];
+            const uint32_t pe[2] = {__builtin_amdgcn_ubfe(b0, 0, 4) | ((b1 & 0x0Fu) << 4),
+                                    __builtin_amdgcn_ubfe(b2, 0, 4) | ((b3 & 0x0Fu) << 4)};
+            const uint32_t po[2] = {(b0 >> 4) | (b1 & 0xF0u), (b2 >> 4) | (b3 & 0xF0u)};
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t ae = lut_addr(pe[h], laneoff, 0), ao = lut_addr(po[h], laneoff, 0);
+                // the remainder dwords read as volatile, so that they are not
+                // merged with the hi dwords into paired reads (whose results
+                // would need register copies to form the two A operands)
+                ph[0][2 * u + h] = *reinterpret_cast<const uint32_t *>(lut + ae);
+                pl[0][2 * u + h] = *(const volatile __attribute__((address_space(3))) uint32_t *)(lut + ae + 4);
+                ph[1][2 * u + h] = *reinterpret_cast<const uint32_t *>(lut + ao);
+                pl[1][2 * u + h] = *(const volatile __attribute__((address_space(3))) uint32_t *)(lut + ao + 4);
+            }
+        }
+        half8_t ahv[2], alv[2];
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            ahv[p] = as_half8(ph[p][0], ph[p][1], ph[p][2], ph[p][3]);
+            alv[p] = as_half8(pl[p][0], pl[p][1], pl[p][2], pl[p][3]);
+        }
         // P of the lane's eight tokens (4g .. 4g + 3 of each half) as one
         // B operand: k slot 8g + j holds token 16 (j / 4) + 4g + j % 4
         half8_t pb[NCB];
@@ -2545,7 +2602,12 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
             for (int u = 0; u < 2; ++u)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) sc[4 * u + i] = acc[c][u][i];
-            if (!full) {
+            // the flag copied through a scalar register per column block, so
+            // each test is a scalar compare rather than a lane mask kept
+            // across the blocks
+            int fu = full;
+            asm volatile("" : "+s"(fu));
+            if (fu == 0) {
                 // the tile's token, opaque here: the compares stay on this
                 // (rare) path instead of being hoisted into every tile
                 int tb = tt;
@@ -2569,59 +2631,37 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
                 const float mt = max_over_groups(mr * qsr[c]);
                 const bool need = mt > m_run[c] + 8.0f;
                 const float f = need ? __builtin_amdgcn_exp2f(m_run[c] - mt) : 1.0f;
+                // the old maximum's last use before the new one is formed
+                // (one register for both: no copy on the path without a rescale)
+                __builtin_amdgcn_sched_barrier(0);
                 oacc[c][0] *= f;
                 oacc[c][1] *= f;
                 lacc[c] *= f;
                 m_run[c] = need ? mt : m_run[c];
                 m_thr[c] = (m_run[c] + 8.0f) * rqsr[c];
-                round_first = round_first ||
-                              __builtin_amdgcn_ballot_w64(fabsf(m_run[c]) >= 8192.0f && m_run[c] > -__FLT_MAX__);
+                round_first |= __builtin_amdgcn_ballot_w64(fabsf(m_run[c]) >= 8192.0f && m_run[c] > -__FLT_MAX__) ? 1 : 0;
+#pragma unroll
+                for (int k = 0; k < NCB; ++k) qmul[k] = round_first ? 1.0f : qmul[k];
             }
             const float nm = -m_run[c];
             if (round_first) {
 #pragma unroll
                 for (int k = 0; k < 8; ++k) sc[k] = sc[k] * qsr[c];
             }
-            const float qm = round_first ? 1.0f : qsr[c];
-            // a masked score (-inf) gives -inf here: qm > 0
+            // a masked score (-inf) gives -inf here: qmul > 0
             float ex[8];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) ex[k] = __builtin_fmaf(sc[k], qm, nm);
+            for (int k = 0; k < 8; ++k) ex[k] = __builtin_fmaf(sc[k], qmul[c], nm);
             uint32_t pw[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 pw[j] = cvt_pk_h2(__builtin_amdgcn_exp2f(ex[2 * j]), __builtin_amdgcn_exp2f(ex[2 * j + 1]));
             pb[c] = as_half8(pw[0], pw[1], pw[2], pw[3]);
             lacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb[c], lacc[c], 0, 0, 0);
-        }
-        // PV: pair bytes of tokens (4g, 4g + 1) and (4g + 2, 4g + 3) of each
-        // half at dims 2n (low nibbles) and 2n + 1 (high nibbles); a LUT
-        // entry is (fp16 hi pair, remainder pair), read as two dwords so the
-        // hi and remainder planes are two A operands over the same P
-        uint32_t ph[2][4], pl[2][4];      // [dim parity][pair byte]
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const uint32_t b0 = R.v[4 * u], b1 = R.v[4 * u + 1], b2 = R.v[4 * u + 2], b3 = R.v[4 * u + 3];
-            const uint32_t pe[2] = {__builtin_amdgcn_ubfe(b0, 0, 4) | ((b1 & 0x0Fu) << 4),
-                                    __builtin_amdgcn_ubfe(b2, 0, 4) | ((b3 & 0x0Fu) << 4)};
-            const uint32_t po[2] = {(b0 >> 4) | (b1 & 0xF0u), (b2 >> 4) | (b3 & 0xF0u)};
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const uint32_t ae = lut_addr(pe[h], laneoff, 0), ao = lut_addr(po[h], laneoff, 0);
-                ph[0][2 * u + h] = *reinterpret_cast<const uint32_t *>(lut + ae);
-                pl[0][2 * u + h] = *reinterpret_cast<const uint32_t *>(lut + ae + 4);
-                ph[1][2 * u + h] = *reinterpret_cast<const uint32_t *>(lut + ao);
-                pl[1][2 * u + h] = *reinterpret_cast<const uint32_t *>(lut + ao + 4);
-            }
-        }
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            const half8_t ah = as_half8(ph[p][0], ph[p][1], ph[p][2], ph[p][3]);
-            const half8_t al = as_half8(pl[p][0], pl[p][1], pl[p][2], pl[p][3]);
-#pragma unroll
-            for (int c = 0; c < NCB; ++c) {
-                oacc[c][p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, pb[c], oacc[c][p], 0, 0, 0);
-                oacc[c][p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, pb[c], oacc[c][p], 0, 0, 0);
+            for (int p = 0; p < 2; ++p) {
+                oacc[c][p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahv[p], pb[c], oacc[c][p], 0, 0, 0);
+                oacc[c][p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alv[p], pb[c], oacc[c][p], 0, 0, 0);
             }
         }
     };
