@@ -2098,87 +2098,103 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
                 }
             }
         }
+        // raw scores of both column blocks first (the row scale qsr >= 0
+        // enters each exponent's fma); one rescale branch for both, then the
+        // exponentials and denominator MFMAs of both as one straight run
         half8_t pb[NCB][2];
+        float sc[NCB][8];
 #pragma unroll
-        for (int c = 0; c < NCB; ++c) {
-            // raw scores; the row scale qsr >= 0 enters each exponent's fma
-            float sc[8];
+        for (int c = 0; c < NCB; ++c)
 #pragma unroll
             for (int u = 0; u < 2; ++u)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) sc[4 * u + i] = acc[c][u][i];
-            // the flag copied through a scalar register per column block, so
-            // each test is a scalar compare rather than a lane mask kept
-            // across the blocks
-            int fu = full;
-            asm volatile("" : "+s"(fu));
-            if (fu == 0) {
-                // the tile's token, opaque here: the compares stay on this
-                // (rare) path instead of being hoisted into every tile
-                int tb = tt;
-                asm volatile("" : "+s"(tb));
+                for (int i = 0; i < 4; ++i) sc[c][4 * u + i] = acc[c][u][i];
+        if (full == 0) {
+            // the tile's token, opaque here: the compares stay on this
+            // (rare) path instead of being hoisted into every tile
+            int tb = tt;
+            asm volatile("" : "+s"(tb));
+#pragma unroll
+            for (int c = 0; c < NCB; ++c)
 #pragma unroll
                 for (int u = 0; u < 2; ++u)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int tn = tb + 16 * u + 4 * g + i;
-                        if (tn >= s_end || tn > lim[c]) sc[4 * u + i] = -INFINITY;
+                        if (tn >= s_end || tn > lim[c]) sc[c][4 * u + i] = -INFINITY;
                     }
+        }
+        // the scaled maximum of a row is the scale times its raw maximum
+        // (rounding is monotonic and qsr >= 0; a fully masked lane gives
+        // -inf, or NaN at a zero scale, and neither rescales); m_run is the
+        // same in the four lane groups of a row, so each lane tests its own
+        // raw maximum against the raw threshold and the cross-group maximum
+        // is formed only when a lane may rescale
+        float mr[NCB];
+        bool may = false;
+#pragma unroll
+        for (int c = 0; c < NCB; ++c) {
+            mr[c] = vmax3(vmax3(sc[c][0], sc[c][1], sc[c][2]), vmax3(sc[c][3], sc[c][4], sc[c][5]), vmax2(sc[c][6], sc[c][7]));
+            may = may || mr[c] > m_thr[c];
+        }
+        if (__builtin_amdgcn_ballot_w64(may)) {
+#pragma unroll
+            for (int c = 0; c < NCB; ++c) {
+                if (__builtin_amdgcn_ballot_w64(mr[c] > m_thr[c])) {
+                    const float mt = max_over_groups(mr[c] * qsr[c]);
+                    const bool need = mt > m_run[c] + 8.0f;
+                    const float f = need ? __builtin_amdgcn_exp2f(m_run[c] - mt) : 1.0f;
+                    // the old maximum's last use before the new one is formed
+                    // (one register for both: no copy on the path without a rescale)
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) oacc[c][k] *= f;
+                    lacc[c] *= f;
+                    m_run[c] = need ? mt : m_run[c];
+                    m_thr[c] = (m_run[c] + 8.0f) * rqsr[c];
+                    round_first |= __builtin_amdgcn_ballot_w64(fabsf(m_run[c]) >= 8192.0f && m_run[c] > -__FLT_MAX__) ? 1 : 0;
+                }
             }
-            // the scaled maximum of a row is the scale times its raw maximum
-            // (rounding is monotonic and qsr >= 0; a fully masked lane gives
-            // -inf, or NaN at a zero scale, and neither rescales); m_run is
-            // the same in the four lane groups of a row, so each lane tests
-            // its own raw maximum against the raw threshold and the
-            // cross-group maximum is formed only when a lane may rescale
-            const float mr = vmax3(vmax3(sc[0], sc[1], sc[2]), vmax3(sc[3], sc[4], sc[5]), vmax2(sc[6], sc[7]));
-            if (__builtin_amdgcn_ballot_w64(mr > m_thr[c])) {
-                const float mt = max_over_groups(mr * qsr[c]);
-                const bool need = mt > m_run[c] + 8.0f;
-                const float f = need ? __builtin_amdgcn_exp2f(m_run[c] - mt) : 1.0f;
-                // the old maximum's last use before the new one is formed
-                // (one register for both: no copy on the path without a rescale)
-                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int k = 0; k < 8; ++k) oacc[c][k] *= f;
-                lacc[c] *= f;
-                m_run[c] = need ? mt : m_run[c];
-                m_thr[c] = (m_run[c] + 8.0f) * rqsr[c];
-                round_first |= __builtin_amdgcn_ballot_w64(fabsf(m_run[c]) >= 8192.0f && m_run[c] > -__FLT_MAX__) ? 1 : 0;
+            for (int k = 0; k < NCB; ++k) qmul[k] = round_first ? 1.0f : qmul[k];
+        }
+        if (round_first) {
 #pragma unroll
-                for (int k = 0; k < NCB; ++k) qmul[k] = round_first ? 1.0f : qmul[k];
-            }
-            const float nm = -m_run[c];
-            if (round_first) {
+            for (int c = 0; c < NCB; ++c)
 #pragma unroll
-                for (int k = 0; k < 8; ++k) sc[k] = sc[k] * qsr[c];
-            }
-            float ex[8];
+                for (int k = 0; k < 8; ++k) sc[c][k] = sc[c][k] * qsr[c];
+        }
+        float ex[NCB][8];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) ex[k] = __builtin_fmaf(sc[k], qmul[c], nm);
-            // -inf x qmul is -inf unless the scale is 0: then the masked
-            // keys' exponents are set again (their tokens tested as above)
-            int zr = zero_scale & (full ^ 1);
-            asm volatile("" : "+s"(zr));
-            if (zr != 0) {
-                int tb = tt;
-                asm volatile("" : "+s"(tb));
+        for (int c = 0; c < NCB; ++c)
+#pragma unroll
+            for (int k = 0; k < 8; ++k) ex[c][k] = __builtin_fmaf(sc[c][k], qmul[c], -m_run[c]);
+        // -inf x qmul is -inf unless the scale is 0: then the masked keys'
+        // exponents are set again (their tokens tested as above)
+        int zr = zero_scale & (full ^ 1);
+        asm volatile("" : "+s"(zr));
+        if (zr != 0) {
+            int tb = tt;
+            asm volatile("" : "+s"(tb));
+#pragma unroll
+            for (int c = 0; c < NCB; ++c)
 #pragma unroll
                 for (int u = 0; u < 2; ++u)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int tn = tb + 16 * u + 4 * g + i;
-                        if (tn >= s_end || tn > lim[c]) ex[4 * u + i] = -INFINITY;
+                        if (tn >= s_end || tn > lim[c]) ex[c][4 * u + i] = -INFINITY;
                     }
-            }
+        }
+#pragma unroll
+        for (int c = 0; c < NCB; ++c)
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
-                const uint32_t p01 = cvt_pk_h2(__builtin_amdgcn_exp2f(ex[4 * u]), __builtin_amdgcn_exp2f(ex[4 * u + 1]));
-                const uint32_t p23 = cvt_pk_h2(__builtin_amdgcn_exp2f(ex[4 * u + 2]), __builtin_amdgcn_exp2f(ex[4 * u + 3]));
+                const uint32_t p01 = cvt_pk_h2(__builtin_amdgcn_exp2f(ex[c][4 * u]), __builtin_amdgcn_exp2f(ex[c][4 * u + 1]));
+                const uint32_t p23 = cvt_pk_h2(__builtin_amdgcn_exp2f(ex[c][4 * u + 2]), __builtin_amdgcn_exp2f(ex[c][4 * u + 3]));
                 pb[c][u] = as_half8(p01, p01, p23, p23);
                 lacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb[c][u], lacc[c], 0, 0, 0);
             }
-        }
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             uint32_t ev[2], od[2];
@@ -2592,76 +2608,88 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
             alv[p] = as_half8(pl[p][0], pl[p][1], pl[p][2], pl[p][3]);
         }
         // P of the lane's eight tokens (4g .. 4g + 3 of each half) as one
-        // B operand: k slot 8g + j holds token 16 (j / 4) + 4g + j % 4
-        half8_t pb[NCB];
+        // B operand: k slot 8g + j holds token 16 (j / 4) + 4g + j % 4.
+        // Raw scores of every column block first (the row scale qsr >= 0
+        // enters each exponent's fma); one rescale branch for all blocks,
+        // then the exponentials and MFMAs of all blocks as one straight run.
+        float sc[NCB][8];
 #pragma unroll
-        for (int c = 0; c < NCB; ++c) {
-            // raw scores; the row scale qsr >= 0 enters each exponent's fma
-            float sc[8];
+        for (int c = 0; c < NCB; ++c)
 #pragma unroll
             for (int u = 0; u < 2; ++u)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) sc[4 * u + i] = acc[c][u][i];
-            // the flag copied through a scalar register per column block, so
-            // each test is a scalar compare rather than a lane mask kept
-            // across the blocks
-            int fu = full;
-            asm volatile("" : "+s"(fu));
-            if (fu == 0) {
-                // the tile's token, opaque here: the compares stay on this
-                // (rare) path instead of being hoisted into every tile
-                int tb = tt;
-                asm volatile("" : "+s"(tb));
+                for (int i = 0; i < 4; ++i) sc[c][4 * u + i] = acc[c][u][i];
+        if (full == 0) {
+            // the tile's token, opaque here: the compares stay on this
+            // (rare) path instead of being hoisted into every tile
+            int tb = tt;
+            asm volatile("" : "+s"(tb));
+#pragma unroll
+            for (int c = 0; c < NCB; ++c)
 #pragma unroll
                 for (int u = 0; u < 2; ++u)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int tn = tb + 16 * u + 4 * g + i;
-                        if (tn >= s_end || tn > lim[c]) sc[4 * u + i] = -INFINITY;
+                        if (tn >= s_end || tn > lim[c]) sc[c][4 * u + i] = -INFINITY;
                     }
-            }
-            // the scaled maximum of a row is the scale times its raw maximum
-            // (rounding is monotonic and qsr > 0, so a fully masked lane
-            // gives -inf); m_run is the same in the four lane groups of a
-            // row, so each lane tests its own raw maximum against the raw
-            // threshold and the cross-group maximum is formed only when a
-            // lane may rescale
-            const float mr = vmax3(vmax3(sc[0], sc[1], sc[2]), vmax3(sc[3], sc[4], sc[5]), vmax2(sc[6], sc[7]));
-            if (__builtin_amdgcn_ballot_w64(mr > m_thr[c])) {
-                const float mt = max_over_groups(mr * qsr[c]);
-                const bool need = mt > m_run[c] + 8.0f;
-                const float f = need ? __builtin_amdgcn_exp2f(m_run[c] - mt) : 1.0f;
-                // the old maximum's last use before the new one is formed
-                // (one register for both: no copy on the path without a rescale)
-                __builtin_amdgcn_sched_barrier(0);
-                oacc[c][0] *= f;
-                oacc[c][1] *= f;
-                lacc[c] *= f;
-                m_run[c] = need ? mt : m_run[c];
-                m_thr[c] = (m_run[c] + 8.0f) * rqsr[c];
-                round_first |= __builtin_amdgcn_ballot_w64(fabsf(m_run[c]) >= 8192.0f && m_run[c] > -__FLT_MAX__) ? 1 : 0;
+        }
+        // the scaled maximum of a row is the scale times its raw maximum
+        // (rounding is monotonic and qsr > 0, so a fully masked lane gives
+        // -inf); m_run is the same in the four lane groups of a row, so each
+        // lane tests its own raw maximum against the raw threshold and the
+        // cross-group maximum is formed only when a lane may rescale
+        float mr[NCB];
+        bool may = false;
 #pragma unroll
-                for (int k = 0; k < NCB; ++k) qmul[k] = round_first ? 1.0f : qmul[k];
-            }
-            const float nm = -m_run[c];
-            if (round_first) {
+        for (int c = 0; c < NCB; ++c) {
+            mr[c] = vmax3(vmax3(sc[c][0], sc[c][1], sc[c][2]), vmax3(sc[c][3], sc[c][4], sc[c][5]), vmax2(sc[c][6], sc[c][7]));
+            may = may || mr[c] > m_thr[c];
+        }
+        if (__builtin_amdgcn_ballot_w64(may)) {
 #pragma unroll
-                for (int k = 0; k < 8; ++k) sc[k] = sc[k] * qsr[c];
+            for (int c = 0; c < NCB; ++c) {
+                if (__builtin_amdgcn_ballot_w64(mr[c] > m_thr[c])) {
+                    const float mt = max_over_groups(mr[c] * qsr[c]);
+                    const bool need = mt > m_run[c] + 8.0f;
+                    const float f = need ? __builtin_amdgcn_exp2f(m_run[c] - mt) : 1.0f;
+                    // the old maximum's last use before the new one is formed
+                    // (one register for both: no copy on the path without a rescale)
+                    __builtin_amdgcn_sched_barrier(0);
+                    oacc[c][0] *= f;
+                    oacc[c][1] *= f;
+                    lacc[c] *= f;
+                    m_run[c] = need ? mt : m_run[c];
+                    m_thr[c] = (m_run[c] + 8.0f) * rqsr[c];
+                    round_first |= __builtin_amdgcn_ballot_w64(fabsf(m_run[c]) >= 8192.0f && m_run[c] > -__FLT_MAX__) ? 1 : 0;
+                }
             }
+#pragma unroll
+            for (int k = 0; k < NCB; ++k) qmul[k] = round_first ? 1.0f : qmul[k];
+        }
+        if (round_first) {
+#pragma unroll
+            for (int c = 0; c < NCB; ++c)
+#pragma unroll
+                for (int k = 0; k < 8; ++k) sc[c][k] = sc[c][k] * qsr[c];
+        }
+#pragma unroll
+        for (int c = 0; c < NCB; ++c) {
             // a masked score (-inf) gives -inf here: qmul > 0
+            const float nm = -m_run[c];
             float ex[8];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) ex[k] = __builtin_fmaf(sc[k], qmul[c], nm);
+            for (int k = 0; k < 8; ++k) ex[k] = __builtin_fmaf(sc[c][k], qmul[c], nm);
             uint32_t pw[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 pw[j] = cvt_pk_h2(__builtin_amdgcn_exp2f(ex[2 * j]), __builtin_amdgcn_exp2f(ex[2 * j + 1]));
-            pb[c] = as_half8(pw[0], pw[1], pw[2], pw[3]);
-            lacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb[c], lacc[c], 0, 0, 0);
+            const half8_t pb = as_half8(pw[0], pw[1], pw[2], pw[3]);
+            lacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb, lacc[c], 0, 0, 0);
 #pragma unroll
             for (int p = 0; p < 2; ++p) {
-                oacc[c][p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahv[p], pb[c], oacc[c][p], 0, 0, 0);
-                oacc[c][p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alv[p], pb[c], oacc[c][p], 0, 0, 0);
+                oacc[c][p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahv[p], pb, oacc[c][p], 0, 0, 0);
+                oacc[c][p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alv[p], pb, oacc[c][p], 0, 0, 0);
             }
         }
     };
