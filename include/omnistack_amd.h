@@ -390,6 +390,32 @@ int omni_attn_paged(const void *q, int q_dtype,
                     float *out, void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * Prepared paged attention: the paged form of omni_attn_plan, for the same
+ * per-step call of the reference serving loop (scripts/run_criteo_benchmark.py:684)
+ * over the page pool above.  omni_attn_paged_plan_create stores the
+ * arguments that stay fixed (pool, geometry, code tables, LoRA bank, shapes,
+ * out, workspace; pointers kept, not copied: the buffers must outlive the
+ * plan); omni_attn_paged_plan_run(plan, q, page_table, seq_lens, x, lora_idx,
+ * stream) is exactly omni_attn_paged with them, including every argument
+ * check (x and lora_idx must be NULL for a plan without a bank).  Read-only
+ * once created; omni_attn_paged_plan_destroy frees it.
+ */
+typedef struct omni_attn_paged_plan omni_attn_paged_plan;
+int omni_attn_paged_plan_create(int q_dtype,
+                                const uint8_t *k_nib, const uint8_t *k_qjl, const float *k_norms,
+                                const uint8_t *v_nib, int64_t n_pages, int page_size, int64_t max_pages,
+                                const void *lora_a, const void *lora_b, int w_dtype,
+                                int hidden, int rank, int n_loras, float lora_alpha,
+                                const float *codebooks, int per_head_codebook, const uint32_t *g_bits,
+                                int64_t B, int Hq, int Hkv, int64_t T, int head_dim,
+                                float scale, int with_qjl, int causal, int rotate_q, const int8_t *sign_flip,
+                                float *out, void *workspace, size_t workspace_bytes,
+                                omni_attn_paged_plan **plan);
+int omni_attn_paged_plan_run(const omni_attn_paged_plan *plan, const void *q, const int32_t *page_table,
+                             const int32_t *seq_lens, const void *x, const int32_t *lora_idx, void *stream);
+void omni_attn_paged_plan_destroy(omni_attn_paged_plan *plan);
+
+/*
  * Measurement helper with no counterpart in the reference: streams `bytes`
  * (a multiple of 16, 16-byte aligned device buffer) once with n_partials
  * blocks and writes one XOR fold per block to partials[0 .. n_partials),

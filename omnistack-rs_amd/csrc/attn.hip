@@ -3290,3 +3290,81 @@ extern "C" int omni_attn_plan_run(const omni_attn_plan *p, const void *q, const 
 }
 
 extern "C" void omni_attn_plan_destroy(omni_attn_plan *p) { delete p; }
+
+// ── prepared paged call (PagedKVAttention) ───────────────────────────────
+//
+// The arguments of omni_attn_paged that stay fixed across a serving loop (the
+// pool, its geometry, the code tables, the LoRA bank, the shapes, output and
+// workspace) stored once, so each call passes the query, the page table,
+// the lengths, the LoRA inputs and the stream.  The plan holds pointers only:
+// the pool and every buffer it names must outlive it.
+struct omni_attn_paged_plan {
+    int q_dtype;
+    const uint8_t *k_nib, *k_qjl;
+    const float *k_norms;
+    const uint8_t *v_nib;
+    int64_t n_pages;
+    int page_size;
+    int64_t max_pages;
+    const void *lora_a, *lora_b;          // lora_a NULL: no adapters
+    int w_dtype, hidden, rank, n_loras;
+    float lora_alpha;
+    const float *codebooks;
+    int per_head_codebook;
+    const uint32_t *g_bits;
+    int64_t B;
+    int Hq, Hkv;
+    int64_t T;
+    int head_dim;
+    float scale;
+    int with_qjl, causal, rotate_q;
+    const int8_t *sign_flip;
+    float *out;
+    void *workspace;
+    size_t workspace_bytes;
+};
+
+extern "C" int omni_attn_paged_plan_create(int q_dtype, const uint8_t *k_nib, const uint8_t *k_qjl,
+                                           const float *k_norms, const uint8_t *v_nib, int64_t n_pages,
+                                           int page_size, int64_t max_pages, const void *lora_a, const void *lora_b,
+                                           int w_dtype, int hidden, int rank, int n_loras, float lora_alpha,
+                                           const float *codebooks, int per_head_codebook, const uint32_t *g_bits,
+                                           int64_t B, int Hq, int Hkv, int64_t T, int head_dim, float scale,
+                                           int with_qjl, int causal, int rotate_q, const int8_t *sign_flip,
+                                           float *out, void *workspace, size_t workspace_bytes,
+                                           omni_attn_paged_plan **plan) {
+    OMNI_CHECK_ARG(plan != nullptr, "omni_attn_paged_plan_create: NULL plan pointer");
+    *plan = nullptr;
+    OMNI_CHECK_ARG(dtype_ok(q_dtype), "omni_attn_paged_plan_create: bad q dtype %d", q_dtype);
+    OMNI_CHECK_ARG(head_dim_ok(head_dim), "omni_attn_paged_plan_create: head_dim must be 128 or 32, got %d", head_dim);
+    int shift = 0;
+    if (!paged_args_ok(B, Hkv, n_pages, page_size, max_pages, shift)) return OMNI_EINVAL;
+    OMNI_CHECK_ARG(lora_a == nullptr || dtype_ok(w_dtype), "omni_attn_paged_plan_create: bad LoRA dtype %d", w_dtype);
+    omni_attn_paged_plan *p = new (std::nothrow) omni_attn_paged_plan;
+    if (p == nullptr) {
+        set_error("omni_attn_paged_plan_create: out of host memory");
+        return OMNI_ERUNTIME;
+    }
+    *p = omni_attn_paged_plan{q_dtype, k_nib, k_qjl, k_norms, v_nib, n_pages, page_size, max_pages, lora_a, lora_b,
+                              w_dtype, hidden, rank, n_loras, lora_alpha, codebooks, per_head_codebook, g_bits, B,
+                              Hq, Hkv, T, head_dim, scale, with_qjl, causal, rotate_q, sign_flip, out, workspace,
+                              workspace_bytes};
+    *plan = p;
+    return OMNI_OK;
+}
+
+extern "C" int omni_attn_paged_plan_run(const omni_attn_paged_plan *p, const void *q, const int32_t *page_table,
+                                        const int32_t *seq_lens, const void *x, const int32_t *lora_idx,
+                                        void *stream) {
+    OMNI_CHECK_ARG(p != nullptr, "omni_attn_paged_plan_run: NULL plan");
+    if (p->lora_a == nullptr)
+        OMNI_CHECK_ARG(x == nullptr && lora_idx == nullptr, "omni_attn_paged_plan_run: LoRA inputs need a plan with a bank");
+    return omni_attn_paged(q, p->q_dtype, p->k_nib, p->k_qjl, p->k_norms, p->v_nib, p->n_pages, p->page_size,
+                           page_table, p->max_pages, seq_lens, p->lora_a ? x : nullptr, p->lora_a, p->lora_b,
+                           p->w_dtype, p->lora_a ? lora_idx : nullptr, p->hidden, p->rank, p->n_loras,
+                           p->lora_alpha, p->codebooks, p->per_head_codebook, p->g_bits, p->B, p->Hq, p->Hkv, p->T,
+                           p->head_dim, p->scale, p->with_qjl, p->causal, p->rotate_q, p->sign_flip, p->out,
+                           p->workspace, p->workspace_bytes, stream);
+}
+
+extern "C" void omni_attn_paged_plan_destroy(omni_attn_paged_plan *p) { delete p; }

@@ -72,6 +72,13 @@ SIGNATURES = {
                                  _vp, _vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_f32,
                                  _vp, _c_int, _vp, _c_i64, _c_int, _c_int, _c_i64, _c_int,
                                  _c_f32, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_sz, _vp]),
+    "omni_attn_paged_plan_create": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _c_i64, _c_int, _c_i64,
+                                             _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_f32,
+                                             _vp, _c_int, _vp, _c_i64, _c_int, _c_int, _c_i64, _c_int,
+                                             _c_f32, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_sz,
+                                             ctypes.POINTER(_vp)]),
+    "omni_attn_paged_plan_run": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "omni_attn_paged_plan_destroy": (None, [_vp]),
     "omni_hbm_read_probe": (_c_int, [_vp, _c_sz, _vp, _c_int, _vp]),
     "omni_attn_noalloc_scratch_bytes": (_c_sz, []),
     "omni_attn_noalloc": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _vp, _vp, _c_int, _vp,

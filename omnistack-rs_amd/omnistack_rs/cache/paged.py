@@ -21,6 +21,7 @@ its page in place, with the same arithmetic as the contiguous ``omni_attn``
 """
 from __future__ import annotations
 
+import ctypes
 import math
 from typing import Optional, Sequence
 
@@ -366,6 +367,23 @@ class PagedKVAttention:
         self.ws_bytes = L.omni_attn_paged_workspace_size(self.B, n_heads, H, self.T, self.max_pages,
                                                          cache.page_size, self.qcode)
         self.ws = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device=dev)
+        # the static arguments stored once in a native plan: run() passes only
+        # q, the page table, the lengths, the LoRA inputs and the stream
+        if self.lora is not None:
+            la, lb, wcode, _, hidden, rank, n_loras, alpha = self.lora
+            lora_static = (_lib.ptr(la), _lib.ptr(lb), wcode, hidden, rank, n_loras, alpha)
+        else:
+            lora_static = (None, None, 0, 0, 0, 0, 0.0)
+        plan = ctypes.c_void_p()
+        _lib.check(L.omni_attn_paged_plan_create(
+            self.qcode, _lib.ptr(cache.k_nibbles), _lib.ptr(cache.k_qjl if with_qjl else None),
+            _lib.ptr(cache.k_norms if with_qjl else None), _lib.ptr(cache.v_nibbles), cache.n_pages,
+            cache.page_size, self.max_pages, *lora_static, _lib.ptr(self.cb), self.per_head, _lib.ptr(self.gb),
+            self.B, self.Hq, H, self.T, D, self.scale, self.with_qjl, self.causal, self.rotate_q,
+            _lib.ptr(self.sf), _lib.ptr(self.out), _lib.ptr(self.ws), self.ws_bytes, ctypes.byref(plan)))
+        self._plan = plan
+        self._run_fn = L.omni_attn_paged_plan_run
+        self._destroy = L.omni_attn_paged_plan_destroy
 
     def run(self, q: torch.Tensor, page_table: torch.Tensor, seq_lens: torch.Tensor,
             x: Optional[torch.Tensor] = None, lora_indices: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -374,17 +392,16 @@ class PagedKVAttention:
         _check_paged_run(q, page_table, seq_lens, x, lora_indices, (self.B, self.Hq, self.T, c.head_dim),
                          self.q_dtype, self.max_pages, self.lora[4] if self.lora is not None else None,
                          self.lora[3] if self.lora is not None else None, dev)
-        if self.lora is not None:
-            la, lb, wcode, wdt, hidden, rank, n_loras, alpha = self.lora
-            lora = (_lib.ptr(x), _lib.ptr(la), _lib.ptr(lb), wcode, _lib.ptr(lora_indices),
-                    hidden, rank, n_loras, alpha)
-        else:
-            lora = (None, None, None, 0, None, 0, 0, 0, 0.0)
-        _lib.check(_lib.lib().omni_attn_paged(
-            _lib.ptr(q), self.qcode, _lib.ptr(c.k_nibbles), _lib.ptr(c.k_qjl if self.with_qjl else None),
-            _lib.ptr(c.k_norms if self.with_qjl else None), _lib.ptr(c.v_nibbles), c.n_pages, c.page_size,
-            _lib.ptr(page_table), self.max_pages, _lib.ptr(seq_lens), *lora,
-            _lib.ptr(self.cb), self.per_head, _lib.ptr(self.gb), self.B, self.Hq, c.n_kv_heads, self.T,
-            c.head_dim, self.scale, self.with_qjl, self.causal, self.rotate_q, _lib.ptr(self.sf),
-            _lib.ptr(self.out), _lib.ptr(self.ws), self.ws_bytes, _lib.stream_of(dev)))
+        xp = x.data_ptr() if x is not None else None
+        ip = lora_indices.data_ptr() if lora_indices is not None else None
+        rc = self._run_fn(self._plan, q.data_ptr(), page_table.data_ptr(), seq_lens.data_ptr(), xp, ip,
+                          _lib.stream_of(dev))
+        if rc:
+            _lib.check(rc)
         return self.out
+
+    def __del__(self):
+        plan = getattr(self, "_plan", None)
+        if plan is not None and plan.value:
+            self._destroy(plan)
+            self._plan = None

@@ -431,3 +431,32 @@ def test_attn_plan_create_checks_and_lifetime(L):
     L.omni_attn_plan_destroy(plan)
     assert L.omni_attn_plan_run(None, None, None, None, None, None) == _lib.OMNI_EINVAL
     assert "NULL plan" in _lib.last_error()
+
+
+def test_attn_paged_plan_create_checks_and_lifetime(L):
+    """omni_attn_paged_plan_create refuses a bad q dtype, head_dim, page
+    size, empty pool, LoRA dtype and a NULL result pointer (host-only
+    checks, no device work); a valid plan is created and destroyed; a run
+    of a NULL plan and LoRA inputs for a plan without a bank are refused
+    before any launch."""
+    import ctypes
+    from omnistack_rs import _lib
+
+    def create(qd=2, D=128, page_size=16, n_pages=64, lora_a=None, wd=2, out=True):
+        plan = ctypes.c_void_p()
+        rc = L.omni_attn_paged_plan_create(qd, None, None, None, None, n_pages, page_size, 8, lora_a, None, wd,
+                                           96, 8, 4, 1.0, None, 1, None, 2, 8, 2, 1, D, 0.1, 1, 0, 0, None,
+                                           None, None, 0, ctypes.byref(plan) if out else None)
+        return rc, plan
+    for kw in (dict(qd=7), dict(D=64), dict(page_size=24), dict(page_size=8), dict(n_pages=0),
+               dict(lora_a=1, wd=9), dict(out=False)):
+        rc, _ = create(**kw)
+        assert rc == _lib.OMNI_EINVAL, kw
+    rc, plan = create()
+    assert rc == _lib.OMNI_OK and plan.value
+    # LoRA inputs for a plan without a bank: refused on the host
+    assert L.omni_attn_paged_plan_run(plan, None, None, None, 1, None, None) == _lib.OMNI_EINVAL
+    assert "need a plan with a bank" in _lib.last_error()
+    L.omni_attn_paged_plan_destroy(plan)
+    assert L.omni_attn_paged_plan_run(None, None, None, None, None, None, None) == _lib.OMNI_EINVAL
+    assert "NULL plan" in _lib.last_error()
