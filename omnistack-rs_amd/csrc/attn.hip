@@ -2577,8 +2577,8 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
             }
         }
         // PV operands, read before the softmax so that each column block's
-        // PV runs on the matrix cores while the next one's softmax runs:
-        // pair bytes of tokens (4g, 4g + 1) and (4g + 2, 4g + 3) of each
+        // PV MFMAs can issue as soon as its probabilities exist (interleaved
+        // with the other blocks' exponentials below): pair bytes of tokens (4g, 4g + 1) and (4g + 2, 4g + 3) of each
         // half at dims 2n (low nibbles) and 2n + 1 (high nibbles); a LUT
         // entry is (fp16 hi pair, remainder pair), read as two dwords so the
         // hi and remainder planes are two A operands over the same P
