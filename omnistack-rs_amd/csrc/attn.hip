@@ -2057,9 +2057,6 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
             for (int u = 0; u < 2; ++u) acc[c][u] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            float4_t qacc[NCB];
-#pragma unroll
-            for (int c = 0; c < NCB; ++c) qacc[c] = float4_t{0.f, 0.f, 0.f, 0.f};
             const uint32_t kw[4] = {R.k[u].x, R.k[u].y, R.k[u].z, R.k[u].w};
 #pragma unroll
             for (int s = 0; s < 8; ++s) {
@@ -2072,31 +2069,41 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
                     if constexpr (QLO) acc[c][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak, bkl[c][s], acc[c][u], 0, 0, 0);
                 }
             }
-            if (QJL) {
-                // signs . (G q as fp16 hi + fp16 remainder), then + norm * that
-                // (norm of token 4g + i: a quad broadcast, fp32); the B images
-                // are read from the stage area (the opaque offset keeps the
-                // reads in the loop)
-                uint32_t qo = qimg_off;
-                asm volatile("" : "+v"(qo));
+        }
+        if (QJL) {
+            // signs . (G q as fp16 hi + fp16 remainder), then + norm * that
+            // (norm of token 4g + i: a quad broadcast, fp32); the B images
+            // are read from the stage area (the opaque offset keeps the
+            // reads in the loop), each once for both 16-token halves
+            uint32_t qo = qimg_off;
+            asm volatile("" : "+v"(qo));
+            float4_t qacc[NCB][2];
 #pragma unroll
-                for (int s = 0; s < 2; ++s) {
-                    const half8_t s8 = sign_halves(smem, s ? R.sg[u].y : R.sg[u].x, 8u * g, slane);
+            for (int c = 0; c < NCB; ++c) qacc[c][0] = qacc[c][1] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                    for (int c = 0; c < NCB; ++c) {
-                        const uint4 vq = *reinterpret_cast<const uint4 *>(smem + qo + ((c * 2 + s) * 2) * 1024);
-                        const uint4 vl = *reinterpret_cast<const uint4 *>(smem + qo + ((c * 2 + s) * 2 + 1) * 1024);
-                        qacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(s8, __builtin_bit_cast(half8_t, vq), qacc[c], 0, 0, 0);
-                        qacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(s8, __builtin_bit_cast(half8_t, vl), qacc[c], 0, 0, 0);
+            for (int s = 0; s < 2; ++s) {
+                half8_t s8[2];
+#pragma unroll
+                for (int u = 0; u < 2; ++u) s8[u] = sign_halves(smem, s ? R.sg[u].y : R.sg[u].x, 8u * g, slane);
+#pragma unroll
+                for (int c = 0; c < NCB; ++c) {
+                    const half8_t vq = __builtin_bit_cast(half8_t, *reinterpret_cast<const uint4 *>(smem + qo + ((c * 2 + s) * 2) * 1024));
+                    const half8_t vl = __builtin_bit_cast(half8_t, *reinterpret_cast<const uint4 *>(smem + qo + ((c * 2 + s) * 2 + 1) * 1024));
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        qacc[c][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(s8[u], vq, qacc[c][u], 0, 0, 0);
+                        qacc[c][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(s8[u], vl, qacc[c][u], 0, 0, 0);
                     }
                 }
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const float nri = dpp_quad_bcast(R.nr[u], i);
 #pragma unroll
-                    for (int c = 0; c < NCB; ++c) acc[c][u][i] = __builtin_fmaf(nri, qacc[c][i], acc[c][u][i]);
+                    for (int c = 0; c < NCB; ++c) acc[c][u][i] = __builtin_fmaf(nri, qacc[c][u][i], acc[c][u][i]);
                 }
-            }
         }
         // raw scores of both column blocks first (the row scale qsr >= 0
         // enters each exponent's fma); one rescale branch for both, then the
