@@ -141,6 +141,29 @@ def test_paged_lora_and_rotation_equal_contiguous(device):
     assert torch.equal(got, ref), f"paged LoRA differs by {(got - ref).abs().max().item():.3e}"
 
 
+def test_prepared_paged_lora_equals_direct_call(device):
+    """PagedKVAttention with a LoRA bank (its prepared native plan) equals
+    paged_attention (one omni_attn_paged call with every argument) bit for
+    bit on the serving step: rank-8 adapters, rotation with a sign flip."""
+    from omnistack_rs.cache import PagedKVAttention, paged_attention
+    B, Hq, Hkv, T, S, uid, L, R, HID = 8, 32, 8, 1, 50, 2, 16, 8, 128
+    kn, kq, kr, vn, cb = _cache(B, Hkv, S, seed=345, user_id=uid)
+    q = _data.query((B, Hq, T, 128), seed=346).to(device)
+    la, lb = (t.to(torch.bfloat16).to(device) for t in _data.lora_bank(L, R, HID, Hq * 128))
+    ids = _data.lora_ids(B, L).to(device)
+    xh = _data.query((B, T, HID), seed=347).to(device)
+    s = _data.sign_flip(128).to(device)
+    cache, pt, lt = _paged(device, kn, kq, kr, vn, 16, seed=18)
+    att = PagedKVAttention(cache, cb.to(device), n_heads=Hq, batch=B, max_pages=pt.shape[1], user_id=uid,
+                           rotate_q=True, sign_flip=s, lora_a=la, lora_b=lb, lora_alpha=0.5)
+    got = att.run(q, pt, lt, xh, ids).clone()
+    want = paged_attention(q, cache, pt, lt, cb.to(device), user_id=uid, rotate_q=True, sign_flip=s, x=xh,
+                           lora_a=la, lora_b=lb, lora_indices=ids, lora_alpha=0.5)
+    assert torch.equal(got, want), f"prepared paged LoRA differs by {(got - want).abs().max().item():.3e}"
+    with pytest.raises(ValueError):
+        att.run(q, pt, lt)                 # a bank needs x and the indices
+
+
 def test_paged_bad_pages_and_empty_sequences(device):
     """Without host validation a page id outside the pool or a length past
     the table gives NaN rows for that sequence only, and an empty sequence
