@@ -1072,11 +1072,28 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     const int tps = (s_end - s_begin + kDecTile - 1) / kDecTile;
     const int tps1 = (s_end1 - s_begin + kDecTile - 1) / kDecTile;
     const int ntiles = tps + (nseq > 1 ? tps1 : 0);
-    DecOffsets OFS;
-    OFS.k = (uint32_t)n * 64u + 16u * g;
-    OFS.sg = (uint32_t)n * 8u;
-    OFS.nr = 16u * g + 4u * (n & 3);      // norm of token 4g + n % 4 (of each 16-token half)
-    OFS.v = 256u * g + 4u * n;
+    auto make_ofs = [](int l) {
+        const int nn = l & 15, gg = l >> 4;
+        DecOffsets o;
+        o.k = (uint32_t)nn * 64u + 16u * gg;
+        o.sg = (uint32_t)nn * 8u;
+        o.nr = 16u * gg + 4u * (nn & 3);      // norm of token 4g + n % 4 (of each 16-token half)
+        o.v = 256u * gg + 4u * nn;
+        return o;
+    };
+    const DecOffsets OFS = make_ofs(lane);
+    // loop-time offsets: with the fused LoRA prologue or two sequences per
+    // block (whose registers run short) they are recomputed from an opaque
+    // lane id at each use instead of being kept live across the loop
+    auto ofs_loop = [&]() {
+        if constexpr (LORA || SPB > 1) {
+            int l = lane;
+            asm volatile("" : "+v"(l));
+            return make_ofs(l);
+        } else {
+            return OFS;
+        }
+    };
 
     // Paged cache: pool rows of a tile's two halves; a page id outside the
     // pool marks this wave's state bad (the sequence's rows come out NaN)
@@ -1602,7 +1619,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
                 uint32_t rb[2];
                 rows_resolve(q, rb);
                 __builtin_amdgcn_sched_barrier(0);
-                tile_load_paged<QJL>(ring[0], P, OFS, rb);
+                tile_load_paged<QJL>(ring[0], P, ofs_loop(), rb);
                 __builtin_amdgcn_sched_barrier(0);
             });
             for (;;) {
@@ -1614,7 +1631,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
                     uint32_t rb[2];
                     rows_resolve(q, rb);
                     __builtin_amdgcn_sched_barrier(0);
-                    tile_load_paged<QJL>(ring[1], P, OFS, rb);
+                    tile_load_paged<QJL>(ring[1], P, ofs_loop(), rb);
                     __builtin_amdgcn_sched_barrier(0);
                 });
                 if (i_nxt >= ntiles) break;
@@ -1625,7 +1642,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
                     uint32_t rb[2];
                     rows_resolve(q, rb);
                     __builtin_amdgcn_sched_barrier(0);
-                    tile_load_paged<QJL>(ring[0], P, OFS, rb);
+                    tile_load_paged<QJL>(ring[0], P, ofs_loop(), rb);
                     __builtin_amdgcn_sched_barrier(0);
                 });
             }
@@ -1633,7 +1650,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
             i_cur = claim_value(c_raw);
             c_raw = claim_issue(tile_cnt, lane);
             __builtin_amdgcn_sched_barrier(0);
-            tile_load<QJL>(ring[0], tile_seq(i_cur) ? P1 : P, OFS, tile_tok(i_cur));
+            tile_load<QJL>(ring[0], tile_seq(i_cur) ? P1 : P, ofs_loop(), tile_tok(i_cur));
             __builtin_amdgcn_sched_barrier(0);
             tile_step(ring[1], tile_tok(i_pre), tile_seq(i_pre), [] {});
             for (;;) {
@@ -1641,14 +1658,14 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
                 const int i_nxt = claim_value(c_raw);
                 c_raw = claim_issue(tile_cnt, lane);
                 __builtin_amdgcn_sched_barrier(0);
-                tile_load<QJL>(ring[1], tile_seq(i_nxt) ? P1 : P, OFS, tile_tok(i_nxt));
+                tile_load<QJL>(ring[1], tile_seq(i_nxt) ? P1 : P, ofs_loop(), tile_tok(i_nxt));
                 __builtin_amdgcn_sched_barrier(0);
                 tile_step(ring[0], tile_tok(i_cur), tile_seq(i_cur), [] {});
                 if (i_nxt >= ntiles) break;
                 i_cur = claim_value(c_raw);
                 c_raw = claim_issue(tile_cnt, lane);
                 __builtin_amdgcn_sched_barrier(0);
-                tile_load<QJL>(ring[0], tile_seq(i_cur) ? P1 : P, OFS, tile_tok(i_cur));
+                tile_load<QJL>(ring[0], tile_seq(i_cur) ? P1 : P, ofs_loop(), tile_tok(i_cur));
                 __builtin_amdgcn_sched_barrier(0);
                 tile_step(ring[1], tile_tok(i_nxt), tile_seq(i_nxt), [] {});
             }
