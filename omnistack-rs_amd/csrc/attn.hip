@@ -1041,10 +1041,25 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     }
     const int s_end = imax(s_begin, (int)imin64(seq_len, (int64_t)s_begin + a.split_len));
     const int s_end1 = imax(s_begin, (int)imin64(seq_len1, (int64_t)s_begin + a.split_len));
-    auto stream_bufs = [&](int64_t bb) {
+    // cache sequences of the block's batch entries: with a pool index both
+    // indices are requested before either is used (one round trip), and
+    // their out-of-pool flags are kept for the epilogue
+    int64_t cs0 = b, cs1 = -1;            // cs1 < 0: no pool (the batch entry itself)
+    bool cs_bad0 = false, cs_bad1 = false;
+    if (!PAGED && a.seq_index != nullptr) {
+        const int64_t v0 = a.seq_index[b], v1 = a.seq_index[nseq > 1 ? b + 1 : b];
+        auto norm = [&](int64_t v, bool &bad) {
+            v = v < 0 ? v + a.n_seqs : v;
+            bad = v < 0 || v >= a.n_seqs;
+            return bad ? (int64_t)0 : v;
+        };
+        cs0 = norm(v0, cs_bad0);
+        cs1 = norm(v1, cs_bad1);
+    }
+    auto stream_bufs = [&](int64_t cs) {
         if constexpr (PAGED) {
             // the whole pool (its row count times 64 fits 32 bits: the host checks)
-            (void)bb;
+            (void)cs;
             const uint32_t rows = (uint32_t)(a.n_pages * a.Hkv * a.page_size);
             DecBufs Q;
             Q.kn = __builtin_amdgcn_make_buffer_rsrc((void *)a.k_nib, (short)0, rows * 64u, kBufWord3);
@@ -1055,8 +1070,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
                                                      QJL ? rows * 4u : 0u, kBufWord3);
             return Q;
         }
-        bool bad_unused;
-        const int64_t kv_base = (cache_seq(a, bb, bad_unused) * a.Hkv + hk) * a.S;
+        const int64_t kv_base = (cs * a.Hkv + hk) * a.S;
         DecBufs Q;
         Q.kn = __builtin_amdgcn_make_buffer_rsrc((void *)(a.k_nib + kv_base * 64), (short)0, s_end * 64, kBufWord3);
         Q.vn = __builtin_amdgcn_make_buffer_rsrc((void *)(a.v_nib + kv_base * 64), (short)0, s_end * 64, kBufWord3);
@@ -1066,8 +1080,8 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
                                                  (short)0, QJL ? s_end * 4 : 0, kBufWord3);
         return Q;
     };
-    const DecBufs P = stream_bufs(b);
-    const DecBufs P1 = stream_bufs(nseq > 1 ? b + 1 : b);
+    const DecBufs P = stream_bufs(cs0);
+    const DecBufs P1 = stream_bufs(cs1 >= 0 ? cs1 : (nseq > 1 ? b + 1 : b));
     // tiles of the split per sequence; claim index i -> sequence (i >= tps)
     const int tps = (s_end - s_begin + kDecTile - 1) / kDecTile;
     const int tps1 = (s_end1 - s_begin + kDecTile - 1) / kDecTile;
@@ -1725,11 +1739,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
         float rmx, lsum, osum;
         if (nw_act == nw) merge(std::integral_constant<int, nw>{}, rr, d, rmx, lsum, osum);
         else merge(nw_act, rr, d, rmx, lsum, osum);
-        if (a.seq_index != nullptr) {
-            bool bad;
-            (void)cache_seq(a, rr_b, bad);
-            if (bad) lsum = __builtin_nanf("");
-        }
+        if (row_seq(rr) ? cs_bad1 : cs_bad0) lsum = __builtin_nanf("");
         if (row_seq(rr) ? len_bad1 : len_bad) lsum = __builtin_nanf("");
         if (a.splits == 1) {
             const int t = div_small(rr_rho, a.g_magic);
