@@ -1545,7 +1545,10 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
 #pragma unroll
             for (int k = 0; k < 8; ++k) oacc[k] *= f;
             lacc_sum *= f;
-            m_run = need ? mt : m_run;
+            // in place (one register for the running maximum on both paths:
+            // no copy where no lane rescales)
+            const uint64_t nmask = __builtin_amdgcn_ballot_w64(need);
+            asm volatile("v_cndmask_b32 %0, %0, %1, %2" : "+v"(m_run) : "v"(mt), "s"(nmask));
             round_first = round_first ||
                           __builtin_amdgcn_ballot_w64(fabsf(m_run) >= 8192.0f && m_run > -__FLT_MAX__ && m_run < __FLT_MAX__);
         }
@@ -1558,13 +1561,14 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
         float ex[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) ex[k] = lo_col ? sc[4 + k] : sc[k];
+        // the two modes as separate code (no select of the multiplier)
         if (round_first) {
 #pragma unroll
-            for (int k = 0; k < 4; ++k) ex[k] = ex[k] * csc;
-        }
-        const float cm = round_first ? 1.0f : csc;
+            for (int k = 0; k < 4; ++k) ex[k] = ex[k] * csc + nm;
+        } else {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) ex[k] = __builtin_fmaf(ex[k], cm, nm);
+            for (int k = 0; k < 4; ++k) ex[k] = __builtin_fmaf(ex[k], csc, nm);
+        }
         const uint32_t my01 = cvt_pk_h2(__builtin_amdgcn_exp2f(ex[0]), __builtin_amdgcn_exp2f(ex[1]));
         const uint32_t my23 = cvt_pk_h2(__builtin_amdgcn_exp2f(ex[2]), __builtin_amdgcn_exp2f(ex[3]));
         const uint32_t ot01 = dpp_row_ror8(my01), ot23 = dpp_row_ror8(my23);
