@@ -2081,6 +2081,11 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
     auto tile_step = [&](TileRaw &R, const int tt) {
         // wave-uniform flags as ints (scalar compares, no lane masks)
         const int full = __builtin_amdgcn_readfirstlane(tt + kDecTile <= full_end ? 1 : 0);
+        // wave priority by phase: the K pass 2, the QJL term and the raw
+        // maxima 1, the softmax and PV 0, so that of a SIMD's two waves the
+        // one feeding the matrix cores issues first and the other's softmax
+        // fills the gaps (issue order only: results do not depend on it)
+        __builtin_amdgcn_s_setprio(2);
         float4_t acc[NCB][2];
 #pragma unroll
         for (int c = 0; c < NCB; ++c)
@@ -2101,6 +2106,7 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
                 }
             }
         }
+        __builtin_amdgcn_s_setprio(1);
         if (QJL) {
             // signs . (G q as fp16 hi + fp16 remainder), then + norm * that
             // (norm of token 4g + i: a quad broadcast, fp32); the B images
@@ -2175,6 +2181,7 @@ __global__ __launch_bounds__(64 * kPreWaves) void attn_prefill128_kernel(AttnArg
             mr[c] = vmax3(vmax3(sc[c][0], sc[c][1], sc[c][2]), vmax3(sc[c][3], sc[c][4], sc[c][5]), vmax2(sc[c][6], sc[c][7]));
             may = may || mr[c] > m_thr[c];
         }
+        __builtin_amdgcn_s_setprio(0);
         if (__builtin_amdgcn_ballot_w64(may)) {
 #pragma unroll
             for (int c = 0; c < NCB; ++c) {
@@ -2587,6 +2594,10 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
     auto tile_step = [&](TileRaw32 &R, const int tt) {
         // wave-uniform as an int (a scalar compare per use, no lane mask)
         const int full = __builtin_amdgcn_readfirstlane(tt + kDecTile <= full_end ? 1 : 0);
+        // wave priority by phase: the K pass and QJL term 2, the PV operand
+        // reads and the raw maxima 1, the softmax and PV 0 (as in the
+        // head_dim-128 kernel)
+        __builtin_amdgcn_s_setprio(2);
         float4_t acc[NCB][2];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
@@ -2620,6 +2631,7 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
         // half at dims 2n (low nibbles) and 2n + 1 (high nibbles); a LUT
         // entry is (fp16 hi pair, remainder pair), read as two dwords so the
         // hi and remainder planes are two A operands over the same P
+        __builtin_amdgcn_s_setprio(1);
         uint32_t ph[2][4], pl[2][4];      // [dim parity][pair byte]
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
@@ -2684,6 +2696,7 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
             mr[c] = vmax3(vmax3(sc[c][0], sc[c][1], sc[c][2]), vmax3(sc[c][3], sc[c][4], sc[c][5]), vmax2(sc[c][6], sc[c][7]));
             may = may || mr[c] > m_thr[c];
         }
+        __builtin_amdgcn_s_setprio(0);
         if (__builtin_amdgcn_ballot_w64(may)) {
 #pragma unroll
             for (int c = 0; c < NCB; ++c) {
