@@ -1485,6 +1485,9 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
     // One 32-token tile: scores, online softmax, PV.
     auto tile_step = [&](TileRaw &R, const int tt, const int tseq, auto &&after_k) {
         const bool full = tt + kDecTile <= full_end;
+        // wave priority by phase: the K pass 2, masks and maxima 1, the
+        // softmax and PV 0 (issue order only: results do not depend on it)
+        __builtin_amdgcn_s_setprio(2);
 
         // scores: lane (n, g) holds tokens tt + 16u + 4g + i
         float sc[8];
@@ -1517,6 +1520,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
                 sc[4 * u + i] = v + __uint_as_float(dpp_row_ror8(__float_as_uint(v)));
             }
         }
+        __builtin_amdgcn_s_setprio(1);
         after_k();
         if (!full) {
 #pragma unroll
@@ -1538,6 +1542,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode128_kernel(AttnArgs
         // only when some lane rescales.
         const float mr = vmax3(vmax3(sc[0], sc[1], sc[2]), vmax3(sc[3], sc[4], sc[5]), vmax2(sc[6], sc[7]));
         float mt = mr * csc;
+        __builtin_amdgcn_s_setprio(0);
         if (__builtin_amdgcn_ballot_w64(mt > m_run + 8.0f)) {
             mt = max_over_groups(mt);
             const bool need = mt > m_run + 8.0f;
