@@ -506,6 +506,10 @@ __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
     // mrow (virtual row v0 + n).
     auto encode_group = [&](const uint4 (&w4)[4], const int64_t mrow, const int64_t v0) {
         const bool store = v0 + n < v_end && g == 0 && (!PAGED || mrow >= 0);
+        // wave priority by phase: the rotation and the projection MFMAs 1,
+        // the rest 0, so that of a SIMD's three waves the ones in those
+        // phases issue first (issue order only: results do not depend on it)
+        __builtin_amdgcn_s_setprio(1);
 
         // flip signs on the raw words (8 x 16-bit per chunk), widen
         float x[4][8];
@@ -561,6 +565,7 @@ __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
                         }
                     }
         }
+        __builtin_amdgcn_s_setprio(0);
         // value bits of each element ((scaled and) rounded to the input dtype)
         uint32_t vb[4][8];
 #pragma unroll
@@ -649,6 +654,7 @@ __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
         // fp32 sum `as` is within a relative 127 * 2^-24 of sum|e|:
         // 1312 * 2^-24 * as bounds the total.  Rows with sum|e| >= 2^127
         // (where a part could round to infinity) take the exact path below.
+        __builtin_amdgcn_s_setprio(1);
         float4_t acc[4];
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb) acc[cb] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -677,6 +683,7 @@ __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
             }
         }
 
+        __builtin_amdgcn_s_setprio(0);
         // signs: lane (n, g) holds P[n][16 cb + 4 g + i]; cb's four bits go
         // to bits 16 (cb & 1) + 4 g .. + 3 of word cb / 2
         const bool finite_row = as < 0x1p127f;                 // false for inf / NaN
