@@ -49,7 +49,7 @@ BYTES_PER_TOKEN_HEAD = 64 + 8 + 4 + 64     # K nibbles + K signs + K norm (f32) 
 # (FETCH_SIZE reads half the copied bytes -> x2.0; WRITE_SIZE reads them
 # exactly -> x1.0).  Recorded in profiles/bench_driver_c3.md; re-measure
 # after any change to the decode kernel.
-C3_TRAFFIC = {"fetch_kib": 143660.0, "fetch_scale": 2.0, "write_kib": 512.0, "write_scale": 1.0}
+C3_TRAFFIC = {"fetch_kib": 143665.8, "fetch_scale": 2.0, "write_kib": 512.0, "write_scale": 1.0}
 
 
 def log(msg: str) -> None:
