@@ -506,7 +506,7 @@ __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
     // mrow (virtual row v0 + n).
     auto encode_group = [&](const uint4 (&w4)[4], const int64_t mrow, const int64_t v0) {
         const bool store = v0 + n < v_end && g == 0 && (!PAGED || mrow >= 0);
-        // wave priority by phase: the rotation and the projection MFMAs 1,
+        // wave priority by phase: the projection MFMAs 2, the rotation 1,
         // the rest 0, so that of a SIMD's three waves the ones in those
         // phases issue first (issue order only: results do not depend on it)
         __builtin_amdgcn_s_setprio(1);
@@ -654,7 +654,7 @@ __global__ __launch_bounds__(64 * kEncWaves) void encode128_kernel(EncArgs a) {
         // fp32 sum `as` is within a relative 127 * 2^-24 of sum|e|:
         // 1312 * 2^-24 * as bounds the total.  Rows with sum|e| >= 2^127
         // (where a part could round to infinity) take the exact path below.
-        __builtin_amdgcn_s_setprio(1);
+        __builtin_amdgcn_s_setprio(2);
         float4_t acc[4];
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb) acc[cb] = float4_t{0.f, 0.f, 0.f, 0.f};
