@@ -2641,8 +2641,9 @@ __global__ __launch_bounds__(64 * kP32Waves) void attn_prefill32_kernel(AttnArgs
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const uint32_t b0 = R.v[4 * u], b1 = R.v[4 * u + 1], b2 = R.v[4 * u + 2], b3 = R.v[4 * u + 3];
-            const uint32_t pe[2] = {__builtin_amdgcn_ubfe(b0, 0, 4) | ((b1 & 0x0Fu) << 4),
-                                    __builtin_amdgcn_ubfe(b2, 0, 4) | ((b3 & 0x0Fu) << 4)};
+            // (only byte 0 of pe reaches the LUT address: the bits above it
+            // may hold b1's high nibble, so one bit-field insert forms it)
+            const uint32_t pe[2] = {(b0 & 0x0Fu) | ((b1 << 4) & ~0x0Fu), (b2 & 0x0Fu) | ((b3 << 4) & ~0x0Fu)};
             const uint32_t po[2] = {(b0 >> 4) | (b1 & 0xF0u), (b2 >> 4) | (b3 & 0xF0u)};
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
